@@ -1,0 +1,144 @@
+/*
+ * librpa -- ragged paged attention (RPA) for AMD Instinct MI355X (gfx950).
+ *
+ * C ABI: plain pointers and sizes, no C++ or torch types.  All tensor
+ * pointers are DEVICE pointers owned by the caller; the library never
+ * allocates or frees on the call path.  Every entry point returns 0 on
+ * success or a negative RPA_E* code; rpa_last_error() then describes it
+ * (thread-local string).
+ *
+ * Tensor layouts are the reference operator's
+ * (ecosystem/source/jax/ragged_paged_attention.py:718-750):
+ *   q            bf16  [num_tokens, num_q_heads, head_dim]
+ *   kv_pages     bf16 | fp8-e4m3 (OCP E4M3FN)  [total_pages, page_size, 2*num_kv_heads, head_dim]
+ *                K of kv head h is combined head 2h, V is 2h+1 (:116-121, :361-393)
+ *   kv_lens      int32 [max_num_seqs]
+ *   page_indices int32 [max_num_seqs, pages_per_seq] (row-major)
+ *   cu_q_lens    int32 [max_num_seqs + 1]
+ *   num_seqs     int32 [1]
+ *   out          bf16  [num_tokens, num_q_heads, head_dim]
+ */
+#ifndef RPA_H_
+#define RPA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RPA_ABI_VERSION 1
+
+enum {
+  RPA_OK = 0,
+  RPA_E_INVALID = -1,    /* bad shape / option / pointer */
+  RPA_E_UNSUPPORTED = -2,/* valid for the reference but not built here (e.g. head_dim) */
+  RPA_E_WORKSPACE = -3,  /* workspace missing or too small */
+  RPA_E_HIP = -4         /* a HIP runtime call failed */
+};
+
+enum { RPA_KV_BF16 = 0, RPA_KV_FP8_E4M3 = 1 };
+
+/* Static description of one call (shapes are the reference's, :73-80). */
+typedef struct rpa_shape {
+  int32_t num_tokens;    /* T = q.shape[0] (max_num_batched_tokens) */
+  int32_t num_q_heads;   /* Hq */
+  int32_t num_kv_heads;  /* Hkv; kv_pages.shape[2] == 2*Hkv */
+  int32_t head_dim;      /* D; 128 is built */
+  int32_t total_pages;   /* P = kv_pages.shape[0] */
+  int32_t page_size;     /* S = kv_pages.shape[1] */
+  int32_t max_num_seqs;  /* N_max = page_indices.shape[0] */
+  int32_t pages_per_seq; /* PPS = page_indices.shape[1] */
+  int32_t kv_dtype;      /* RPA_KV_BF16 | RPA_KV_FP8_E4M3 */
+} rpa_shape_t;
+
+/* Scalar knobs of the reference signature (:718-731).  Zero-initialise and
+ * set what is used: sliding_window 0 = none, soft_cap 0 = none,
+ * has_mask_value 0 = DEFAULT_MASK_VALUE (-0.7 * FLT_MAX, :32),
+ * has_k_scale / has_v_scale 0 = no scalar K/V scale. */
+typedef struct rpa_options {
+  float sm_scale;
+  int32_t sliding_window;
+  float soft_cap;
+  int32_t has_mask_value;
+  float mask_value;
+  int32_t has_k_scale;
+  float k_scale;
+  int32_t has_v_scale;
+  float v_scale;
+} rpa_options_t;
+
+/* ABI version of the loaded library (RPA_ABI_VERSION). */
+int rpa_abi_version(void);
+
+/* Message for the last nonzero return on this thread ("" if none). */
+const char* rpa_last_error(void);
+
+/* Bytes of device workspace rpa_ragged_paged_attention needs for this shape
+ * on the CURRENT device (split-K partials, error word).  0 on error.
+ * Replaces the scratch the reference's pallas_call allocates itself
+ * (ragged_paged_attention.py:837-863). */
+size_t rpa_workspace_size(const rpa_shape_t* shape);
+
+/* One-time initialisation of a freshly allocated workspace (zeroes the error
+ * word), stream-ordered.  Call once per workspace buffer. */
+int rpa_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* Ragged paged attention forward.  Replaces
+ *   ragged_paged_attention(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *,
+ *       sm_scale, sliding_window, soft_cap, mask_value, k_scale, v_scale, ...)
+ *   ecosystem/source/jax/ragged_paged_attention.py:718-899
+ * with the semantics of its oracle ref_ragged_paged_attention (:73-148):
+ * causal (query j of a sequence sits at kv position kv_len - q_len + j),
+ * GQA kv_head = q_head / (Hq / Hkv), fp32 softmax and accumulation.
+ *
+ * kv_scales: NULL, or fp32 [total_pages, num_kv_heads, 2] per-(page, kv head)
+ *   K and V dequantisation scales (an extension of the reference's scalar
+ *   k_scale / v_scale, :124-129); dequantised K = bf16(float(k) * scale).
+ * Rows of `out` at or past cu_q_lens[num_seqs] are written as zeros.
+ * Stream-ordered and asynchronous; no host synchronisation inside.
+ * Metadata is range-checked on the device: an out-of-range page id or query
+ * row is never dereferenced, the affected rows are left unwritten, and a
+ * nonzero error word is recorded (rpa_read_error_word). */
+int rpa_ragged_paged_attention(const rpa_shape_t* shape, const rpa_options_t* options,
+                               const void* q, const void* kv_pages, const float* kv_scales,
+                               const int32_t* kv_lens, const int32_t* page_indices,
+                               const int32_t* cu_q_lens, const int32_t* num_seqs,
+                               void* out, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* Measurement hook: rpa_ragged_paged_attention, additionally recording the
+ * caller's hipEvent_t event_begin / event_end on `stream` immediately before
+ * and after the attention kernel (not the split-K combine), so a caller can
+ * time the dominant kernel alone.  No counterpart in the reference (its runner
+ * reads per-kernel device time from XProf, src/tpu_cake/rpa_bundle.py:114-139). */
+int rpa_ragged_paged_attention_timed(const rpa_shape_t* shape, const rpa_options_t* options,
+                                     const void* q, const void* kv_pages, const float* kv_scales,
+                                     const int32_t* kv_lens, const int32_t* page_indices,
+                                     const int32_t* cu_q_lens, const int32_t* num_seqs, void* out,
+                                     void* workspace, size_t workspace_bytes, void* stream,
+                                     void* event_begin, void* event_end);
+
+/* Gather probe: copies every (sequence, token < kv_len) K/V row the attention
+ * kernel reads, in logical order, into dense [sum(kv_lens), 2*Hkv, head_dim]
+ * (same element type as kv_pages).  Uses the attention kernel's page-address
+ * function; restates the gather of MultiPageAsyncCopyDescriptor
+ * (ragged_paged_attention.py:35-70).  Row offsets are the exclusive prefix
+ * sum of kv_lens over the first num_seqs sequences. */
+int rpa_gather_kv(const rpa_shape_t* shape, const void* kv_pages, const int32_t* kv_lens,
+                  const int32_t* page_indices, const int32_t* num_seqs, void* dense_out,
+                  int64_t dense_rows, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Copies the workspace error word to *host_word (synchronous on `stream`).
+ * Bit 0: page id out of [0, total_pages); bit 1: query row out of
+ * [0, num_tokens); bit 2: kv_len clamped to pages_per_seq * page_size;
+ * bit 3: a sequence with q_len > kv_len (its uncovered rows are left unwritten). */
+int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* host_word,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RPA_H_ */

@@ -1,0 +1,85 @@
+// Work decomposition shared by the device kernels and the host-side checker.
+//
+// A call's work is linearised into UNITS.  One unit is KV_CHUNK consecutive
+// keys of one (sequence i, kv head h, row block rb):
+//   * a row block is ROW_BLOCK consecutive query rows of sequence i, where
+//     query row r <-> (query token r / G, query head h*G + r % G), G = Hq/Hkv
+//     (the GQA mapping of ragged_paged_attention.py:130-131);
+//   * a row block only visits keys up to the causal limit of its last row,
+//     kv_len - q_len + last_token (ragged_paged_attention.py:134-138), so
+//     fully masked chunks are never loaded -- exact when the mask value makes
+//     masked weights vanish in fp32 (skip_masked); with a finite mask value
+//     the reference gives masked keys weight exp(s + mask - m), so every key
+//     below kv_len is visited instead.
+// Units are ordered sequence-major, then kv head, then row block, then chunk.
+// Workgroup b of a grid of `grid` owns units [start(b), start(b+1)) with
+// start(b) = floor(b * W / grid): every workgroup gets the same number of
+// KV chunks (+-1) whatever the length distribution ("stream-K").
+//
+// Everything here is plain integer arithmetic usable on host and device.
+#ifndef RPA_SCHEDULE_H_
+#define RPA_SCHEDULE_H_
+
+#include <stdint.h>
+
+#ifndef RPA_HD
+#if defined(__HIPCC__)
+#define RPA_HD __host__ __device__ __forceinline__
+#else
+#define RPA_HD inline
+#endif
+#endif
+
+namespace rpa {
+
+constexpr int KV_CHUNK = 32;   // keys per unit (the K extent of one PV MFMA)
+constexpr int ROW_BLOCK = 16;  // query rows per row block (the N extent of the MFMAs)
+
+// Keys visible to row block rb (causal limit of its last valid row), or 0.
+RPA_HD int rb_visible_keys(int kv_len, int q_len, int group, int rb, bool skip_masked) {
+  if (!skip_masked) return kv_len;
+  int last_row_tok = (rb * ROW_BLOCK + ROW_BLOCK - 1) / group;
+  int last_tok = q_len - 1 < last_row_tok ? q_len - 1 : last_row_tok;
+  int vis = kv_len - q_len + last_tok + 1;
+  return vis < kv_len ? vis : kv_len;
+}
+
+RPA_HD int rb_units(int kv_len, int q_len, int group, int rb, bool skip_masked) {
+  int vis = rb_visible_keys(kv_len, q_len, group, rb, skip_masked);
+  return vis > 0 ? (vis + KV_CHUNK - 1) / KV_CHUNK : 0;
+}
+
+RPA_HD int num_row_blocks(int q_len, int group) {
+  return q_len > 0 ? (q_len * group + ROW_BLOCK - 1) / ROW_BLOCK : 0;
+}
+
+// Units of one kv head of a sequence (sum over its row blocks).
+RPA_HD int seq_units_per_head(int kv_len, int q_len, int group, bool skip_masked) {
+  if (q_len <= 0 || kv_len <= 0) return 0;
+  int nrb = num_row_blocks(q_len, group);
+  int u = 0;
+  for (int rb = 0; rb < nrb; ++rb) u += rb_units(kv_len, q_len, group, rb, skip_masked);
+  return u;
+}
+
+// First unit of workgroup b.
+RPA_HD int64_t range_start(int64_t b, int64_t total, int64_t grid) {
+  return b * total / grid;
+}
+
+// The workgroup whose range holds unit u (largest b with range_start(b) <= u).
+RPA_HD int64_t owner_of(int64_t u, int64_t total, int64_t grid) {
+  return ((u + 1) * grid - 1) / total;
+}
+
+// Split-K partial slots: each workgroup writes at most two partial segments,
+// slot 2b for the segment its range starts inside of (the triple began in an
+// earlier workgroup), slot 2b+1 for the segment that begins in b and runs past
+// its range end.
+RPA_HD int64_t partial_slot(int64_t b, bool started_here) {
+  return 2 * b + (started_here ? 1 : 0);
+}
+
+}  // namespace rpa
+
+#endif  // RPA_SCHEDULE_H_

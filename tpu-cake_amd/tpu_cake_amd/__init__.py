@@ -1,0 +1,24 @@
+"""tpu_cake_amd: ragged paged attention (RPA) for AMD Instinct MI355X.
+
+The hot path of sdrshn-nmbr/tpu-cake's Inkling RPA workload, rebuilt as
+hand-written gfx950 HIP kernels (``librpa.so``, C ABI in ``include/rpa.h``)
+behind the reference operator's Python surface (``tpu_cake_amd.ops``).
+"""
+
+from .ops import (  # noqa: F401
+    DEFAULT_MASK_VALUE,
+    dynamic_validate_inputs,
+    gather_kv,
+    ragged_paged_attention,
+    read_error_word,
+    static_validate_inputs,
+)
+
+__all__ = [
+    "DEFAULT_MASK_VALUE",
+    "dynamic_validate_inputs",
+    "gather_kv",
+    "ragged_paged_attention",
+    "read_error_word",
+    "static_validate_inputs",
+]

@@ -1,0 +1,284 @@
+"""The RPA operator on MI355X: the reference's Python surface over ``librpa.so``.
+
+``ragged_paged_attention`` keeps the signature and error behaviour of the
+upstream JAX operator (``ecosystem/source/jax/ragged_paged_attention.py:718-899``):
+the same positional tensors, the same keyword knobs, ``ValueError`` with the
+reference's messages from ``static_validate_inputs`` (:216-287) before any
+launch, and a fresh output shaped like ``q``.  Tensors are torch tensors on the
+GPU (torch is only the allocator); the work is two HIP kernels launched through
+the C ABI on torch's current stream.  The Pallas block-size knobs
+(``num_kv_pages_per_block``, ``num_queries_per_block``, ``vmem_limit_bytes``)
+are validated like upstream and otherwise ignored: the HIP schedule balances
+work itself.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+DEFAULT_MASK_VALUE = -0.7 * float(torch.finfo(torch.float32).max)  # ragged_paged_attention.py:32
+
+_KV_DTYPES = {torch.bfloat16: _lib.RPA_KV_BF16, torch.float8_e4m3fn: _lib.RPA_KV_FP8_E4M3,
+              torch.uint8: _lib.RPA_KV_FP8_E4M3}
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _require_cuda(name: str, t: torch.Tensor) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a GPU device, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def static_validate_inputs(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *,
+                           sm_scale=None, sliding_window=None, soft_cap=None, mask_value=None,
+                           k_scale=None, v_scale=None, num_kv_pages_per_block=None,
+                           num_queries_per_block=None, vmem_limit_bytes=None) -> None:
+    """Shape/dtype checks of ``static_validate_inputs`` (ragged_paged_attention.py:216-287)."""
+    _, num_q_heads, head_dim = q.shape
+    _, _, num_combined_kv_heads, head_dim_k = kv_pages.shape
+    if num_combined_kv_heads % 2:
+        raise ValueError(f"num_combined_kv_heads={num_combined_kv_heads} must be even")
+    if not (isinstance(k_scale, float) or k_scale is None):
+        raise ValueError(f"k_scale={k_scale!r} must be a float or None")
+    if not (isinstance(v_scale, float) or v_scale is None):
+        raise ValueError(f"v_scale={v_scale!r} must be a float or None")
+    num_kv_heads = num_combined_kv_heads // 2
+    max_num_seqs, pages_per_seq = page_indices.shape
+    if tuple(num_seqs.shape) != (1,):
+        raise ValueError(f"num_seqs.shape={tuple(num_seqs.shape)} must be (1,)")
+    if head_dim_k != head_dim:
+        raise ValueError(f"Q head_dim {head_dim} must be the same as that of K/V {head_dim_k}.")
+    if tuple(kv_lens.shape) != (max_num_seqs,):
+        raise ValueError(
+            f"Expected kv_lens.shape={tuple(kv_lens.shape)} to be ({max_num_seqs},) where"
+            " `max_num_seqs` is `page_indices.shape[0]`.")
+    if tuple(cu_q_lens.shape) != (max_num_seqs + 1,):
+        raise ValueError(
+            f"Expected cu_q_lens.shape={tuple(cu_q_lens.shape)} to be ({max_num_seqs + 1},)  where"
+            " `max_num_seqs` is `page_indices.shape[0]`.")
+    if kv_lens.dtype != torch.int32 or page_indices.dtype != torch.int32 or cu_q_lens.dtype != torch.int32:
+        raise ValueError(
+            "The dtype of `kv_lens`, `page_indices`, and `cu_q_lens` must be"
+            f" int32. Got kv_lens.dtype={kv_lens.dtype}, page_indices.dtype={page_indices.dtype},"
+            f" cu_q_lens.dtype={cu_q_lens.dtype}.")
+    if num_q_heads % num_kv_heads != 0:
+        raise ValueError(f"num_q_heads={num_q_heads} must be divisible by num_kv_heads={num_kv_heads}")
+    if sliding_window is not None and sliding_window <= 0:
+        raise ValueError(f"sliding_window={sliding_window} must be positive.")
+    if soft_cap is not None and soft_cap == 0.0:
+        raise ValueError(f"soft_cap={soft_cap} must not be 0.0.")
+    if num_kv_pages_per_block is not None and not 0 < num_kv_pages_per_block <= pages_per_seq:
+        raise ValueError(f"num_kv_pages_per_block={num_kv_pages_per_block} must be in range (0, {pages_per_seq}].")
+    if num_queries_per_block is not None and num_queries_per_block <= 0:
+        raise ValueError(f"num_queries_per_block={num_queries_per_block} must be positive.")
+    if vmem_limit_bytes is not None and vmem_limit_bytes <= 0:
+        raise ValueError(f"vmem_limit_bytes={vmem_limit_bytes} must be positive.")
+
+
+def dynamic_validate_inputs(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, **kwargs) -> None:
+    """``dynamic_validate_inputs`` (ragged_paged_attention.py:152-212); reads metadata to the host."""
+    static_validate_inputs(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, **kwargs)
+    max_num_batched_tokens = q.shape[0]
+    page_size = kv_pages.shape[1]
+    max_num_seqs, pages_per_seq = page_indices.shape
+    n = int(num_seqs.reshape(-1)[0].item())
+    if n > max_num_seqs:
+        raise ValueError(f"num_seqs[0]={n} must be less or equal to max_num_seqs={max_num_seqs}")
+    lens = kv_lens.cpu()
+    cu = cu_q_lens.cpu()
+    max_kv_len = int(lens.max().item()) if lens.numel() else 0
+    min_pages_per_seq = -(-max_kv_len // page_size)
+    if pages_per_seq < min_pages_per_seq:
+        raise ValueError(
+            f"pages_per_seq={pages_per_seq} must be greater or equal to"
+            f" min_pages_per_seq={min_pages_per_seq} given max_kv_len={max_kv_len} and page_size={page_size}.")
+    if int(cu[n]) > max_num_batched_tokens:
+        raise ValueError(f"Total q tokens {int(cu[n])} must be less or equal to"
+                         f" max_num_batched_tokens={max_num_batched_tokens}.")
+    for i in range(n):
+        q_len = int(cu[i + 1]) - int(cu[i])
+        kv_len = int(lens[i])
+        if q_len > kv_len:
+            raise ValueError(f"q_len={q_len} must be less or equal to kv_len={kv_len} at sequence {i}.")
+
+
+def make_shape(q, kv_pages, page_indices) -> _lib.RpaShape:
+    T, Hq, D = q.shape
+    P, S, C, _ = kv_pages.shape
+    n_max, pps = page_indices.shape
+    kvd = _KV_DTYPES.get(kv_pages.dtype)
+    if kvd is None:
+        raise ValueError(f"kv_pages dtype {kv_pages.dtype} is not bf16 or fp8-e4m3")
+    return _lib.RpaShape(T, Hq, C // 2, D, P, S, n_max, pps, kvd)
+
+
+def workspace_for(shape: _lib.RpaShape, device: torch.device, stream: int) -> torch.Tensor:
+    """Cached per-(device, stream) workspace; calls that share one must not overlap."""
+    lib = _lib.load()
+    need = lib.rpa_workspace_size(ctypes.byref(shape))
+    if need == 0:
+        _lib.check(-1)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+        _lib.check(lib.rpa_workspace_init(ws.data_ptr(), ws.numel(), stream))
+        _workspaces[key] = ws
+    return ws
+
+
+def ragged_paged_attention(
+    q: torch.Tensor,             # bf16 [max_num_batched_tokens, num_q_heads, head_dim]
+    kv_pages: torch.Tensor,      # bf16 | float8_e4m3fn | uint8 (e4m3 codes) [pages, page_size, 2*Hkv, D]
+    kv_lens: torch.Tensor,       # i32[max_num_seqs]
+    page_indices: torch.Tensor,  # i32[max_num_seqs, pages_per_seq]
+    cu_q_lens: torch.Tensor,     # i32[max_num_seqs + 1]
+    num_seqs: torch.Tensor,      # i32[1]
+    *,
+    sm_scale: float = 1.0,
+    sliding_window: int | None = None,
+    soft_cap: float | None = None,
+    mask_value: float | None = DEFAULT_MASK_VALUE,
+    k_scale: float | None = None,
+    v_scale: float | None = None,
+    num_kv_pages_per_block: int | None = None,
+    num_queries_per_block: int | None = None,
+    vmem_limit_bytes: int | None = None,
+    kv_scales: torch.Tensor | None = None,   # f32 [pages, Hkv, 2] per-(page, kv head) K/V scales
+    out: torch.Tensor | None = None,
+    kernel_events: tuple | None = None,      # (begin, end) torch.cuda.Event around the attention kernel
+) -> torch.Tensor:
+    """Ragged paged attention (mixed prefill and decode) on MI355X.
+
+    Semantics of ``ref_ragged_paged_attention`` (ragged_paged_attention.py:73-148).
+    Returns a new ``[T, Hq, D]`` bf16 tensor (or fills ``out``); rows at or past
+    ``cu_q_lens[num_seqs]`` are zero.
+    """
+    static_validate_inputs(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, sm_scale=sm_scale,
+                           sliding_window=sliding_window, soft_cap=soft_cap, mask_value=mask_value,
+                           k_scale=k_scale, v_scale=v_scale, num_kv_pages_per_block=num_kv_pages_per_block,
+                           num_queries_per_block=num_queries_per_block, vmem_limit_bytes=vmem_limit_bytes)
+    for name, t in (("q", q), ("kv_pages", kv_pages), ("kv_lens", kv_lens), ("page_indices", page_indices),
+                    ("cu_q_lens", cu_q_lens), ("num_seqs", num_seqs)):
+        _require_cuda(name, t)
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"q dtype {q.dtype} must be bfloat16")
+    if num_seqs.dtype != torch.int32:
+        raise ValueError(f"num_seqs dtype {num_seqs.dtype} must be int32")
+    shape = make_shape(q, kv_pages, page_indices)
+    if kv_scales is not None:
+        if shape.kv_dtype != _lib.RPA_KV_FP8_E4M3:
+            raise ValueError("kv_scales requires fp8 kv_pages")
+        _require_cuda("kv_scales", kv_scales)
+        if kv_scales.dtype != torch.float32 or tuple(kv_scales.shape) != (shape.total_pages, shape.num_kv_heads, 2):
+            raise ValueError(f"kv_scales must be float32 [{shape.total_pages}, {shape.num_kv_heads}, 2]")
+        if k_scale is not None or v_scale is not None:
+            raise ValueError("pass either per-page kv_scales or scalar k_scale/v_scale, not both")
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require_cuda("out", out)
+        if out.shape != q.shape or out.dtype != q.dtype or out.data_ptr() == q.data_ptr():
+            raise ValueError("out must be a separate tensor shaped like q")
+    if mask_value is None:
+        mask_value = DEFAULT_MASK_VALUE
+    opts = _lib.RpaOptions(
+        float(sm_scale), int(sliding_window or 0), float(soft_cap or 0.0),
+        1, float(mask_value),
+        int(k_scale is not None), float(k_scale if k_scale is not None else 1.0),
+        int(v_scale is not None), float(v_scale if v_scale is not None else 1.0),
+    )
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        ws = workspace_for(shape, q.device, stream)
+        lib = _lib.load()
+        args = (ctypes.byref(shape), ctypes.byref(opts), q.data_ptr(), kv_pages.data_ptr(),
+                kv_scales.data_ptr() if kv_scales is not None else None,
+                kv_lens.data_ptr(), page_indices.data_ptr(), cu_q_lens.data_ptr(), num_seqs.data_ptr(),
+                out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        if kernel_events is None:
+            rc = lib.rpa_ragged_paged_attention(*args)
+        else:
+            begin, end = kernel_events
+            if not begin.cuda_event or not end.cuda_event:
+                raise ValueError("kernel_events must be recorded once before use (HIP events are created lazily)")
+            rc = lib.rpa_ragged_paged_attention_timed(*args, begin.cuda_event, end.cuda_event)
+        _lib.check(rc)
+    return out
+
+
+def read_error_word(device: torch.device | None = None) -> int:
+    """Synchronously read the device-side metadata error word of the current stream's workspace."""
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _workspaces.get(key)
+    if ws is None:
+        return 0
+    word = ctypes.c_int32(0)
+    _lib.check(_lib.load().rpa_read_error_word(ws.data_ptr(), ws.numel(), ctypes.byref(word), stream))
+    return int(word.value)
+
+
+def gather_kv(kv_pages, kv_lens, page_indices, num_seqs) -> torch.Tensor:
+    """Dense ``[sum(kv_lens[:num_seqs]), 2*Hkv, D]`` copy of the K/V rows the kernel reads."""
+    for name, t in (("kv_pages", kv_pages), ("kv_lens", kv_lens), ("page_indices", page_indices),
+                    ("num_seqs", num_seqs)):
+        _require_cuda(name, t)
+    n = int(num_seqs.reshape(-1)[0].item())
+    rows = int(kv_lens[:n].to(torch.int64).sum().item())
+    P, S, C, D = kv_pages.shape
+    dense = torch.zeros((rows, C, D), dtype=kv_pages.dtype, device=kv_pages.device)
+    dummy_q = torch.empty((0, C // 2, D), dtype=torch.bfloat16, device=kv_pages.device)
+    shape = make_shape(dummy_q, kv_pages, page_indices)
+    with torch.cuda.device(kv_pages.device):
+        stream = torch.cuda.current_stream(kv_pages.device).cuda_stream
+        ws = workspace_for(shape, kv_pages.device, stream)
+        _lib.check(_lib.load().rpa_gather_kv(
+            ctypes.byref(shape), kv_pages.data_ptr(), kv_lens.data_ptr(), page_indices.data_ptr(),
+            num_seqs.data_ptr(), dense.data_ptr() if rows else None, rows, ws.data_ptr(), ws.numel(), stream))
+    return dense
+
+
+def case_to_device(case, device="cuda") -> dict:
+    """Host ``RpaCase`` (tpu_cake_amd.workloads) -> dict of device tensors for the operator."""
+    import numpy as np
+
+    dev = torch.device(device)
+    q = torch.from_numpy(np.ascontiguousarray(case.q).view(np.int16)).view(torch.bfloat16).to(dev)
+    if case.kv_dtype == "fp8":
+        kv = torch.from_numpy(np.ascontiguousarray(case.kv_pages)).view(torch.float8_e4m3fn).to(dev)
+    else:
+        kv = torch.from_numpy(np.ascontiguousarray(case.kv_pages).view(np.int16)).view(torch.bfloat16).to(dev)
+    d = {
+        "q": q,
+        "kv_pages": kv,
+        "kv_lens": torch.from_numpy(np.ascontiguousarray(case.kv_lens, dtype=np.int32)).to(dev),
+        "page_indices": torch.from_numpy(np.ascontiguousarray(case.page_indices, dtype=np.int32)).to(dev),
+        "cu_q_lens": torch.from_numpy(np.ascontiguousarray(case.cu_q_lens, dtype=np.int32)).to(dev),
+        "num_seqs": torch.from_numpy(np.ascontiguousarray(case.num_seqs, dtype=np.int32)).to(dev),
+    }
+    if case.kv_scales is not None:
+        d["kv_scales"] = torch.from_numpy(np.ascontiguousarray(case.kv_scales, dtype=np.float32)).to(dev)
+    return d
+
+
+def run_case(case, device="cuda", **kwargs) -> torch.Tensor:
+    """Run the operator on a host ``RpaCase``; returns the device output."""
+    d = case_to_device(case, device)
+    kv_scales = d.pop("kv_scales", None)
+    return ragged_paged_attention(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
+                                  d["num_seqs"], sm_scale=case.sm_scale, kv_scales=kv_scales, **kwargs)
+
+
+def default_sm_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

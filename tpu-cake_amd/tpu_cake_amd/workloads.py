@@ -1,0 +1,249 @@
+"""Seeded synthetic RPA workloads: the five MI355X benchmark configurations.
+
+Each builder returns an :class:`RpaCase` of host numpy arrays in the
+reference's operator layout (``ecosystem/source/jax/ragged_paged_attention.py:718-750``):
+
+* ``q``            bf16 bits ``uint16 [T, Hq, D]``
+* ``kv_pages``     bf16 bits ``uint16`` or fp8-e4m3 codes ``uint8`` ``[P, S, 2*Hkv, D]``;
+                   K of kv-head h is combined head ``2h``, V is ``2h+1``
+* ``kv_scales``    ``float32 [P, Hkv, 2]`` (K, V) for fp8 pools, else ``None``
+* ``kv_lens``      ``int32 [N]``; ``page_indices`` ``int32 [N, PPS]``;
+  ``cu_q_lens`` ``int32 [N+1]``; ``num_seqs`` ``int32 [1]``
+
+Inputs follow the reference's recipe (``src/tpu_cake/workloads/inkling_rpa.py:413-418``):
+N(0,1) float32 draws rounded to bf16 with round-to-nearest-even.  Lengths and
+the page permutation come from ``numpy.random.default_rng(seed)`` in that
+order.  Query and K/V values come from a second source chosen by ``values``:
+``"host"`` continues the numpy generator (queries, then the pool), ``"cuda"``
+draws them on the GPU with ``torch.Generator("cuda").manual_seed(seed * 16 + k)``
+(k = 1 queries, k = 2 pool) -- the same distribution, fast for pools of
+hundreds of MB.  Both are deterministic; ``"auto"`` picks ``"cuda"`` when a GPU
+is present.  Logical page ``p`` of
+sequence ``i`` is ``perm[offset_i + p]`` for ``p < cdiv(L_i, S)``; unused
+page-table slots hold 0, as upstream clamps them (``ragged_paged_attention.py:53``).
+
+Pinned choices the benchmark description leaves open:
+
+* C2/C4 log-normal sigma = 0.5; C5 pool = 1.25x the pages in use (like C2).
+* fp8 scales are separate for K and V: ``scale[p, h, c] = max|x| / 448`` over
+  the (page, kv-head, K-or-V) tile of the bf16 source (1.0 for an all-zero tile).
+* ``sm_scale = 1/sqrt(128)`` for every configuration.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import numpy as np
+import torch
+
+LOGNORMAL_SIGMA = 0.5
+POOL_FACTOR = 1.25
+FP8_MAX = 448.0
+
+CONFIG_SEEDS = {"c1": 97, "c2": 98, "c3": 99, "c4": 98, "c5": 101}
+
+CONFIG_DESCRIPTIONS = {
+    "c1": "tiny decode: 4 seqs x 1 token, kv_len U[1,512], Hq 8 / Hkv 2, D 128, page 16, 160-page pool",
+    "c2": "GQA decode: 64 seqs x 1 token, kv_len lognormal(median 2048, sigma 0.5) clip 128-8192, Hq 32 / Hkv 8, D 128, page 64",
+    "c3": "mixed: 24 decode rows (kv_len U[512,8192]) + 4 causal prefill chunks of 512 over prior U[0,3584], Hq 32 / Hkv 8, page 64",
+    "c4": "fp8-e4m3 KV decode: C2 shapes, per-(page, kv head) K and V scales = max|x|/448",
+    "c5": "heavy-tail decode: 256 seqs x 1 token, kv_len 16*(1+Lomax(1.2)) clip 16-131072, Hq 64 / Hkv 8, D 128, page 64",
+}
+
+
+@dataclasses.dataclass
+class RpaCase:
+    name: str
+    q: np.ndarray
+    kv_pages: np.ndarray
+    kv_lens: np.ndarray
+    page_indices: np.ndarray
+    cu_q_lens: np.ndarray
+    num_seqs: np.ndarray
+    sm_scale: float
+    kv_dtype: str = "bf16"
+    kv_scales: np.ndarray | None = None
+    kv_source: np.ndarray | None = None  # bf16 pool the fp8 pool was quantised from
+
+    @property
+    def num_q_heads(self) -> int:
+        return int(self.q.shape[1])
+
+    @property
+    def num_kv_heads(self) -> int:
+        return int(self.kv_pages.shape[2] // 2)
+
+    @property
+    def head_dim(self) -> int:
+        return int(self.q.shape[2])
+
+    @property
+    def page_size(self) -> int:
+        return int(self.kv_pages.shape[1])
+
+    @property
+    def q_lens(self) -> np.ndarray:
+        n = int(self.num_seqs[0])
+        return np.diff(self.cu_q_lens[: n + 1]).astype(np.int64)
+
+    def kv_read_bytes(self) -> int:
+        """Algorithmic KV bytes one call must read: sum(L) * Hkv * 2 * D * elem (+ scales)."""
+        n = int(self.num_seqs[0])
+        toks = int(np.sum(self.kv_lens[:n], dtype=np.int64))
+        elem = 1 if self.kv_dtype == "fp8" else 2
+        b = toks * self.num_kv_heads * 2 * self.head_dim * elem
+        if self.kv_scales is not None:
+            pages = int(np.sum(-(-self.kv_lens[:n].astype(np.int64) // self.page_size)))
+            b += pages * self.num_kv_heads * 2 * 4
+        return b
+
+    def prefill_flops(self) -> int:
+        """Causal QK^T + PV flops of rows with q_len > 1: 4*Hq*D*sum(visible keys)."""
+        n = int(self.num_seqs[0])
+        total = 0
+        for i in range(n):
+            ql = int(self.cu_q_lens[i + 1] - self.cu_q_lens[i])
+            if ql <= 1:
+                continue
+            L = int(self.kv_lens[i])
+            prior = L - ql
+            total += ql * prior + ql * (ql + 1) // 2
+        return 4 * self.num_q_heads * self.head_dim * total
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bf16 bit patterns (via torch's cast)."""
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32))
+    return t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _page_table(rng, kv_lens, page_size, pool_pages, pages_per_seq):
+    need = -(-kv_lens.astype(np.int64) // page_size)
+    total = int(need.sum())
+    if total > pool_pages:
+        raise ValueError(f"pool of {pool_pages} pages cannot hold {total} pages")
+    perm = rng.permutation(pool_pages).astype(np.int32)
+    table = np.zeros((len(kv_lens), pages_per_seq), dtype=np.int32)
+    off = 0
+    for i, n in enumerate(need):
+        table[i, :n] = perm[off: off + n]
+        off += int(n)
+    return table
+
+
+def _normal_bf16(rng, shape, values: str = "host", seed: int = 0, stream: int = 0) -> np.ndarray:
+    if values == "cuda":
+        g = torch.Generator(device="cuda").manual_seed(int(seed) * 16 + stream)
+        x = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(torch.bfloat16)
+        return x.view(torch.int16).cpu().numpy().view(np.uint16)
+    return f32_to_bf16_bits(rng.standard_normal(size=shape, dtype=np.float32))
+
+
+def _resolve_values(values: str) -> str:
+    if values == "auto":
+        return "cuda" if torch.cuda.is_available() else "host"
+    if values not in ("host", "cuda"):
+        raise ValueError(f"values must be 'auto', 'host' or 'cuda', got {values!r}")
+    return values
+
+
+def build_case(name: str, *, kv_lens, q_lens, num_q_heads, num_kv_heads, head_dim, page_size,
+               pool_pages, pages_per_seq, rng, sm_scale=None, values="host", seed=0) -> RpaCase:
+    kv_lens = np.asarray(kv_lens, dtype=np.int32)
+    q_lens = np.asarray(q_lens, dtype=np.int32)
+    table = _page_table(rng, kv_lens, page_size, pool_pages, pages_per_seq)
+    cu = np.zeros(len(kv_lens) + 1, dtype=np.int32)
+    cu[1:] = np.cumsum(q_lens)
+    T = int(cu[-1])
+    q = _normal_bf16(rng, (T, num_q_heads, head_dim), values, seed, 1)
+    kv = _normal_bf16(rng, (pool_pages, page_size, 2 * num_kv_heads, head_dim), values, seed, 2)
+    return RpaCase(
+        name=name, q=q, kv_pages=kv, kv_lens=kv_lens, page_indices=table, cu_q_lens=cu,
+        num_seqs=np.array([len(kv_lens)], dtype=np.int32),
+        sm_scale=float(sm_scale if sm_scale is not None else 1.0 / math.sqrt(head_dim)),
+    )
+
+
+def quantize_fp8(case: RpaCase) -> RpaCase:
+    """fp8-e4m3 pool + per-(page, kv-head, K|V) scales from a bf16 case."""
+    P, S, C, D = case.kv_pages.shape
+    Hkv = C // 2
+    dev = "cuda" if torch.cuda.is_available() else "cpu"
+    src = torch.from_numpy(case.kv_pages.view(np.int16)).view(torch.bfloat16).to(dev)
+    x = src.float().view(P, S, Hkv, 2, D)
+    amax = x.abs().amax(dim=(1, 4))  # [P, Hkv, 2]
+    scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
+    q = (x / scale.view(P, 1, Hkv, 2, 1)).clamp_(-FP8_MAX, FP8_MAX)
+    codes = q.to(torch.float8_e4m3fn).view(torch.uint8).view(P, S, C, D).cpu().numpy()
+    return dataclasses.replace(case, kv_pages=codes, kv_dtype="fp8",
+                               kv_scales=scale.cpu().numpy().astype(np.float32),
+                               kv_source=case.kv_pages)
+
+
+def make_config(cfg: str, seed: int | None = None, values: str = "auto") -> RpaCase:
+    """Build one of the benchmark configurations ``c1`` .. ``c5``."""
+    cfg = cfg.lower()
+    if seed is None:
+        seed = CONFIG_SEEDS[cfg]
+    rng = np.random.default_rng(seed)
+    vk = dict(values=_resolve_values(values), seed=seed)
+    if cfg == "c1":
+        lens = rng.integers(1, 512, size=4, endpoint=True)
+        return build_case("c1", kv_lens=lens, q_lens=np.ones(4), num_q_heads=8, num_kv_heads=2,
+                          head_dim=128, page_size=16, pool_pages=160, pages_per_seq=32, rng=rng, **vk)
+    if cfg in ("c2", "c4"):
+        z = rng.standard_normal(64)
+        lens = np.clip(np.rint(np.exp(math.log(2048.0) + LOGNORMAL_SIGMA * z)), 128, 8192).astype(np.int64)
+        pages = int(np.sum(-(-lens // 64)))
+        case = build_case(cfg, kv_lens=lens, q_lens=np.ones(64), num_q_heads=32, num_kv_heads=8,
+                          head_dim=128, page_size=64, pool_pages=math.ceil(POOL_FACTOR * pages),
+                          pages_per_seq=128, rng=rng, **vk)
+        return quantize_fp8(case) if cfg == "c4" else case
+    if cfg == "c3":
+        dec = rng.integers(512, 8192, size=24, endpoint=True)
+        prior = rng.integers(0, 3584, size=4, endpoint=True)
+        lens = np.concatenate([dec, prior + 512])
+        qls = np.concatenate([np.ones(24, dtype=np.int64), np.full(4, 512)])
+        pages = int(np.sum(-(-lens // 64)))
+        return build_case("c3", kv_lens=lens, q_lens=qls, num_q_heads=32, num_kv_heads=8,
+                          head_dim=128, page_size=64, pool_pages=math.ceil(POOL_FACTOR * pages),
+                          pages_per_seq=128, rng=rng, **vk)
+    if cfg == "c5":
+        lens = np.clip(np.floor(16.0 * (1.0 + rng.pareto(1.2, size=256))), 16, 131072).astype(np.int64)
+        pages = int(np.sum(-(-lens // 64)))
+        return build_case("c5", kv_lens=lens, q_lens=np.ones(256), num_q_heads=64, num_kv_heads=8,
+                          head_dim=128, page_size=64, pool_pages=math.ceil(POOL_FACTOR * pages),
+                          pages_per_seq=2048, rng=rng, **vk)
+    raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+
+
+def make_custom(*, kv_lens, q_lens, num_q_heads, num_kv_heads, head_dim=128, page_size=16,
+                pool_factor=1.25, pages_per_seq=None, seed=0, sm_scale=None, max_num_seqs=None,
+                num_tokens=None, kv_dtype="bf16", values="auto") -> RpaCase:
+    """Small ad-hoc case for tests: explicit lengths, optional padding of N_max / T."""
+    rng = np.random.default_rng(seed)
+    kv_lens = np.asarray(kv_lens, dtype=np.int64)
+    need = int(np.sum(-(-kv_lens // page_size)))
+    pps = pages_per_seq or max(1, int(-(-max(int(kv_lens.max(initial=0)), 1) // page_size)))
+    case = build_case("custom", kv_lens=kv_lens, q_lens=q_lens, num_q_heads=num_q_heads,
+                      num_kv_heads=num_kv_heads, head_dim=head_dim, page_size=page_size,
+                      pool_pages=max(1, math.ceil(pool_factor * need)), pages_per_seq=pps, rng=rng,
+                      sm_scale=sm_scale, values=_resolve_values(values), seed=seed)
+    n = len(kv_lens)
+    if max_num_seqs is not None and max_num_seqs > n:
+        pad = max_num_seqs - n
+        case.kv_lens = np.concatenate([case.kv_lens, np.zeros(pad, np.int32)])
+        case.page_indices = np.concatenate([case.page_indices, np.zeros((pad, pps), np.int32)])
+        case.cu_q_lens = np.concatenate([case.cu_q_lens, np.full(pad, case.cu_q_lens[-1], np.int32)])
+    if num_tokens is not None and num_tokens > case.q.shape[0]:
+        extra = _normal_bf16(rng, (num_tokens - case.q.shape[0],) + case.q.shape[1:])
+        case.q = np.concatenate([case.q, extra])
+    if kv_dtype == "fp8":
+        case = quantize_fp8(case)
+    return case
