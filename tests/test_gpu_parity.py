@@ -144,9 +144,14 @@ def test_scalar_kv_scales_bf16(cuda):
 
 def test_fp8_kv_per_page_scales(cuda):
     _say("fp8 KV with per-(page, head) scales")
-    case = make_custom(kv_lens=[1, 100, 257, 1500], q_lens=[1, 1, 1, 1], num_q_heads=32, num_kv_heads=8,
-                       page_size=64, seed=31, kv_dtype="fp8")
-    out = _check(case)  # vs the oracle on the same fp8 codes and scales
+    # vs the oracle on the same fp8 codes and scales (2e-2), any length
+    _check(make_custom(kv_lens=[1, 2, 33, 100], q_lens=[1, 1, 1, 1], num_q_heads=32, num_kv_heads=8,
+                       page_size=64, seed=31, kv_dtype="fp8"))
+    # vs the bf16 source the pool was quantised from (6e-2): C4's lengths (>= 128 keys, so the
+    # output averages many e4m3 values; a single-key output is one dequantised V row, off by up to 2^-4 relative)
+    case = make_custom(kv_lens=[128, 257, 1500, 4000], q_lens=[1, 1, 1, 1], num_q_heads=32, num_kv_heads=8,
+                       page_size=64, seed=32, kv_dtype="fp8")
+    out = _check(case)
     src = orc.ref_ragged_paged_attention(case.q, case.kv_source, case.kv_lens, case.page_indices, case.cu_q_lens,
                                          case.num_seqs, sm_scale=case.sm_scale)
     err = orc.errors(out[: src.shape[0]], src)
