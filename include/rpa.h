@@ -82,7 +82,9 @@ const char* rpa_last_error(void);
 size_t rpa_workspace_size(const rpa_shape_t* shape);
 
 /* One-time initialisation of a freshly allocated workspace (zeroes the error
- * word), stream-ordered.  Call once per workspace buffer. */
+ * word and the split-K descriptors, which every call leaves cleared again),
+ * stream-ordered.  Call once per workspace buffer.  Calls sharing one
+ * workspace must not overlap in time (same stream, or ordered by events). */
 int rpa_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
 /* Ragged paged attention forward.  Replaces
@@ -110,8 +112,8 @@ int rpa_ragged_paged_attention(const rpa_shape_t* shape, const rpa_options_t* op
 
 /* Measurement hook: rpa_ragged_paged_attention, additionally recording the
  * caller's hipEvent_t event_begin / event_end on `stream` immediately before
- * and after the attention kernel (not the split-K combine), so a caller can
- * time the dominant kernel alone.  No counterpart in the reference (its runner
+ * and after the attention kernel (not the split-K combine that follows it),
+ * so a caller can time the dominant kernel alone.  No counterpart in the reference (its runner
  * reads per-kernel device time from XProf, src/tpu_cake/rpa_bundle.py:114-139). */
 int rpa_ragged_paged_attention_timed(const rpa_shape_t* shape, const rpa_options_t* options,
                                      const void* q, const void* kv_pages, const float* kv_scales,

@@ -6,11 +6,14 @@
 //
 // Structure (one call = two launches on the caller's stream):
 //   rpa_attn_kernel     stream-K over (sequence, kv head, row block, 32-key chunk) units
-//                       (see rpa_schedule.h); one 64-lane wave per workgroup; QK^T and PV
-//                       on v_mfma_f32_16x16x32_bf16; online softmax in fp32 (exp2 domain);
-//                       writes finished rows, or a split-K partial (m, l, acc).
-//   rpa_combine_kernel  log-sum-exp merge of the partials of rows split across workgroups,
-//                       and zeroes output rows at or past cu_q_lens[num_seqs].
+//                       (see rpa_schedule.h); one 64-lane wave per workgroup; QK^T and PV on
+//                       v_mfma_f32_16x16x32_bf16; online softmax in fp32 (exp2 domain).  A row
+//                       block finished inside one workgroup is written directly; a row block
+//                       split across workgroups leaves one partial (m, l, acc) per workgroup,
+//                       and the workgroup owning its last unit leaves a descriptor of it.
+//   rpa_combine_kernel  one 4-wave workgroup per descriptor: log-sum-exp merge of the row
+//                       block's partials (the waves take every 4th contributor, then merge
+//                       through LDS), writes the rows, clears the descriptor.
 //
 // MFMA operand layouts (16x16x32 bf16, wave64): A[i][k] and B[k][j] place row i / column j
 // at lane%16 and the 32 k-slots at (lane/16, element 0..7); D[i][j] sits at lane
@@ -54,6 +57,12 @@ enum KvMode { KV_BF16 = 0, KV_BF16_SCALED = 1, KV_FP8 = 2 };
 
 enum ErrBits { ERR_PAGE = 1, ERR_QROW = 2, ERR_KVLEN = 4, ERR_QLEN = 8 };
 
+// A row block split across workgroups b0..b (b = the owner of its last unit).
+struct SplitDesc {
+  int valid, nch, q_start, q_len, h, rb;
+  long long b0;
+};
+
 struct Params {
   const uint16_t* q;
   const uint8_t* kv;
@@ -65,6 +74,7 @@ struct Params {
   uint16_t* out;
   float* part_acc;  // [2*grid][16][kD]
   float* part_ml;   // [2*grid][16][2]  (m in log2 units, l)
+  struct SplitDesc* desc;  // [grid] split row block ending in workgroup b (valid = 0 otherwise)
   int32_t* err;
   int T, Hq, Hkv, G, P, S, log2S, Nmax, PPS;
   float sm_scale;
@@ -140,20 +150,18 @@ struct SeqInfo {
   int kv_len, q_start, q_len, units;  // units: per kv head
 };
 
-__device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq) {
+__device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, int& err) {
   SeqInfo s{0, 0, 0, 0};
   if (i < nseq) {
     int kv = p.kv_lens[i];
     int c0 = p.cu_q_lens[i];
     int c1 = p.cu_q_lens[i + 1];
-    int err = 0;
     long long cap = (long long)p.PPS * p.S;
     if (kv > cap) { kv = (int)cap; err |= ERR_KVLEN; }
     if (kv < 0) kv = 0;
     int ql = c1 - c0;
     if (c0 < 0 || ql < 0 || c1 > p.T) { ql = 0; err |= ERR_QROW; }
     if (ql > kv) err |= ERR_QLEN;
-    if (err) atomicOr(p.err, err);
     s.kv_len = kv;
     s.q_start = c0;
     s.q_len = ql;
@@ -162,10 +170,10 @@ __device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq) {
   return s;
 }
 
-__device__ __forceinline__ long long total_units(const Params& p, int nseq, int lane) {
+__device__ __forceinline__ long long total_units(const Params& p, int nseq, int lane, int& err) {
   long long w = 0;
   for (int base = 0; base < nseq; base += 64) {
-    SeqInfo s = load_seq(p, base + lane, nseq);
+    SeqInfo s = load_seq(p, base + lane, nseq, err);
     w += wave_sum64((long long)s.units * p.Hkv);
   }
   return w;
@@ -173,10 +181,10 @@ __device__ __forceinline__ long long total_units(const Params& p, int nseq, int 
 
 // Sequence holding unit u and the first unit of that sequence (wave-uniform results).
 __device__ __forceinline__ void locate_seq(const Params& p, int nseq, int lane, long long u, int& seq,
-                                           long long& seq_start) {
+                                           long long& seq_start, int& err) {
   long long off = 0;
   for (int base = 0; base < nseq; base += 64) {
-    SeqInfo s = load_seq(p, base + lane, nseq);
+    SeqInfo s = load_seq(p, base + lane, nseq, err);
     long long cnt = (long long)s.units * p.Hkv;
     long long incl = wave_incl_scan64(cnt, lane);
     long long tile = rl64(incl, 63);
@@ -199,9 +207,9 @@ struct Window {
   SeqInfo s;
 };
 
-__device__ __forceinline__ void load_window(const Params& p, int nseq, int base, int lane, Window& w) {
+__device__ __forceinline__ void load_window(const Params& p, int nseq, int base, int lane, Window& w, int& err) {
   w.base = base;
-  w.s = load_seq(p, base + lane, nseq);
+  w.s = load_seq(p, base + lane, nseq, err);
 }
 
 struct Cursor {
@@ -240,7 +248,7 @@ __device__ __forceinline__ Cursor cursor_at(const Params& p, const Window& w, in
   return x;
 }
 
-__device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Window& w, Cursor& x) {
+__device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Window& w, Cursor& x, int& err) {
   if (x.c + 1 < x.nch) {
     x.c++;
     return;
@@ -260,7 +268,7 @@ __device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Win
           x.nch = 0;
           return;
         }
-        if (i >= w.base + 64) load_window(p, nseq, i, lane, w);
+        if (i >= w.base + 64) load_window(p, nseq, i, lane, w, err);
         if (rl(w.s.units, i - w.base) > 0) break;
       }
       cursor_load_seq(p, w, i, x);
@@ -280,92 +288,103 @@ struct Pages {
   int pg[2];
 };
 
+// Loads in the streaming loop are never predicated: lanes past kv_len (and cursors past the
+// end of the range, nch == 0) read clamped, always-valid addresses -- key kv_len-1, or row 0 --
+// whose values the -inf scores then exclude.  Straight-line loads let the compiler count
+// outstanding loads exactly (s_waitcnt vmcnt(N)) so the next unit's loads stay in flight.
 __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, int n) {
   Pages r;
+  const bool live = x.nch > 0;
+  const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
+  const size_t row = live ? (size_t)x.i * p.PPS : 0;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.c * KV_CHUNK + 16 * blk + n;
-    r.pg[blk] = 0;
-    if (x.nch > 0 && kt < x.kv_len) r.pg[blk] = p.page_indices[(size_t)x.i * p.PPS + page_of(kt, p)];
+    kt = live ? (kt < last ? kt : last) : 0;
+    r.pg[blk] = p.page_indices[row + page_of(kt, p)];
   }
   return r;
 }
 
+// K and V of one unit for one lane: keys c*32 + 16*blk + n, dims 32*s + 8*j .. +8.
 template <int MODE>
-struct KvRegs;
+struct HalfRegs;
 
 template <>
-struct KvRegs<KV_BF16> {
-  u32x4 k[2][4], v[2][4];
+struct HalfRegs<KV_BF16> {
+  u32x4 w[2][4];
 };
 template <>
-struct KvRegs<KV_BF16_SCALED> {
-  u32x4 k[2][4], v[2][4];
+struct HalfRegs<KV_BF16_SCALED> {
+  u32x4 w[2][4];
 };
 template <>
-struct KvRegs<KV_FP8> {
-  u32x2 k[2][4], v[2][4];
-  float ks[2], vs[2];
+struct HalfRegs<KV_FP8> {
+  u32x2 w[2][4];
+  float sc[2];  // per-(page, kv head) scale of each of the lane's two keys
 };
 
-template <int MODE>
-__device__ __forceinline__ void load_kv(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
-                                        KvRegs<MODE>& r) {
+// Where this lane's two keys of unit x live (element index of their K row) and their pages.
+struct UnitAddr {
+  size_t e[2];
+  int pg[2];
+  int h;
+};
+
+__device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
+                                              int& err) {
+  UnitAddr a;
+  const bool live = x.nch > 0;
+  const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
+  a.h = live ? x.h : 0;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.c * KV_CHUNK + 16 * blk + n;
+    const bool in_seq = live && kt < x.kv_len;
+    kt = live ? (kt < last ? kt : last) : 0;
     int pg = pages.pg[blk];
-    bool in_seq = x.nch > 0 && kt < x.kv_len;
-    bool ok = in_seq && pg >= 0 && pg < p.P;
-    if (in_seq && !ok) atomicOr(p.err, ERR_PAGE);
+    const bool pg_ok = pg >= 0 && pg < p.P;
+    if (in_seq && !pg_ok) err |= ERR_PAGE;
+    pg = pg_ok ? pg : 0;
+    a.pg[blk] = pg;
+    a.e[blk] = kv_elem(p, pg, kt, 2 * a.h) + 8 * j;
+  }
+  return a;
+}
+
+// which = 0 loads K (combined head 2h), 1 loads V (2h+1, one row of kD further).
+template <int MODE>
+__device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, int which, HalfRegs<MODE>& r) {
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const size_t e = a.e[blk] + (size_t)which * kD;
     if constexpr (MODE == KV_FP8) {
-      r.ks[blk] = p.k_scale;
-      r.vs[blk] = p.v_scale;
+      const uint8_t* kp = p.kv + e;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) r.k[blk][s] = r.v[blk][s] = u32x2{0u, 0u};
-      if (ok) {
-        size_t e = kv_elem(p, pg, kt, 2 * x.h) + 8 * j;
-        const uint8_t* kp = p.kv + e;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          r.k[blk][s] = *(const u32x2*)(kp + 32 * s);
-          r.v[blk][s] = *(const u32x2*)(kp + kD + 32 * s);
-        }
-        if (p.kv_scales) {
-          const float* sc = p.kv_scales + ((size_t)pg * p.Hkv + x.h) * 2;
-          r.ks[blk] *= sc[0];
-          r.vs[blk] *= sc[1];
-        }
-      }
+      for (int s = 0; s < 4; ++s) r.w[blk][s] = *(const u32x2*)(kp + 32 * s);
+      float sc = which ? p.v_scale : p.k_scale;
+      if (p.kv_scales) sc *= p.kv_scales[((size_t)a.pg[blk] * p.Hkv + a.h) * 2 + which];
+      r.sc[blk] = sc;
     } else {
+      const uint16_t* kp = (const uint16_t*)p.kv + e;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) r.k[blk][s] = r.v[blk][s] = u32x4{0u, 0u, 0u, 0u};
-      if (ok) {
-        size_t e = kv_elem(p, pg, kt, 2 * x.h) + 8 * j;
-        const uint16_t* kp = (const uint16_t*)p.kv + e;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          r.k[blk][s] = *(const u32x4*)(kp + 32 * s);
-          r.v[blk][s] = *(const u32x4*)(kp + kD + 32 * s);
-        }
-      }
+      for (int s = 0; s < 4; ++s) r.w[blk][s] = *(const u32x4*)(kp + 32 * s);
     }
   }
 }
 
-// Query rows of cursor x as the B operand of QK^T (zero for rows past q_len * G).
+// Query rows of cursor x as the B operand of QK^T.  Rows past q_len * G read row 0 of the
+// sequence instead: their columns of S and O are never stored, and MFMA columns are independent.
 __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, bf16x8 q[4]) {
+  const bool live = x.nch > 0;
   int row = x.rb * ROW_BLOCK + n;
-  bool ok = x.nch > 0 && row < x.q_len * p.G;
-  int tok = row / p.G;
-  int g = row - tok * p.G;
+  if (!(live && row < x.q_len * p.G)) row = 0;
+  const int tok = row / p.G;
+  const int g = row - tok * p.G;
+  const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)x.h * p.G : 0;
+  const uint16_t* qp = p.q + ((size_t)tok * p.Hq + base + g) * kD + 8 * j;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) q[s] = bf16x8{};
-  if (ok) {
-    const uint16_t* qp = p.q + ((size_t)(x.q_start + tok) * p.Hq + (size_t)x.h * p.G + g) * kD + 8 * j;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
-  }
+  for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
 }
 
 // bf16(float(x) * scale) for 8 packed bf16 values (the reference's k_scale formula, :124-129).
@@ -394,23 +413,14 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 w, float sc) {
 }
 
 template <int MODE>
-__device__ __forceinline__ void kv_to_bf16(const KvRegs<MODE>& r, const Params& p, u32x4 k[2][4],
-                                           u32x4 v[2][4]) {
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if constexpr (MODE == KV_FP8) {
-        k[blk][s] = fp8x8_to_bf16x8(r.k[blk][s], r.ks[blk]);
-        v[blk][s] = fp8x8_to_bf16x8(r.v[blk][s], r.vs[blk]);
-      } else if constexpr (MODE == KV_BF16_SCALED) {
-        k[blk][s] = scale_bf16x8(r.k[blk][s], p.k_scale);
-        v[blk][s] = scale_bf16x8(r.v[blk][s], p.v_scale);
-      } else {
-        k[blk][s] = r.k[blk][s];
-        v[blk][s] = r.v[blk][s];
-      }
-    }
+__device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which) {
+  if constexpr (MODE == KV_FP8) {
+    return fp8x8_to_bf16x8(r.w[blk][s], r.sc[blk]);
+  } else if constexpr (MODE == KV_BF16_SCALED) {
+    return scale_bf16x8(r.w[blk][s], which ? p.v_scale : p.k_scale);
+  } else {
+    return r.w[blk][s];
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -420,24 +430,25 @@ struct RowState {
   f32x4 acc[8];  // O^T: dims 16*blk + 4j + r, row n
   float m, l;    // running max (log2 units) and this lane's partial sum
   int pos;       // causal limit of this lane's row (last visible key)
-  int row_ok;    // row < q_len * G
-  int tok, head; // query token and query head of this lane's row
   bool started_here;
 };
 
+// One unit.  S = K Q^T; then the next unit's queries are loaded into q (their registers are
+// free once QK^T has issued); V^T goes to LDS, after which the next unit's V is loaded into the
+// registers just released; then softmax and O^T += V^T P^T.
 template <int MODE>
-__device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const KvRegs<MODE>& r,
-                                             const bf16x8 q[4], RowState& st, uint8_t* vt, int n, int j) {
-  u32x4 kb[2][4], vb[2][4];
-  kv_to_bf16<MODE>(r, p, kb, vb);
-
+__device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const HalfRegs<MODE>& kr,
+                                             const HalfRegs<MODE>& vr, bf16x8 q[4], const Cursor& nx,
+                                             const UnitAddr& nx_addr, HalfRegs<MODE>& v_next, RowState& st,
+                                             uint8_t* vt, int n, int j) {
   // S = K Q^T for the two 16-key blocks
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    s0 = mfma(__builtin_bit_cast(bf16x8, kb[0][s]), q[s], s0);
-    s1 = mfma(__builtin_bit_cast(bf16x8, kb[1][s]), q[s], s1);
+    s0 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE>(kr, p, 0, s, 0)), q[s], s0);
+    s1 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE>(kr, p, 1, s, 0)), q[s], s1);
   }
+  load_q(p, nx, n, j, q);
 
   // V^T into LDS: key t = 16*blk + n goes to slot pos = 8*(n/4) + 4*blk + n%4 of each dim row
   __syncthreads();
@@ -445,15 +456,18 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   for (int blk = 0; blk < 2; ++blk) {
     const int slot_b = 2 * (8 * (n >> 2) + 4 * blk + (n & 3));
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 vw = to_bf16x8<MODE>(vr, p, blk, s, 1);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        uint32_t w = vb[blk][s][t];
+        uint32_t w = vw[t];
         int d = 32 * s + 8 * j + 2 * t;
         *(uint16_t*)(vt + d * kVTRow + slot_b) = (uint16_t)(w & 0xffffu);
         *(uint16_t*)(vt + (d + 1) * kVTRow + slot_b) = (uint16_t)(w >> 16);
       }
+    }
   }
+  load_half<MODE>(p, nx_addr, 1, v_next);
 
   // scores in log2 units with masks; this lane holds keys 16*blk + 4j + rr of row n
   float xs[2][4];
@@ -521,11 +535,8 @@ __device__ __forceinline__ void begin_row_block(const Params& p, const Cursor& x
   for (int d = 0; d < 8; ++d) st.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = -INFINITY;
   st.l = 0.f;
-  int row = x.rb * ROW_BLOCK + n;
-  st.row_ok = row < x.q_len * p.G;
-  st.tok = row / p.G;
-  st.head = x.h * p.G + (row - st.tok * p.G);
-  st.pos = x.kv_len - x.q_len + st.tok;
+  const int row = x.rb * ROW_BLOCK + n;
+  st.pos = x.kv_len - x.q_len + row / p.G;
   st.started_here = x.c == 0;
 }
 
@@ -535,9 +546,12 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
   lt += __shfl_xor(lt, 16, 64);
   lt += __shfl_xor(lt, 32, 64);
   if (complete) {
-    if (st.row_ok) {
+    const int row = x.rb * ROW_BLOCK + n;
+    if (row < x.q_len * p.G) {
+      const int tok = row / p.G;
+      const int head = x.h * p.G + (row - tok * p.G);
       const float inv = 1.f / lt;
-      uint16_t* op = p.out + ((size_t)(x.q_start + st.tok) * p.Hq + st.head) * kD + 4 * j;
+      uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * kD + 4 * j;
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         u32x2 w;
@@ -547,14 +561,18 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
       }
     }
   } else {
-    const size_t slot = (size_t)partial_slot(b, st.started_here);
-    float* ap = p.part_acc + (slot * ROW_BLOCK + n) * kD + 4 * j;
+    // split row block: this workgroup's share, rows that exist only (read by rpa_combine_kernel)
+    const int row = x.rb * ROW_BLOCK + n;
+    if (row < x.q_len * p.G) {
+      const size_t slot = (size_t)partial_slot(b, st.started_here);
+      float* ap = p.part_acc + (slot * ROW_BLOCK + n) * kD + 4 * j;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) *(f32x4*)(ap + 16 * d) = st.acc[d];
-    if (j == 0) {
-      float* mp = p.part_ml + (slot * ROW_BLOCK + n) * 2;
-      mp[0] = st.m;
-      mp[1] = lt;
+      for (int d = 0; d < 8; ++d) *(f32x4*)(ap + 16 * d) = st.acc[d];
+      if (j == 0) {
+        float* mp = p.part_ml + (slot * ROW_BLOCK + n) * 2;
+        mp[0] = st.m;
+        mp[1] = lt;
+      }
     }
   }
 }
@@ -562,35 +580,42 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
 template <int MODE>
 __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n, int j, int b, long long u,
                                      long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
-                                     Pages& pg_nxt, const KvRegs<MODE>& kv_cur, KvRegs<MODE>& kv_nxt,
-                                     bf16x8 q[4], RowState& st, uint8_t* vt) {
-  // Prefetch.  Every buffer is redefined on every path (zeros when there is no next unit) so a
-  // buffer's previous contents are never kept alive across a step.
-  //   K/V of the next unit: its page ids arrived during the previous step.
-  load_kv<MODE>(p, nxt, pg_nxt, n, j, kv_nxt);
-  //   queries of the next unit: new rows only when it starts a row block.
-  bf16x8 qn[4];
-  if (nxt.nch > 0 && nxt.c == 0) {
-    load_q(p, nxt, n, j, qn);
-  } else {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qn[s] = q[s];
-  }
-  //   page ids two units ahead.
+                                     Pages& pg_nxt, const HalfRegs<MODE>& k_cur, const HalfRegs<MODE>& v_cur,
+                                     HalfRegs<MODE>& k_nxt, HalfRegs<MODE>& v_nxt, bf16x8 q[4], RowState& st,
+                                     uint8_t* vt, int& err, const Partition& pt) {
+  // Prefetch, oldest-needed first: page ids two units ahead, then the next unit's K (its page
+  // ids arrived a step ago); its queries and V follow inside compute_unit as registers free up.
+  // Every buffer is redefined each step.
   Cursor ahead = nxt;
   if (u + 2 < u1)
-    advance(p, nseq, lane, win, ahead);
+    advance(p, nseq, lane, win, ahead, err);
   else
     ahead.nch = 0;
-  pg_nxt = load_pages(p, ahead, n);
+  const Pages pg_ahead = load_pages(p, ahead, n);
+  const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, err);
+  load_half<MODE>(p, nx_addr, 0, k_nxt);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit<MODE>(p, cur, kv_cur, q, st, vt, n, j);
+  compute_unit<MODE>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j);
   const bool last_of_rb = cur.c == cur.nch - 1;
-  if (last_of_rb || u == u1 - 1) finish_row_block(p, cur, st, b, st.started_here && last_of_rb, n, j);
+  if (last_of_rb || u == u1 - 1) {
+    const bool complete = st.started_here && last_of_rb;
+    finish_row_block(p, cur, st, b, complete, n, j);
+    if (!complete && !st.started_here && last_of_rb && lane == 0) {
+      // this workgroup owns the split row block's last unit: describe it for the combine
+      SplitDesc d;
+      d.valid = 1;
+      d.nch = cur.nch;
+      d.q_start = cur.q_start;
+      d.q_len = cur.q_len;
+      d.h = cur.h;
+      d.rb = cur.rb;
+      d.b0 = owner_of(u - cur.c, pt);
+      p.desc[b] = d;
+    }
+  }
 
-#pragma unroll
-  for (int s = 0; s < 4; ++s) q[s] = qn[s];
+  pg_nxt = pg_ahead;
   cur = nxt;
   nxt = ahead;
 }
@@ -603,117 +628,139 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int b = blockIdx.x;
   int nseq = uni(p.num_seqs[0]);
   nseq = nseq < 0 ? 0 : (nseq > p.Nmax ? p.Nmax : nseq);
+  int err = 0;
 
-  const long long W = total_units(p, nseq, lane);
-  if (W == 0) return;
-  const long long u0 = uni64(range_start(b, W, p.grid)), u1 = uni64(range_start(b + 1, W, p.grid));
-  if (u0 >= u1) return;
-
-  int seq;
-  long long seq_start;
-  locate_seq(p, nseq, lane, u0, seq, seq_start);
-  if (seq >= nseq) return;
-  Window win;
-  load_window(p, nseq, seq, lane, win);
-
-  Cursor cur = cursor_at(p, win, seq, u0 - seq_start);
-  Cursor nxt = cur;
-  if (u0 + 1 < u1)
-    advance(p, nseq, lane, win, nxt);
-  else
-    nxt.nch = 0;
-  const Pages pg_cur = load_pages(p, cur, n);
-  Pages pg_nxt = load_pages(p, nxt, n);
-  KvRegs<MODE> kva, kvb;
-  bf16x8 q[4];
-  load_kv<MODE>(p, cur, pg_cur, n, j, kva);
-  load_q(p, cur, n, j, q);
-  RowState st;
-
-  long long u = u0;
-  for (;;) {
-    step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kva, kvb, q, st, vt);
-    if (++u >= u1) break;
-    step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kvb, kva, q, st, vt);
-    if (++u >= u1) break;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------
-// split-K combine (+ zero fill of rows past the last sequence)
-// ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void rpa_combine_kernel(Params p) {
-  const int lane = threadIdx.x;
-  const int b = blockIdx.x;
-  int nseq = p.num_seqs[0];
-  nseq = nseq < 0 ? 0 : (nseq > p.Nmax ? p.Nmax : nseq);
-
-  if (b == 0) {
-    int tv = p.cu_q_lens[nseq];
+  {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
+    int tv = uni(p.cu_q_lens[nseq]);
     tv = tv < 0 ? 0 : (tv > p.T ? p.T : tv);
     const size_t first = (size_t)tv * p.Hq * kD / 8, last = (size_t)p.T * p.Hq * kD / 8;
     u32x4* o = (u32x4*)p.out;
-    for (size_t k = first + lane; k < last; k += 64) o[k] = u32x4{0u, 0u, 0u, 0u};
+    for (size_t k = first + (size_t)b * 64 + lane; k < last; k += (size_t)p.grid * 64) o[k] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  const long long W = total_units(p, nseq, lane);
-  if (W == 0) return;
-  const long long u0 = range_start(b, W, p.grid), u1 = range_start(b + 1, W, p.grid);
-  if (u0 >= u1) return;
-  int seq;
-  long long seq_start;
-  locate_seq(p, nseq, lane, u0, seq, seq_start);
-  if (seq >= nseq) return;
-  Window win;
-  load_window(p, nseq, seq, lane, win);
-  const Cursor x = cursor_at(p, win, seq, u0 - seq_start);
-  if (x.c == 0) return;                         // the row block began in this workgroup
-  const long long tstart = u0 - x.c, tend = tstart + x.nch;
-  if (tend > u1) return;                        // a later workgroup holds its end
-  const long long b0 = owner_of(tstart, W, p.grid);
+  const long long W = total_units(p, nseq, lane, err);
+  const Partition pt = make_partition(W, p.grid);
+  const long long u0 = uni64(range_start(b, pt)), u1 = uni64(range_start(b + 1, pt));
+  if (W > 0 && u0 < u1) {
+    int seq;
+    long long seq_start;
+    locate_seq(p, nseq, lane, u0, seq, seq_start, err);
+    if (seq < nseq) {
+      Window win;
+      load_window(p, nseq, seq, lane, win, err);
+      Cursor cur = cursor_at(p, win, seq, u0 - seq_start);
+      Cursor nxt = cur;
+      if (u0 + 1 < u1)
+        advance(p, nseq, lane, win, nxt, err);
+      else
+        nxt.nch = 0;
+      const Pages pg_cur = load_pages(p, cur, n);
+      Pages pg_nxt = load_pages(p, nxt, n);
+      HalfRegs<MODE> ka, va, kb, vb;
+      bf16x8 q[4];
+      {
+        const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, err);
+        load_half<MODE>(p, a0, 0, ka);
+        load_half<MODE>(p, a0, 1, va);
+      }
+      load_q(p, cur, n, j, q);
+      RowState st;
 
-  const int n = lane & 15, quarter = lane >> 4;  // row n, dims 32*quarter .. +32
-  float mstar = -INFINITY;
-  for (long long bb = b0; bb <= b; ++bb) {
-    if (range_start(bb, W, p.grid) == range_start(bb + 1, W, p.grid)) continue;
-    const size_t slot = (size_t)partial_slot(bb, bb == b0);
-    mstar = fmaxf(mstar, p.part_ml[(slot * ROW_BLOCK + n) * 2]);
-  }
-  const float mu = mstar == -INFINITY ? 0.f : mstar;
-  float o[32];
-#pragma unroll
-  for (int k = 0; k < 32; ++k) o[k] = 0.f;
-  float lsum = 0.f;
-  for (long long bb = b0; bb <= b; ++bb) {
-    if (range_start(bb, W, p.grid) == range_start(bb + 1, W, p.grid)) continue;
-    const size_t slot = (size_t)partial_slot(bb, bb == b0);
-    const float* ml = p.part_ml + (slot * ROW_BLOCK + n) * 2;
-    const float w = __builtin_amdgcn_exp2f(ml[0] - mu);
-    lsum += w * ml[1];
-    const f32x4* ap = (const f32x4*)(p.part_acc + (slot * ROW_BLOCK + n) * kD + 32 * quarter);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      f32x4 a = ap[k];
-      o[4 * k + 0] += w * a[0];
-      o[4 * k + 1] += w * a[1];
-      o[4 * k + 2] += w * a[2];
-      o[4 * k + 3] += w * a[3];
+      long long u = u0;
+      for (;;) {
+        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt);
+        if (++u >= u1) break;
+        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt);
+        if (++u >= u1) break;
+      }
     }
   }
-  const int row = x.rb * ROW_BLOCK + n;
-  if (row < x.q_len * p.G) {
-    const int tok = row / p.G;
-    const int head = x.h * p.G + (row - tok * p.G);
-    const float inv = 1.f / lsum;
-    // partial acc rows are stored as O^T column n: dim d at index d (see finish_row_block)
-    uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * kD + 32 * quarter;
+  if (err) atomicOr(p.err, err);
+}
+
+// ---------------------------------------------------------------------------------------------
+// split-K combine
+// ---------------------------------------------------------------------------------------------
+struct Merge {
+  float m, l, o[32];
+};
+
+__device__ __forceinline__ void merge_in(Merge& a, float mc, float lc, const float* oc) {
+  const float mn = fmaxf(a.m, mc);
+  const float mu = mn == -INFINITY ? 0.f : mn;
+  const float wa = __builtin_amdgcn_exp2f(a.m - mu), wc = __builtin_amdgcn_exp2f(mc - mu);
+  a.l = a.l * wa + lc * wc;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      u32x2 w;
-      w[0] = pack_bf16x2(o[4 * k + 0] * inv, o[4 * k + 1] * inv);
-      w[1] = pack_bf16x2(o[4 * k + 2] * inv, o[4 * k + 3] * inv);
-      *(u32x2*)(op + 4 * k) = w;
+  for (int k = 0; k < 32; ++k) a.o[k] = a.o[k] * wa + oc[k] * wc;
+  a.m = mn;
+}
+
+// Workgroup b merges the row block described by desc[b]: contributors b0..b, b0's share in slot
+// 2*b0+1 and every later one's in slot 2*bb.  Wave w takes contributors w, w+4, ... (two per
+// iteration, loads issued together); lane (row n = lane%16, dims 32*(lane/16) .. +32).  The four
+// waves' results are merged through LDS in a fixed order, so the output is deterministic.
+__global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
+  __shared__ float red[4][64][34];
+  const int b = blockIdx.x;
+  const SplitDesc d = p.desc[b];
+  if (!d.valid) return;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const int n = lane & 15, quarter = lane >> 4;
+  const int row = d.rb * ROW_BLOCK + n;
+  const bool row_ok = row < d.q_len * p.G;
+  const int ncontrib = (int)(b - d.b0 + 1);
+
+  Merge acc;
+  acc.m = -INFINITY;
+  acc.l = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) acc.o[k] = 0.f;
+  if (row_ok) {
+    for (int k = wv; k < ncontrib; k += 8) {
+      const bool two = k + 4 < ncontrib;
+      const size_t s0 = (size_t)partial_slot(d.b0 + k, k == 0);
+      const size_t s1 = (size_t)partial_slot(d.b0 + k + 4, false);
+      const float* ml0 = p.part_ml + (s0 * ROW_BLOCK + n) * 2;
+      const float* ml1 = p.part_ml + ((two ? s1 : s0) * ROW_BLOCK + n) * 2;
+      const f32x4* a0 = (const f32x4*)(p.part_acc + (s0 * ROW_BLOCK + n) * kD + 32 * quarter);
+      const f32x4* a1 = (const f32x4*)(p.part_acc + ((two ? s1 : s0) * ROW_BLOCK + n) * kD + 32 * quarter);
+      float o0[32], o1[32];
+      const float m0 = ml0[0], l0 = ml0[1], m1 = ml1[0], l1 = ml1[1];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const f32x4 x0 = a0[v], x1 = a1[v];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          o0[4 * v + r] = x0[r];
+          o1[4 * v + r] = x1[r];
+        }
+      }
+      merge_in(acc, m0, l0, o0);
+      if (two) merge_in(acc, m1, l1, o1);
     }
+  }
+  red[wv][lane][0] = acc.m;
+  red[wv][lane][1] = acc.l;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) red[wv][lane][2 + k] = acc.o[k];
+  __syncthreads();
+  if (wv == 0) {
+    if (row_ok) {
+      for (int w = 1; w < 4; ++w) merge_in(acc, red[w][lane][0], red[w][lane][1], &red[w][lane][2]);
+      const int tok = row / p.G;
+      const int head = d.h * p.G + (row - tok * p.G);
+      const float inv = 1.f / acc.l;
+      // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
+      uint16_t* op = p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + 32 * quarter;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        u32x2 w;
+        w[0] = pack_bf16x2(acc.o[4 * k + 0] * inv, acc.o[4 * k + 1] * inv);
+        w[1] = pack_bf16x2(acc.o[4 * k + 2] * inv, acc.o[4 * k + 3] * inv);
+        *(u32x2*)(op + 4 * k) = w;
+      }
+    }
+    if (lane == 0) p.desc[b].valid = 0;
   }
 }
 
@@ -800,12 +847,26 @@ int device_info(DeviceInfo& out) {
   return RPA_OK;
 }
 
-size_t workspace_bytes_for(const DeviceInfo& d) {
-  int gmax = d.cus * kMaxWavesPerCU;
-  size_t ml = (size_t)2 * gmax * ROW_BLOCK * 2 * sizeof(float);
-  size_t acc = (size_t)2 * gmax * ROW_BLOCK * kD * sizeof(float);
-  return kHeaderBytes + ((ml + 255) / 256) * 256 + acc;
+// Workspace: [error word | pad to 256] [split descriptors, one per workgroup] [partial m,l]
+// [partial acc].  Header and descriptors are zeroed once (rpa_workspace_init); every call
+// leaves each descriptor invalid again when its combine has run.
+struct WsLayout {
+  size_t desc, ml, acc, total;
+};
+
+size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+WsLayout ws_layout(const DeviceInfo& d) {
+  const size_t gmax = (size_t)d.cus * kMaxWavesPerCU;
+  WsLayout w;
+  w.desc = kHeaderBytes;
+  w.ml = w.desc + round256(gmax * sizeof(SplitDesc));
+  w.acc = w.ml + round256(2 * gmax * ROW_BLOCK * 2 * sizeof(float));
+  w.total = w.acc + 2 * gmax * ROW_BLOCK * kD * sizeof(float);
+  return w;
 }
+
+size_t workspace_bytes_for(const DeviceInfo& d) { return ws_layout(d).total; }
 
 int check_shape(const rpa_shape_t* s) {
   if (!s) return fail(RPA_E_INVALID, "shape is NULL");
@@ -859,8 +920,12 @@ size_t rpa_workspace_size(const rpa_shape_t* shape) {
 }
 
 int rpa_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
-  if (!workspace || workspace_bytes < kHeaderBytes) return fail(RPA_E_WORKSPACE, "workspace too small");
-  if (hipMemsetAsync(workspace, 0, kHeaderBytes, (hipStream_t)stream) != hipSuccess)
+  DeviceInfo d;
+  int rc = device_info(d);
+  if (rc) return rc;
+  const WsLayout w = ws_layout(d);
+  if (!workspace || workspace_bytes < w.total) return fail(RPA_E_WORKSPACE, "workspace too small");
+  if (hipMemsetAsync(workspace, 0, w.ml, (hipStream_t)stream) != hipSuccess)
     return fail(RPA_E_HIP, "hipMemsetAsync failed");
   return RPA_OK;
 }
@@ -904,10 +969,10 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   p.num_seqs = num_seqs;
   p.out = (uint16_t*)out;
   p.err = (int32_t*)workspace;
-  const int gmax = d.cus * kMaxWavesPerCU;
-  const size_t ml_bytes = (((size_t)2 * gmax * ROW_BLOCK * 2 * sizeof(float)) + 255) / 256 * 256;
-  p.part_ml = (float*)((uint8_t*)workspace + kHeaderBytes);
-  p.part_acc = (float*)((uint8_t*)workspace + kHeaderBytes + ml_bytes);
+  const WsLayout w = ws_layout(d);
+  p.desc = (SplitDesc*)((uint8_t*)workspace + w.desc);
+  p.part_ml = (float*)((uint8_t*)workspace + w.ml);
+  p.part_acc = (float*)((uint8_t*)workspace + w.acc);
   p.sm_scale = opt->sm_scale;
   p.scale_log2 = opt->sm_scale * kLog2e;
   const float mask = opt->has_mask_value ? opt->mask_value : kDefaultMask;
@@ -940,7 +1005,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("attention launch failed: ") + hipGetErrorString(e));
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(end) failed");
-  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid), dim3(64), 0, st, p);
+  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid), dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
   return RPA_OK;

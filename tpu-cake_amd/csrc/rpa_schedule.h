@@ -12,8 +12,9 @@
 //     the reference gives masked keys weight exp(s + mask - m), so every key
 //     below kv_len is visited instead.
 // Units are ordered sequence-major, then kv head, then row block, then chunk.
-// Workgroup b of a grid of `grid` owns units [start(b), start(b+1)) with
-// start(b) = floor(b * W / grid): every workgroup gets the same number of
+// Workgroup b of a grid of `grid` owns units [start(b), start(b+1)): with q = W / grid and
+// r = W % grid, the first r workgroups own q + 1 units and the rest q, so every workgroup gets
+// the same number of
 // KV chunks (+-1) whatever the length distribution ("stream-K").
 //
 // Everything here is plain integer arithmetic usable on host and device.
@@ -62,14 +63,29 @@ RPA_HD int seq_units_per_head(int kv_len, int q_len, int group, bool skip_masked
   return u;
 }
 
-// First unit of workgroup b.
-RPA_HD int64_t range_start(int64_t b, int64_t total, int64_t grid) {
-  return b * total / grid;
+// Balanced partition of W units over `grid` workgroups (q = W / grid, r = W % grid): the first
+// r workgroups own q + 1 units, the rest q.  Workgroups that own nothing (b >= W when W < grid)
+// all come last, so the owners of any unit range are consecutive non-empty workgroups.
+struct Partition {
+  int64_t q, r;
+};
+
+RPA_HD Partition make_partition(int64_t total, int64_t grid) {
+  Partition pt;
+  pt.q = total / grid;
+  pt.r = total - pt.q * grid;
+  return pt;
 }
 
-// The workgroup whose range holds unit u (largest b with range_start(b) <= u).
-RPA_HD int64_t owner_of(int64_t u, int64_t total, int64_t grid) {
-  return ((u + 1) * grid - 1) / total;
+// First unit of workgroup b.
+RPA_HD int64_t range_start(int64_t b, const Partition& pt) {
+  return b * pt.q + (b < pt.r ? b : pt.r);
+}
+
+// The workgroup whose range holds unit u.
+RPA_HD int64_t owner_of(int64_t u, const Partition& pt) {
+  const int64_t big = pt.r * (pt.q + 1);  // units owned by the first r workgroups
+  return u < big ? u / (pt.q + 1) : pt.r + (u - big) / pt.q;
 }
 
 // Split-K partial slots: each workgroup writes at most two partial segments,
