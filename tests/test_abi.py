@@ -1,0 +1,102 @@
+"""The C ABI: librpa.so loads, exports every entry point include/rpa.h declares, the ctypes
+structs match the C layout, host-side argument checks fail before any GPU work, and the
+work-decomposition math the kernels share passes the host checker.  No GPU needed."""
+
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from tpu_cake_amd import _lib
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "rpa.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.library_path().exists():
+        from tpu_cake_amd import build
+        build.build()
+    return _lib.load()
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(rpa_[a-z_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.library_path())], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (rpa_\w+)", out))
+    missing = [s for s in declared_functions() if s not in exported]
+    assert not missing, missing
+    for s in declared_functions():
+        assert hasattr(lib, s)
+
+
+def test_abi_version(lib):
+    assert lib.rpa_abi_version() == _lib.ABI_VERSION == 1
+
+
+def test_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "rpa.h"\n'
+        "int main(void){\n"
+        '  printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t), offsetof(rpa_shape_t, kv_dtype),\n'
+        "         sizeof(rpa_options_t), offsetof(rpa_options_t, mask_value), offsetof(rpa_options_t, v_scale),\n"
+        "         offsetof(rpa_options_t, has_k_scale));\n  return 0; }\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(_lib.RpaShape), _lib.RpaShape.kv_dtype.offset, ctypes.sizeof(_lib.RpaOptions),
+            _lib.RpaOptions.mask_value.offset, _lib.RpaOptions.v_scale.offset, _lib.RpaOptions.has_k_scale.offset]
+    assert got == want
+
+
+def _shape(**kw):
+    base = dict(num_tokens=4, num_q_heads=8, num_kv_heads=2, head_dim=128, total_pages=10, page_size=16,
+                max_num_seqs=4, pages_per_seq=4, kv_dtype=0)
+    base.update(kw)
+    return _lib.RpaShape(**base)
+
+
+def test_unsupported_head_dim_rejected_before_launch(lib):
+    opts = _lib.RpaOptions(sm_scale=1.0)
+    rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape(head_dim=64)), ctypes.byref(opts), *([None] * 9), 0,
+                                        None)
+    assert rc == -2
+    assert b"head_dim 64" in lib.rpa_last_error()
+
+
+@pytest.mark.parametrize("bad,msg", [(dict(num_q_heads=6, num_kv_heads=4), b"divisible"),
+                                     (dict(kv_dtype=7), b"kv_dtype"),
+                                     (dict(page_size=0), b"non-positive")])
+def test_invalid_shapes_rejected(lib, bad, msg):
+    opts = _lib.RpaOptions(sm_scale=1.0)
+    rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape(**bad)), ctypes.byref(opts), *([None] * 9), 0, None)
+    assert rc == -1 and msg in lib.rpa_last_error()
+
+
+def test_null_pointers_rejected(lib):
+    rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape()), None, *([None] * 9), 0, None)
+    assert rc == -1 and b"options" in lib.rpa_last_error()
+    opts = _lib.RpaOptions(sm_scale=1.0)
+    rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape()), ctypes.byref(opts), *([None] * 9), 0, None)
+    assert rc == -1 and b"NULL" in lib.rpa_last_error()
+
+
+def test_schedule_math_host_checker(tmp_path):
+    exe = tmp_path / "sched_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", f"-I{ROOT / 'tpu-cake_amd' / 'csrc'}",
+                    str(ROOT / "tests" / "sched_check.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and out.stdout.startswith("OK"), out.stdout + out.stderr
