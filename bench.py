@@ -87,6 +87,9 @@ def main() -> int:
     ap.add_argument("--rotate-bytes", type=float, default=2.0e9,
                     help="KV pool copies rotated so that at least this many bytes separate reuses")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", type=float, default=0.0, metavar="BYTES",
+                    help="instead of the benchmark, run 5 device-to-device copies of BYTES (the known-size "
+                         "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -105,6 +108,16 @@ def main() -> int:
         return 2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+
+    if args.copy_probe:
+        n = int(args.copy_probe) // 16 * 16
+        src = torch.empty(n // 4, dtype=torch.int32, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
+        return 0
 
     t0 = time.perf_counter()
     case = make_config(args.config, seed=args.seed)

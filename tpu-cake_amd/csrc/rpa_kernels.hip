@@ -5,8 +5,12 @@
 // 2h+1, fp32 scores and softmax, optional sliding window / soft cap / mask value / K,V scales).
 //
 // Structure (one call = two launches on the caller's stream):
-//   rpa_attn_kernel     stream-K over (sequence, kv head, row block, 32-key chunk) units
-//                       (see rpa_schedule.h); one 64-lane wave per workgroup; QK^T and PV on
+//   rpa_attn_kernel     stream-K over (sequence, kv-head group, row block, 32-key chunk) units
+//                       (see rpa_schedule.h).  A workgroup is one wave per kv head of a group of
+//                       HG heads (HG = the largest divisor of Hkv that is <= 8): its waves walk
+//                       the same units in step, wave w computing kv head group*HG + w, so the
+//                       HG heads' slices of each key's 2*Hkv*D row are fetched together (full
+//                       rows reach HBM far better than isolated per-head slices); QK^T and PV on
 //                       v_mfma_f32_16x16x32_bf16; online softmax in fp32 (exp2 domain).  A row
 //                       block finished inside one workgroup is written directly; a row block
 //                       split across workgroups leaves one partial (m, l, acc) per workgroup,
@@ -31,6 +35,7 @@
 
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -46,6 +51,7 @@ constexpr int kD = 128;          // head_dim built
 constexpr int kVTRow = 80;       // bytes per LDS row (one dim) of the transposed V chunk: 64 + 16 pad
 constexpr int kMaxWavesPerCU = 8;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleLog2 = 8.f;  // lazy softmax rescale threshold (log2 units)
 constexpr float kDefaultMask = -0.7f * 3.4028234663852886e38f;  // ragged_paged_attention.py:32
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -59,7 +65,8 @@ enum ErrBits { ERR_PAGE = 1, ERR_QROW = 2, ERR_KVLEN = 4, ERR_QLEN = 8 };
 
 // A row block split across workgroups b0..b (b = the owner of its last unit).
 struct SplitDesc {
-  int valid, nch, q_start, q_len, h, rb;
+  int valid[8];  // one flag per wave (kv head of the group); the combine clears its own
+  int nch, q_start, q_len, h, rb, pad;  // h = kv-head group
   long long b0;
 };
 
@@ -77,6 +84,7 @@ struct Params {
   struct SplitDesc* desc;  // [grid] split row block ending in workgroup b (valid = 0 otherwise)
   int32_t* err;
   int T, Hq, Hkv, G, P, S, log2S, Nmax, PPS;
+  int HG, NG;  // kv heads per workgroup (one wave each) and kv-head groups (Hkv / HG)
   float sm_scale;
   float scale_log2;  // sm_scale * log2(e)
   float mask_log2;   // mask_value * log2(e)
@@ -118,6 +126,28 @@ __device__ __forceinline__ long long wave_incl_scan64(long long x, int lane) {
     if (lane >= o) x += y;
   }
   return x;
+}
+
+// Reduce a per-lane value over lanes {l, l^16, l^32, l^48} -- the four 16-lane rows that hold
+// one query row's keys -- with gfx950's v_permlane16_swap / v_permlane32_swap (VALU, no LDS).
+// permlane16_swap(x, x) returns rows (0,0,2,2) and (1,1,3,3); permlane32_swap returns
+// halves (lo,lo) and (hi,hi): combining each pair reduces over all four rows in every lane.
+__device__ __forceinline__ float rows4_max(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, (unsigned)a[0]), __builtin_bit_cast(float, (unsigned)a[1]));
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto c = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)c[0]), __builtin_bit_cast(float, (unsigned)c[1]));
+}
+
+__device__ __forceinline__ float rows4_sum(float v) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = __builtin_bit_cast(float, (unsigned)a[0]) + __builtin_bit_cast(float, (unsigned)a[1]);
+  const unsigned w = __builtin_bit_cast(unsigned, v);
+  const auto c = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __builtin_bit_cast(float, (unsigned)c[0]) + __builtin_bit_cast(float, (unsigned)c[1]);
 }
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -174,7 +204,7 @@ __device__ __forceinline__ long long total_units(const Params& p, int nseq, int 
   long long w = 0;
   for (int base = 0; base < nseq; base += 64) {
     SeqInfo s = load_seq(p, base + lane, nseq, err);
-    w += wave_sum64((long long)s.units * p.Hkv);
+    w += wave_sum64((long long)s.units * p.NG);
   }
   return w;
 }
@@ -185,7 +215,7 @@ __device__ __forceinline__ void locate_seq(const Params& p, int nseq, int lane, 
   long long off = 0;
   for (int base = 0; base < nseq; base += 64) {
     SeqInfo s = load_seq(p, base + lane, nseq, err);
-    long long cnt = (long long)s.units * p.Hkv;
+    long long cnt = (long long)s.units * p.NG;
     long long incl = wave_incl_scan64(cnt, lane);
     long long tile = rl64(incl, 63);
     if (u < off + tile) {
@@ -213,7 +243,7 @@ __device__ __forceinline__ void load_window(const Params& p, int nseq, int base,
 }
 
 struct Cursor {
-  int i, h, rb, c;  // sequence, kv head, row block, chunk
+  int i, h, rb, c;  // sequence, kv-head group, row block, chunk
   int nch;          // chunks of (i, h, rb); 0 = past the end
   int nrb;
   int kv_len, q_len, q_start;
@@ -257,7 +287,7 @@ __device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Win
   for (;;) {
     if (x.rb + 1 < x.nrb) {
       x.rb++;
-    } else if (x.h + 1 < p.Hkv) {
+    } else if (x.h + 1 < p.NG) {
       x.h++;
       x.rb = 0;
     } else {
@@ -332,11 +362,11 @@ struct UnitAddr {
 };
 
 __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
-                                              int& err) {
+                                              int wv, int& err) {
   UnitAddr a;
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
-  a.h = live ? x.h : 0;
+  a.h = live ? x.h * p.HG + wv : 0;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.c * KV_CHUNK + 16 * blk + n;
@@ -375,13 +405,13 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 
 // Query rows of cursor x as the B operand of QK^T.  Rows past q_len * G read row 0 of the
 // sequence instead: their columns of S and O are never stored, and MFMA columns are independent.
-__device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, bf16x8 q[4]) {
+__device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, int wv, bf16x8 q[4]) {
   const bool live = x.nch > 0;
   int row = x.rb * ROW_BLOCK + n;
   if (!(live && row < x.q_len * p.G)) row = 0;
   const int tok = row / p.G;
   const int g = row - tok * p.G;
-  const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)x.h * p.G : 0;
+  const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)(x.h * p.HG + wv) * p.G : 0;
   const uint16_t* qp = p.q + ((size_t)tok * p.Hq + base + g) * kD + 8 * j;
 #pragma unroll
   for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
@@ -440,7 +470,7 @@ template <int MODE>
 __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const HalfRegs<MODE>& kr,
                                              const HalfRegs<MODE>& vr, bf16x8 q[4], const Cursor& nx,
                                              const UnitAddr& nx_addr, HalfRegs<MODE>& v_next, RowState& st,
-                                             uint8_t* vt, int n, int j) {
+                                             uint8_t* vt, int n, int j, int wv) {
   // S = K Q^T for the two 16-key blocks
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -448,7 +478,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     s0 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE>(kr, p, 0, s, 0)), q[s], s0);
     s1 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE>(kr, p, 1, s, 0)), q[s], s1);
   }
-  load_q(p, nx, n, j, q);
+  load_q(p, nx, n, j, wv, q);
 
   // V^T into LDS: key t = 16*blk + n goes to slot pos = 8*(n/4) + 4*blk + n%4 of each dim row
   __syncthreads();
@@ -469,38 +499,56 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   }
   load_half<MODE>(p, nx_addr, 1, v_next);
 
-  // scores in log2 units with masks; this lane holds keys 16*blk + 4j + rr of row n
+  // scores in log2 units; this lane holds keys 16*blk + 4j + rr of row n.  A chunk every row
+  // of the block sees in full (no window, no soft cap) needs no per-score masking.
   float xs[2][4];
-  const int key0 = x.c * KV_CHUNK + 4 * j;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
+  const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
+  const bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
+                     (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
+  if (plain) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      float sv = blk ? s1[rr] : s0[rr];
-      float xv;
-      if (p.soft_cap > 0.f) {
-        float t = sv * p.sm_scale;
-        xv = p.soft_cap * tanhf(t / p.soft_cap) * kLog2e;
-      } else {
-        xv = sv * p.scale_log2;
-      }
-      int kt = key0 + 16 * blk + rr;
-      bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
-      if (masked) xv += p.mask_log2;
-      if (kt >= x.kv_len) xv = -INFINITY;
-      xs[blk][rr] = xv;
+      xs[0][rr] = s0[rr] * p.scale_log2;
+      xs[1][rr] = s1[rr] * p.scale_log2;
     }
+  } else {
+    const int key0 = x.c * KV_CHUNK + 4 * j;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float sv = blk ? s1[rr] : s0[rr];
+        float xv;
+        if (p.soft_cap > 0.f) {
+          float t = sv * p.sm_scale;
+          xv = p.soft_cap * tanhf(t / p.soft_cap) * kLog2e;
+        } else {
+          xv = sv * p.scale_log2;
+        }
+        int kt = key0 + 16 * blk + rr;
+        bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
+        if (masked) xv += p.mask_log2;
+        if (kt >= x.kv_len) xv = -INFINITY;
+        xs[blk][rr] = xv;
+      }
+  }
 
-  float mc = xs[0][0];
+  // Online softmax with a lazily moved reference: st.m only moves when a row's chunk maximum
+  // exceeds it by more than kRescaleLog2 (probabilities then stay <= 2^kRescaleLog2), so most
+  // chunks skip the rescale of l and acc.  Any reference gives the same normalised result.
+  float mc = fmaxf(fmaxf(fmaxf(xs[0][0], xs[0][1]), fmaxf(xs[0][2], xs[0][3])),
+                   fmaxf(fmaxf(xs[1][0], xs[1][1]), fmaxf(xs[1][2], xs[1][3])));
+  mc = rows4_max(mc);
+  const bool grow = mc > st.m + kRescaleLog2;
+  if (__ballot(grow)) {
+    const float mn = grow ? mc : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
+    st.l *= alpha;
 #pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) mc = fmaxf(mc, xs[blk][rr]);
-  mc = fmaxf(mc, __shfl_xor(mc, 16, 64));
-  mc = fmaxf(mc, __shfl_xor(mc, 32, 64));
-  const float mn = fmaxf(st.m, mc);
-  const float mu = (mn == -INFINITY) ? 0.f : mn;
-  const float alpha = __builtin_amdgcn_exp2f(st.m - mu);
+    for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+    st.m = mn;
+  }
+  const float mu = st.m == -INFINITY ? 0.f : st.m;
   float pr[2][4];
   float lsum = 0.f;
 #pragma unroll
@@ -510,10 +558,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
       pr[blk][rr] = __builtin_amdgcn_exp2f(xs[blk][rr] - mu);
       lsum += pr[blk][rr];
     }
-  st.l = st.l * alpha + lsum;
-  st.m = mn;
-#pragma unroll
-  for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+  st.l += lsum;
 
   u32x4 pw;
   pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
@@ -541,15 +586,13 @@ __device__ __forceinline__ void begin_row_block(const Params& p, const Cursor& x
 }
 
 __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& x, RowState& st, int b,
-                                                 bool complete, int n, int j) {
-  float lt = st.l;
-  lt += __shfl_xor(lt, 16, 64);
-  lt += __shfl_xor(lt, 32, 64);
+                                                 bool complete, int n, int j, int wv) {
+  const float lt = rows4_sum(st.l);
   if (complete) {
     const int row = x.rb * ROW_BLOCK + n;
     if (row < x.q_len * p.G) {
       const int tok = row / p.G;
-      const int head = x.h * p.G + (row - tok * p.G);
+      const int head = (x.h * p.HG + wv) * p.G + (row - tok * p.G);
       const float inv = 1.f / lt;
       uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * kD + 4 * j;
 #pragma unroll
@@ -564,7 +607,7 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
     // split row block: this workgroup's share, rows that exist only (read by rpa_combine_kernel)
     const int row = x.rb * ROW_BLOCK + n;
     if (row < x.q_len * p.G) {
-      const size_t slot = (size_t)partial_slot(b, st.started_here);
+      const size_t slot = (size_t)partial_slot(b, st.started_here) * p.HG + wv;
       float* ap = p.part_acc + (slot * ROW_BLOCK + n) * kD + 4 * j;
 #pragma unroll
       for (int d = 0; d < 8; ++d) *(f32x4*)(ap + 16 * d) = st.acc[d];
@@ -582,7 +625,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
                                      long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
                                      Pages& pg_nxt, const HalfRegs<MODE>& k_cur, const HalfRegs<MODE>& v_cur,
                                      HalfRegs<MODE>& k_nxt, HalfRegs<MODE>& v_nxt, bf16x8 q[4], RowState& st,
-                                     uint8_t* vt, int& err, const Partition& pt) {
+                                     uint8_t* vt, int& err, const Partition& pt, int wv) {
   // Prefetch, oldest-needed first: page ids two units ahead, then the next unit's K (its page
   // ids arrived a step ago); its queries and V follow inside compute_unit as registers free up.
   // Every buffer is redefined each step.
@@ -592,26 +635,26 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   else
     ahead.nch = 0;
   const Pages pg_ahead = load_pages(p, ahead, n);
-  const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, err);
+  const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, wv, err);
   load_half<MODE>(p, nx_addr, 0, k_nxt);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit<MODE>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j);
+  compute_unit<MODE>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j, wv);
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
-    finish_row_block(p, cur, st, b, complete, n, j);
+    finish_row_block(p, cur, st, b, complete, n, j, wv);
     if (!complete && !st.started_here && last_of_rb && lane == 0) {
-      // this workgroup owns the split row block's last unit: describe it for the combine
-      SplitDesc d;
-      d.valid = 1;
-      d.nch = cur.nch;
-      d.q_start = cur.q_start;
-      d.q_len = cur.q_len;
-      d.h = cur.h;
-      d.rb = cur.rb;
-      d.b0 = owner_of(u - cur.c, pt);
-      p.desc[b] = d;
+      // this workgroup owns the split row block's last unit: describe it for the combine (every
+      // wave writes the same fields and its own valid flag)
+      SplitDesc* d = p.desc + b;
+      d->nch = cur.nch;
+      d->q_start = cur.q_start;
+      d->q_len = cur.q_len;
+      d->h = cur.h;
+      d->rb = cur.rb;
+      d->b0 = owner_of(u - cur.c, pt);
+      d->valid[wv] = 1;
     }
   }
 
@@ -621,9 +664,11 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
 }
 
 template <int MODE>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint8_t vt[kD * kVTRow];
-  const int lane = threadIdx.x;
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x transposed V chunk
+  const int lane = threadIdx.x & 63;
+  const int wv = uni(threadIdx.x >> 6);
+  uint8_t* vt = smem + wv * (kD * kVTRow);
   const int n = lane & 15, j = lane >> 4;
   const int b = blockIdx.x;
   int nseq = uni(p.num_seqs[0]);
@@ -635,7 +680,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     tv = tv < 0 ? 0 : (tv > p.T ? p.T : tv);
     const size_t first = (size_t)tv * p.Hq * kD / 8, last = (size_t)p.T * p.Hq * kD / 8;
     u32x4* o = (u32x4*)p.out;
-    for (size_t k = first + (size_t)b * 64 + lane; k < last; k += (size_t)p.grid * 64) o[k] = u32x4{0u, 0u, 0u, 0u};
+    for (size_t k = first + (size_t)b * blockDim.x + threadIdx.x; k < last; k += (size_t)p.grid * blockDim.x)
+      o[k] = u32x4{0u, 0u, 0u, 0u};
   }
 
   const long long W = total_units(p, nseq, lane, err);
@@ -659,18 +705,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2, 2))) void
       HalfRegs<MODE> ka, va, kb, vb;
       bf16x8 q[4];
       {
-        const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, err);
+        const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err);
         load_half<MODE>(p, a0, 0, ka);
         load_half<MODE>(p, a0, 1, va);
       }
-      load_q(p, cur, n, j, q);
+      load_q(p, cur, n, j, wv, q);
       RowState st;
 
       long long u = u0;
       for (;;) {
-        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt);
+        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt, wv);
         if (++u >= u1) break;
-        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt);
+        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt, wv);
         if (++u >= u1) break;
       }
     }
@@ -701,9 +747,9 @@ __device__ __forceinline__ void merge_in(Merge& a, float mc, float lc, const flo
 // waves' results are merged through LDS in a fixed order, so the output is deterministic.
 __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
   __shared__ float red[4][64][34];
-  const int b = blockIdx.x;
+  const int b = blockIdx.x / p.HG, hw = blockIdx.x - b * p.HG;  // descriptor, wave (head) of its group
+  if (!p.desc[b].valid[hw]) return;
   const SplitDesc d = p.desc[b];
-  if (!d.valid) return;
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
   const int n = lane & 15, quarter = lane >> 4;
   const int row = d.rb * ROW_BLOCK + n;
@@ -718,8 +764,8 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
   if (row_ok) {
     for (int k = wv; k < ncontrib; k += 8) {
       const bool two = k + 4 < ncontrib;
-      const size_t s0 = (size_t)partial_slot(d.b0 + k, k == 0);
-      const size_t s1 = (size_t)partial_slot(d.b0 + k + 4, false);
+      const size_t s0 = (size_t)partial_slot(d.b0 + k, k == 0) * p.HG + hw;
+      const size_t s1 = (size_t)partial_slot(d.b0 + k + 4, false) * p.HG + hw;
       const float* ml0 = p.part_ml + (s0 * ROW_BLOCK + n) * 2;
       const float* ml1 = p.part_ml + ((two ? s1 : s0) * ROW_BLOCK + n) * 2;
       const f32x4* a0 = (const f32x4*)(p.part_acc + (s0 * ROW_BLOCK + n) * kD + 32 * quarter);
@@ -748,7 +794,7 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
     if (row_ok) {
       for (int w = 1; w < 4; ++w) merge_in(acc, red[w][lane][0], red[w][lane][1], &red[w][lane][2]);
       const int tok = row / p.G;
-      const int head = d.h * p.G + (row - tok * p.G);
+      const int head = (d.h * p.HG + hw) * p.G + (row - tok * p.G);
       const float inv = 1.f / acc.l;
       // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
       uint16_t* op = p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + 32 * quarter;
@@ -760,7 +806,7 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
         *(u32x2*)(op + 4 * k) = w;
       }
     }
-    if (lane == 0) p.desc[b].valid = 0;
+    if (lane == 0) p.desc[b].valid[hw] = 0;
   }
 }
 
@@ -813,19 +859,39 @@ constexpr size_t kHeaderBytes = 256;
 
 struct DeviceInfo {
   int cus = 0;
-  int grid[3] = {0, 0, 0};
+  int grid[3][9] = {};  // workgroups per launch, by kv mode and heads per workgroup (1..8)
 };
 
 std::mutex g_mu;
 DeviceInfo g_dev[64];
 
+// Heads per workgroup: the largest divisor of Hkv that is <= 8 (one wave each).
+int heads_per_group(int hkv) {
+  for (int g = hkv < 8 ? hkv : 8; g > 1; --g)
+    if (hkv % g == 0) return g;
+  return 1;
+}
+
+constexpr int kVtBytes = kD * kVTRow;
+
+// Workgroups for the persistent grid: the kernel's occupancy (2 waves per SIMD) in workgroups
+// of hg waves, capped so no CU holds more than kMaxWavesPerCU waves; RPA_WAVES_PER_CU (1..8)
+// lowers the cap -- a tuning knob, like the reference's block-size parameters.
 template <int MODE>
-int occupancy_grid(int cus) {
+int occupancy_grid(int cus, int hg) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE>, 64, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE>, 64 * hg, hg * kVtBytes) !=
+          hipSuccess ||
       per_cu <= 0)
-    per_cu = 2;
-  if (per_cu > kMaxWavesPerCU) per_cu = kMaxWavesPerCU;
+    per_cu = 1;
+  int cap = kMaxWavesPerCU;
+  if (const char* env = getenv("RPA_WAVES_PER_CU")) {
+    const int v = atoi(env);
+    if (v >= 1 && v < cap) cap = v;
+  }
+  int max_groups = cap / hg;
+  if (max_groups < 1) max_groups = 1;
+  if (per_cu > max_groups) per_cu = max_groups;
   return cus * per_cu;
 }
 
@@ -838,9 +904,11 @@ int device_info(DeviceInfo& out) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       return fail(RPA_E_HIP, "hipDeviceGetAttribute(MultiprocessorCount) failed");
-    d.grid[KV_BF16] = occupancy_grid<KV_BF16>(cus);
-    d.grid[KV_BF16_SCALED] = occupancy_grid<KV_BF16_SCALED>(cus);
-    d.grid[KV_FP8] = occupancy_grid<KV_FP8>(cus);
+    for (int hg = 1; hg <= 8; ++hg) {
+      d.grid[KV_BF16][hg] = occupancy_grid<KV_BF16>(cus, hg);
+      d.grid[KV_BF16_SCALED][hg] = occupancy_grid<KV_BF16_SCALED>(cus, hg);
+      d.grid[KV_FP8][hg] = occupancy_grid<KV_FP8>(cus, hg);
+    }
     d.cus = cus;
   }
   out = d;
@@ -898,6 +966,8 @@ Params base_params(const rpa_shape_t* s) {
   if ((s->page_size & (s->page_size - 1)) == 0) p.log2S = __builtin_ctz((unsigned)s->page_size);
   p.Nmax = s->max_num_seqs;
   p.PPS = s->pages_per_seq;
+  p.HG = heads_per_group(p.Hkv);
+  p.NG = p.Hkv / p.HG;
   return p;
 }
 
@@ -991,21 +1061,21 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (kv_scales) return fail(RPA_E_INVALID, "kv_scales is only used with fp8 kv_pages");
     if (opt->has_k_scale || opt->has_v_scale) mode = KV_BF16_SCALED;
   }
-  p.grid = d.grid[mode];
+  p.grid = d.grid[mode][p.HG];
   hipStream_t st = (hipStream_t)stream;
   if (ev_begin && hipEventRecord((hipEvent_t)ev_begin, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");
   if (mode == KV_FP8)
-    hipLaunchKernelGGL(rpa_attn_kernel<KV_FP8>, dim3(p.grid), dim3(64), 0, st, p);
+    hipLaunchKernelGGL(rpa_attn_kernel<KV_FP8>, dim3(p.grid), dim3(64 * p.HG), p.HG * kVtBytes, st, p);
   else if (mode == KV_BF16_SCALED)
-    hipLaunchKernelGGL(rpa_attn_kernel<KV_BF16_SCALED>, dim3(p.grid), dim3(64), 0, st, p);
+    hipLaunchKernelGGL(rpa_attn_kernel<KV_BF16_SCALED>, dim3(p.grid), dim3(64 * p.HG), p.HG * kVtBytes, st, p);
   else
-    hipLaunchKernelGGL(rpa_attn_kernel<KV_BF16>, dim3(p.grid), dim3(64), 0, st, p);
+    hipLaunchKernelGGL(rpa_attn_kernel<KV_BF16>, dim3(p.grid), dim3(64 * p.HG), p.HG * kVtBytes, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("attention launch failed: ") + hipGetErrorString(e));
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(end) failed");
-  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid * p.HG), dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
   return RPA_OK;
