@@ -322,8 +322,17 @@ struct Pages {
 // end of the range, nch == 0) read clamped, always-valid addresses -- key kv_len-1, or row 0 --
 // whose values the -inf scores then exclude.  Straight-line loads let the compiler count
 // outstanding loads exactly (s_waitcnt vmcnt(N)) so the next unit's loads stay in flight.
+// UPG: page_size is a multiple of KV_CHUNK, so a chunk lies in one page and its page id is
+// wave-uniform: one scalar load instead of two vector loads per lane.
+template <bool UPG>
 __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, int n) {
   Pages r;
+  if constexpr (UPG) {
+    const size_t idx = x.nch > 0 ? (size_t)x.i * p.PPS + page_of(x.c * KV_CHUNK, p) : 0;
+    const int pg = uni(p.page_indices[idx]);
+    r.pg[0] = r.pg[1] = pg;
+    return r;
+  }
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
   const size_t row = live ? (size_t)x.i * p.PPS : 0;
@@ -620,7 +629,7 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
   }
 }
 
-template <int MODE>
+template <int MODE, bool UPG>
 __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n, int j, int b, long long u,
                                      long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
                                      Pages& pg_nxt, const HalfRegs<MODE>& k_cur, const HalfRegs<MODE>& v_cur,
@@ -634,7 +643,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
     advance(p, nseq, lane, win, ahead, err);
   else
     ahead.nch = 0;
-  const Pages pg_ahead = load_pages(p, ahead, n);
+  const Pages pg_ahead = load_pages<UPG>(p, ahead, n);
   const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, wv, err);
   load_half<MODE>(p, nx_addr, 0, k_nxt);
 
@@ -663,7 +672,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   nxt = ahead;
 }
 
-template <int MODE>
+template <int MODE, bool UPG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x transposed V chunk
   const int lane = threadIdx.x & 63;
@@ -684,24 +693,40 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       o[k] = u32x4{0u, 0u, 0u, 0u};
   }
 
-  const long long W = total_units(p, nseq, lane, err);
+  // Schedule: total work W, this workgroup's range [u0, u1), the sequence holding u0 and a
+  // window of per-lane sequence metadata.  Up to 64 sequences take a single metadata load.
+  Window win;
+  load_window(p, nseq, 0, lane, win, err);
+  long long W;
+  if (nseq <= 64) {
+    W = wave_sum64((long long)win.s.units * p.NG);
+  } else {
+    W = total_units(p, nseq, lane, err);
+  }
   const Partition pt = make_partition(W, p.grid);
   const long long u0 = uni64(range_start(b, pt)), u1 = uni64(range_start(b + 1, pt));
   if (W > 0 && u0 < u1) {
     int seq;
     long long seq_start;
-    locate_seq(p, nseq, lane, u0, seq, seq_start, err);
-    if (seq < nseq) {
-      Window win;
+    if (nseq <= 64) {
+      const long long cnt = (long long)win.s.units * p.NG;
+      const long long incl = wave_incl_scan64(cnt, lane);
+      const int idx = __popcll(__ballot(incl <= u0));
+      seq = uni(idx);
+      seq_start = uni64(rl64(incl - cnt, idx));
+    } else {
+      locate_seq(p, nseq, lane, u0, seq, seq_start, err);
       load_window(p, nseq, seq, lane, win, err);
+    }
+    if (seq < nseq) {
       Cursor cur = cursor_at(p, win, seq, u0 - seq_start);
       Cursor nxt = cur;
       if (u0 + 1 < u1)
         advance(p, nseq, lane, win, nxt, err);
       else
         nxt.nch = 0;
-      const Pages pg_cur = load_pages(p, cur, n);
-      Pages pg_nxt = load_pages(p, nxt, n);
+      const Pages pg_cur = load_pages<UPG>(p, cur, n);
+      Pages pg_nxt = load_pages<UPG>(p, nxt, n);
       HalfRegs<MODE> ka, va, kb, vb;
       bf16x8 q[4];
       {
@@ -714,9 +739,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
       long long u = u0;
       for (;;) {
-        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt, wv);
+        step<MODE, UPG>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt, wv);
         if (++u >= u1) break;
-        step<MODE>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt, wv);
+        step<MODE, UPG>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt, wv);
         if (++u >= u1) break;
       }
     }
@@ -880,7 +905,7 @@ constexpr int kVtBytes = kD * kVTRow;
 template <int MODE>
 int occupancy_grid(int cus, int hg) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE>, 64 * hg, hg * kVtBytes) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE, false>, 64 * hg, hg * kVtBytes) !=
           hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
@@ -1065,12 +1090,19 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   hipStream_t st = (hipStream_t)stream;
   if (ev_begin && hipEventRecord((hipEvent_t)ev_begin, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");
-  if (mode == KV_FP8)
-    hipLaunchKernelGGL(rpa_attn_kernel<KV_FP8>, dim3(p.grid), dim3(64 * p.HG), p.HG * kVtBytes, st, p);
-  else if (mode == KV_BF16_SCALED)
-    hipLaunchKernelGGL(rpa_attn_kernel<KV_BF16_SCALED>, dim3(p.grid), dim3(64 * p.HG), p.HG * kVtBytes, st, p);
-  else
-    hipLaunchKernelGGL(rpa_attn_kernel<KV_BF16>, dim3(p.grid), dim3(64 * p.HG), p.HG * kVtBytes, st, p);
+  const bool upg = p.S % KV_CHUNK == 0;
+  const dim3 grid(p.grid), block(64 * p.HG);
+  const size_t lds = (size_t)p.HG * kVtBytes;
+  if (mode == KV_FP8) {
+    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true>), grid, block, lds, st, p);
+    else hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, false>), grid, block, lds, st, p);
+  } else if (mode == KV_BF16_SCALED) {
+    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true>), grid, block, lds, st, p);
+    else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, false>), grid, block, lds, st, p);
+  } else {
+    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true>), grid, block, lds, st, p);
+    else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, false>), grid, block, lds, st, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("attention launch failed: ") + hipGetErrorString(e));
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess)
