@@ -77,6 +77,23 @@ def cpu_baseline(case, budget_s: float = 20.0) -> dict:
     }
 
 
+def measured_traffic(cfg: str):
+    """HBM bytes per attention-kernel dispatch from the committed rocprofv3 PMC summary
+    (profiles/pmc_traffic.json: FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's
+    reading for a 1 GiB copy), used only if it was measured on the current kernel sources."""
+    import hashlib
+
+    path = ROOT / "profiles" / "pmc_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    csrc = ROOT / "tpu-cake_amd" / "csrc"
+    digest = hashlib.sha256(b"".join((csrc / f).read_bytes() for f in ("rpa_kernels.hip", "rpa_schedule.h")))
+    if digest.hexdigest()[:16] != data.get("source_sha256_16") or cfg not in data.get("configs", {}):
+        return None
+    return data["configs"][cfg]["traffic_bytes"]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,6 +212,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved_bw, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved_bw / HBM_PEAK_GBPS, 4), "traffic": None},
     }
+    traffic = measured_traffic(args.config)
+    if traffic is not None:
+        result["roofline"]["traffic"] = traffic
     if flops and args.config == "c3":
         result["prefill_mfma"] = {"flops": flops, "achieved_tflops_over_attn_kernel": round(roof_flops, 2),
                                   "peak_tflops": BF16_PEAK_TFLOPS}
