@@ -150,6 +150,15 @@ __device__ __forceinline__ float rows4_sum(float v) {
   return __builtin_bit_cast(float, (unsigned)c[0]) + __builtin_bit_cast(float, (unsigned)c[1]);
 }
 
+// Orders this wave's accesses to its private LDS tile across lanes.  A wave's LDS instructions
+// execute in issue order, so keeping the compiler from moving LDS accesses across this point
+// (wavefront-scope fences; no instruction is emitted) is all that is needed.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -490,7 +499,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   load_q(p, nx, n, j, wv, q);
 
   // V^T into LDS: key t = 16*blk + n goes to slot pos = 8*(n/4) + 4*blk + n%4 of each dim row
-  __syncthreads();
+  wave_lds_fence();
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     const int slot_b = 2 * (8 * (n >> 2) + 4 * blk + (n & 3));
@@ -576,7 +585,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
   const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
 
-  __syncthreads();
+  wave_lds_fence();
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
     bf16x8 a = *(const bf16x8*)(vt + (16 * d + n) * kVTRow + 16 * j);
@@ -645,6 +654,9 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
     ahead.nch = 0;
   const Pages pg_ahead = load_pages<UPG>(p, ahead, n);
   const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, wv, err);
+  // keep the workgroup's waves (the kv heads of one group) in step, so the heads' slices of the
+  // same keys reach the memory system together
+  __syncthreads();
   load_half<MODE>(p, nx_addr, 0, k_nxt);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
