@@ -9,7 +9,8 @@ from HBM (the 256 MB Infinity Cache never holds the next call's pages).
 
 value      = algorithmic KV bytes per step / measured step time (SI GB/s)
 roofline   = (KV + Q + O bytes) / average duration of the attention kernel,
-             timed with HIP events recorded around that kernel alone, against
+             timed with HIP events recorded around that kernel alone in every
+             timed step (timing-only events: no system-scope fence), against
              MI355X's 8 TB/s HBM peak (or the bf16 MFMA peak for prefill rows)
 cpu_baseline = the numpy oracle (oracle/rpa_oracle.py) on a bounded sample of
              the same configuration, 1 thread, on this host.
@@ -118,6 +119,7 @@ def main() -> int:
     import torch
 
     from tpu_cake_amd import ops
+    from tpu_cake_amd.timing import KernelEvent
     from tpu_cake_amd.workloads import CONFIG_DESCRIPTIONS, make_config
 
     if not torch.cuda.is_available():
@@ -161,10 +163,8 @@ def main() -> int:
     for i in range(args.warmup):
         call(i)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    for a, b in evs:  # create the HIP events before they are handed to the library
-        a.record()
-        b.record()
+    # timing-only HIP events (no system-scope fence at record) around the attention kernel
+    evs = [(KernelEvent(), KernelEvent()) for _ in range(args.steps)]
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()

@@ -4,8 +4,10 @@
 //   * the balanced partition covers units [0, W) exactly once, ranges contiguous, sizes q or q+1;
 //   * owner_of(u) is the workgroup whose range holds u;
 //   * every row block split across workgroups has exactly one describer (the owner of its last
-//     unit), its contributors are the consecutive workgroups owner(first)..owner(last), and the
-//     partial slots they write (2*b0+1, then 2*b) are distinct across the whole call;
+//     unit, so no two split row blocks share a descriptor), its contributors are the consecutive
+//     workgroups owner(first)..owner(last), each workgroup contributes to at most one split row
+//     block that began before its range and one that runs past its end, and the partial slots
+//     they write (2*b0+1, then 2*b) are distinct across the whole call;
 //   * a row block's units visit keys up to the causal limit of its last row and no further.
 // Prints "OK <cases>" or the first violation.
 #include <cstdio>
@@ -82,7 +84,8 @@ int main() {
         if (owner_of(u, pt) != owner[u]) return fail("owner_of", owner_of(u, pt), owner[u]);
       }
       // split row blocks: describer, contributors, slots
-      std::set<long long> slots;
+      std::set<long long> slots, counters;  // counters: descriptor indices
+      std::vector<int> heads(grid, 0), tails(grid, 0);
       long long start = 0;
       while (start < W) {
         const Unit& f = units[start];
@@ -94,7 +97,9 @@ int main() {
         if (b0 != b1) {
           // the kernel's view: b0 processes c == 0 (started_here) and runs past its range end;
           // every later contributor starts inside the block; b1 ends it and describes it.
+          if (!counters.insert(b1).second) return fail("descriptor reused", b1, b0);
           for (long long b = b0; b <= b1; ++b) {
+            if (++(b == b0 ? tails : heads)[b] > 1) return fail("two pieces of one kind", b, b0);
             const long long u0 = range_start(b, pt), u1 = range_start(b + 1, pt);
             if (u1 <= u0) return fail("empty workgroup inside a split row block", b, 0);
             const bool started_here = u0 <= start;

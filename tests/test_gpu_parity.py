@@ -244,3 +244,34 @@ def test_full_config_parity(cuda, cfg):
         err = orc.errors(out[: src.shape[0]], src)
         print(f"  vs bf16 source: max_abs={err['max_abs']:.3e}")
         assert err["max_abs"] <= TOL_FP8_VS_SOURCE
+
+
+def test_split_partials_follow_inputs(cuda):
+    """Back-to-back calls over identical shapes (same partition, same partial slots) but different
+    values: every output matches its own oracle, so no call reads another call's split-K partials,
+    and no error bit is left."""
+    _say("split-K partials across back-to-back calls")
+    lens = [3000, 2500, 1800, 4000, 700, 2200, 3500, 1200] * 4
+    cases = [make_custom(kv_lens=lens, q_lens=[1] * len(lens), num_q_heads=32, num_kv_heads=8, page_size=64,
+                         seed=s) for s in (61, 62)]
+    refs = [orc.bf16_round(_oracle(c)) for c in cases]
+    devs = [ops.case_to_device(c, "cuda") for c in cases]
+    for rep in range(3):
+        for c, d, ref in zip(cases, devs, refs):
+            out = ops.ragged_paged_attention(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
+                                             d["num_seqs"], sm_scale=c.sm_scale)
+            got = out.float().cpu().numpy()[: ref.shape[0]]
+            err = orc.errors(got, ref)
+            assert err["max_abs"] <= TOL_BF16, (rep, err)
+    assert ops.read_error_word() == 0
+
+
+@pytest.mark.parametrize("nseq,nmax", [(65, 80), (200, 256), (300, 320)])
+def test_many_sequences(cuda, nseq, nmax):
+    """Sequence counts across the one-round-trip metadata windows (64 each, four at once) and
+    past them, with padded max_num_seqs."""
+    _say(f"many sequences {nseq} (max {nmax})")
+    rng = np.random.default_rng(nseq)
+    lens = rng.integers(1, 700, nseq).tolist()
+    _check(make_custom(kv_lens=lens, q_lens=[1] * nseq, num_q_heads=16, num_kv_heads=4, page_size=32,
+                       seed=nseq, max_num_seqs=nmax, num_tokens=nseq + 5))

@@ -16,8 +16,8 @@
 //                       split across workgroups leaves one partial (m, l, acc) per workgroup,
 //                       and the workgroup owning its last unit leaves a descriptor of it.
 //   rpa_combine_kernel  one 4-wave workgroup per descriptor: log-sum-exp merge of the row
-//                       block's partials (the waves take every 4th contributor, then merge
-//                       through LDS), writes the rows, clears the descriptor.
+//                       block's partials (the waves take every 4th contributor, four at a
+//                       time, then merge through LDS), writes the rows, clears the descriptor.
 //
 // MFMA operand layouts (16x16x32 bf16, wave64): A[i][k] and B[k][j] place row i / column j
 // at lane%16 and the 32 k-slots at (lane/16, element 0..7); D[i][j] sits at lane
@@ -189,12 +189,10 @@ struct SeqInfo {
   int kv_len, q_start, q_len, units;  // units: per kv head
 };
 
-__device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, int& err) {
+// Sequence metadata from raw kv_lens[i], cu_q_lens[i], cu_q_lens[i + 1] (valid = i < num_seqs).
+__device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int c1, bool valid, int& err) {
   SeqInfo s{0, 0, 0, 0};
-  if (i < nseq) {
-    int kv = p.kv_lens[i];
-    int c0 = p.cu_q_lens[i];
-    int c1 = p.cu_q_lens[i + 1];
+  if (valid) {
     long long cap = (long long)p.PPS * p.S;
     if (kv > cap) { kv = (int)cap; err |= ERR_KVLEN; }
     if (kv < 0) kv = 0;
@@ -207,6 +205,19 @@ __device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, in
     s.units = seq_units_per_head(kv, ql, p.G, p.skip_masked);
   }
   return s;
+}
+
+// Field-wise conditional copy (value selects keep the windows in registers).
+__device__ __forceinline__ void select_seq(SeqInfo& d, const SeqInfo& s, bool c) {
+  d.kv_len = c ? s.kv_len : d.kv_len;
+  d.q_start = c ? s.q_start : d.q_start;
+  d.q_len = c ? s.q_len : d.q_len;
+  d.units = c ? s.units : d.units;
+}
+
+__device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, int& err) {
+  if (i >= nseq) return SeqInfo{0, 0, 0, 0};
+  return make_seq(p, p.kv_lens[i], p.cu_q_lens[i], p.cu_q_lens[i + 1], true, err);
 }
 
 __device__ __forceinline__ long long total_units(const Params& p, int nseq, int lane, int& err) {
@@ -692,26 +703,47 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint8_t* vt = smem + wv * (kD * kVTRow);
   const int n = lane & 15, j = lane >> 4;
   const int b = blockIdx.x;
-  int nseq = uni(p.num_seqs[0]);
-  nseq = nseq < 0 ? 0 : (nseq > p.Nmax ? p.Nmax : nseq);
   int err = 0;
 
-  {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
-    int tv = uni(p.cu_q_lens[nseq]);
-    tv = tv < 0 ? 0 : (tv > p.T ? p.T : tv);
-    const size_t first = (size_t)tv * p.Hq * kD / 8, last = (size_t)p.T * p.Hq * kD / 8;
-    u32x4* o = (u32x4*)p.out;
-    for (size_t k = first + (size_t)b * blockDim.x + threadIdx.x; k < last; k += (size_t)p.grid * blockDim.x)
-      o[k] = u32x4{0u, 0u, 0u, 0u};
-  }
-
   // Schedule: total work W, this workgroup's range [u0, u1), the sequence holding u0 and a
-  // window of per-lane sequence metadata.  Up to 64 sequences take a single metadata load.
+  // window of per-lane sequence metadata.  num_seqs and the metadata of the first 256 sequences
+  // (four 64-sequence windows) are fetched in one round trip; lanes past max_num_seqs load
+  // nothing.  More sequences than that take one further round trip per window.
+  constexpr int kWin = 4;
   Window win;
-  load_window(p, nseq, 0, lane, win, err);
-  long long W;
-  if (nseq <= 64) {
-    W = wave_sum64((long long)win.s.units * p.NG);
+  SeqInfo wsi[kWin];
+  int nseq, tv;
+  {
+    int kv[kWin], c0[kWin], c1[kWin];
+    const int ns_raw = p.num_seqs[0];
+#pragma unroll
+    for (int w = 0; w < kWin; ++w) {
+      kv[w] = c0[w] = c1[w] = 0;
+      const int i = 64 * w + lane;
+      if (i < p.Nmax) {
+        kv[w] = p.kv_lens[i];
+        c0[w] = p.cu_q_lens[i];
+        c1[w] = p.cu_q_lens[i + 1];
+      }
+    }
+    nseq = uni(ns_raw);
+    nseq = nseq < 0 ? 0 : (nseq > p.Nmax ? p.Nmax : nseq);
+    // cu_q_lens[num_seqs]: rows from here on belong to no sequence
+    tv = rl(c0[0], 0);
+#pragma unroll
+    for (int w = 0; w < kWin; ++w)
+      if (nseq > 64 * w && nseq <= 64 * (w + 1)) tv = rl(c1[w], nseq - 1 - 64 * w);
+    if (nseq > 64 * kWin) tv = uni(p.cu_q_lens[nseq]);
+#pragma unroll
+    for (int w = 0; w < kWin; ++w) wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, err);
+  }
+  long long W = 0, tile[kWin];
+  if (nseq <= 64 * kWin) {
+#pragma unroll
+    for (int w = 0; w < kWin; ++w) {
+      tile[w] = wave_sum64((long long)wsi[w].units * p.NG);
+      W += tile[w];
+    }
   } else {
     W = total_units(p, nseq, lane, err);
   }
@@ -720,12 +752,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (W > 0 && u0 < u1) {
     int seq;
     long long seq_start;
-    if (nseq <= 64) {
-      const long long cnt = (long long)win.s.units * p.NG;
-      const long long incl = wave_incl_scan64(cnt, lane);
-      const int idx = __popcll(__ballot(incl <= u0));
-      seq = uni(idx);
-      seq_start = uni64(rl64(incl - cnt, idx));
+    if (nseq <= 64 * kWin) {
+      // the window holding u0 (u0 < W, so one does), then the sequence inside it
+      int wsel = -1;
+      long long off = 0, off_sel = 0;
+#pragma unroll
+      for (int w = 0; w < kWin; ++w) {
+        if (wsel < 0 && u0 < off + tile[w]) {
+          wsel = w;
+          off_sel = off;
+        }
+        off += tile[w];
+      }
+      if (wsel < 0) {  // not reached: u0 < W
+        seq = nseq;
+        seq_start = W;
+      } else {
+        win.base = 64 * wsel;
+        win.s = wsi[0];
+#pragma unroll
+        for (int w = 1; w < kWin; ++w) select_seq(win.s, wsi[w], wsel == w);
+        const long long cnt = (long long)win.s.units * p.NG;
+        const long long incl = wave_incl_scan64(cnt, lane);
+        const int idx = __popcll(__ballot(off_sel + incl <= u0));
+        seq = uni(win.base + idx);
+        seq_start = uni64(off_sel + rl64(incl - cnt, idx));
+      }
     } else {
       locate_seq(p, nseq, lane, u0, seq, seq_start, err);
       load_window(p, nseq, seq, lane, win, err);
@@ -757,6 +809,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (++u >= u1) break;
       }
     }
+  }
+
+  {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
+    tv = tv < 0 ? 0 : (tv > p.T ? p.T : tv);
+    const size_t first = (size_t)tv * p.Hq * kD / 8, last = (size_t)p.T * p.Hq * kD / 8;
+    u32x4* o = (u32x4*)p.out;
+    for (size_t k = first + (size_t)b * blockDim.x + threadIdx.x; k < last; k += (size_t)p.grid * blockDim.x)
+      o[k] = u32x4{0u, 0u, 0u, 0u};
   }
   if (err) atomicOr(p.err, err);
 }

@@ -155,7 +155,8 @@ def ragged_paged_attention(
     vmem_limit_bytes: int | None = None,
     kv_scales: torch.Tensor | None = None,   # f32 [pages, Hkv, 2] per-(page, kv head) K/V scales
     out: torch.Tensor | None = None,
-    kernel_events: tuple | None = None,      # (begin, end) torch.cuda.Event around the attention kernel
+    kernel_events: tuple | None = None,      # (begin, end) events around the attention kernel: torch.cuda.Event
+                                             # or timing.KernelEvent (anything with a .cuda_event handle)
 ) -> torch.Tensor:
     """Ragged paged attention (mixed prefill and decode) on MI355X.
 
