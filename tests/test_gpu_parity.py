@@ -275,3 +275,38 @@ def test_many_sequences(cuda, nseq, nmax):
     lens = rng.integers(1, 700, nseq).tolist()
     _check(make_custom(kv_lens=lens, q_lens=[1] * nseq, num_q_heads=16, num_kv_heads=4, page_size=32,
                        seed=nseq, max_num_seqs=nmax, num_tokens=nseq + 5))
+
+
+# Prefill tiles (bf16 KV, eight kv heads per workgroup, sequences with >= 16 query tokens): tile
+# shapes over the GQA group sizes, prior lengths, page sizes and ragged tile tails, next to decode
+# rows that keep the stream-K path.
+@pytest.mark.parametrize("hq,q_lens,kv_lens,page", [
+    (32, [512, 1, 300, 1], [1536, 900, 300, 77], 64),     # G=4: 64-token tiles, prior 1024 / none
+    (64, [100, 1, 17], [100, 4000, 50], 16),              # G=8: 32-token tiles, q_len == kv_len
+    (8, [300, 2], [337, 2], 24),                          # G=1: 256-token tiles, page not a power of two
+    (128, [40, 1], [1040, 8], 32),                        # G=16: 16-token tiles
+    (32, [16, 1, 1000], [16, 600, 1000], 64),             # shortest prefill, long self-attention
+])
+def test_prefill_tiles(cuda, hq, q_lens, kv_lens, page):
+    _say(f"prefill tiles hq={hq} q_lens={q_lens} kv_lens={kv_lens} page={page}")
+    _check(make_custom(kv_lens=kv_lens, q_lens=q_lens, num_q_heads=hq, num_kv_heads=8, page_size=page,
+                       seed=sum(q_lens) + hq))
+
+
+def test_prefill_tiles_window_and_soft_cap(cuda):
+    _say("prefill tiles with sliding window and soft cap")
+    case = make_custom(kv_lens=[900, 300, 50], q_lens=[200, 300, 1], num_q_heads=32, num_kv_heads=8, page_size=64,
+                       seed=71)
+    _check(case, gpu_kw=dict(sliding_window=100, soft_cap=30.0), oracle_kw=dict(sliding_window=100, soft_cap=30.0))
+
+
+def test_prefill_tiles_match_stream_k(cuda, monkeypatch):
+    """The same batch with prefill tiles switched off (RPA_NO_PREFILL_TILES, read per call)
+    agrees with the tiled result to the bf16 output tolerance."""
+    _say("prefill tiles vs stream-K only")
+    case = make_custom(kv_lens=[1200, 700, 64], q_lens=[256, 1, 64], num_q_heads=32, num_kv_heads=8, page_size=64,
+                       seed=73)
+    tiled = _gpu_out(case)
+    monkeypatch.setenv("RPA_NO_PREFILL_TILES", "1")
+    plain = _gpu_out(case)
+    assert orc.errors(tiled, plain)["max_abs"] <= TOL_BF16

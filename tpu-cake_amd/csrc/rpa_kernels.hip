@@ -93,6 +93,9 @@ struct Params {
   float k_scale, v_scale;
   int grid;
   bool skip_masked;  // mask value so negative that masked keys get weight exactly 0
+  int pf_tq;         // tokens per prefill tile (0 = prefill tiles off)
+  int pf_min;        // sequences with at least this many query tokens take prefill tiles
+  float pf_cost;     // cost of one prefill tile chunk in stream-K units (work split model)
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -190,7 +193,10 @@ struct SeqInfo {
 };
 
 // Sequence metadata from raw kv_lens[i], cu_q_lens[i], cu_q_lens[i + 1] (valid = i < num_seqs).
-__device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int c1, bool valid, int& err) {
+// A sequence with at least pf_min query tokens (pf_min > 0) belongs to the prefill tiles and
+// contributes no stream-K units.
+__device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int c1, bool valid, int pf_min,
+                                            int& err) {
   SeqInfo s{0, 0, 0, 0};
   if (valid) {
     long long cap = (long long)p.PPS * p.S;
@@ -202,7 +208,7 @@ __device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int
     s.kv_len = kv;
     s.q_start = c0;
     s.q_len = ql;
-    s.units = seq_units_per_head(kv, ql, p.G, p.skip_masked);
+    s.units = (pf_min > 0 && ql >= pf_min) ? 0 : seq_units_per_head(kv, ql, p.G, p.skip_masked);
   }
   return s;
 }
@@ -215,15 +221,15 @@ __device__ __forceinline__ void select_seq(SeqInfo& d, const SeqInfo& s, bool c)
   d.units = c ? s.units : d.units;
 }
 
-__device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, int& err) {
+__device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, int pf_min, int& err) {
   if (i >= nseq) return SeqInfo{0, 0, 0, 0};
-  return make_seq(p, p.kv_lens[i], p.cu_q_lens[i], p.cu_q_lens[i + 1], true, err);
+  return make_seq(p, p.kv_lens[i], p.cu_q_lens[i], p.cu_q_lens[i + 1], true, pf_min, err);
 }
 
 __device__ __forceinline__ long long total_units(const Params& p, int nseq, int lane, int& err) {
   long long w = 0;
   for (int base = 0; base < nseq; base += 64) {
-    SeqInfo s = load_seq(p, base + lane, nseq, err);
+    SeqInfo s = load_seq(p, base + lane, nseq, 0, err);
     w += wave_sum64((long long)s.units * p.NG);
   }
   return w;
@@ -234,7 +240,7 @@ __device__ __forceinline__ void locate_seq(const Params& p, int nseq, int lane, 
                                            long long& seq_start, int& err) {
   long long off = 0;
   for (int base = 0; base < nseq; base += 64) {
-    SeqInfo s = load_seq(p, base + lane, nseq, err);
+    SeqInfo s = load_seq(p, base + lane, nseq, 0, err);
     long long cnt = (long long)s.units * p.NG;
     long long incl = wave_incl_scan64(cnt, lane);
     long long tile = rl64(incl, 63);
@@ -251,15 +257,16 @@ __device__ __forceinline__ void locate_seq(const Params& p, int nseq, int lane, 
   seq_start = off;
 }
 
-// Per-lane metadata of sequences [base, base + 64).
+// Per-lane metadata of sequences [base, base + 64); pf_min as in make_seq.
 struct Window {
   int base;
+  int pf_min;
   SeqInfo s;
 };
 
 __device__ __forceinline__ void load_window(const Params& p, int nseq, int base, int lane, Window& w, int& err) {
   w.base = base;
-  w.s = load_seq(p, base + lane, nseq, err);
+  w.s = load_seq(p, base + lane, nseq, w.pf_min, err);
 }
 
 struct Cursor {
@@ -695,6 +702,347 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   nxt = ahead;
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// prefill tiles (sequences with many query tokens)
+// ---------------------------------------------------------------------------------------------
+// A tile is (sequence, kv head h, pf_tq consecutive query tokens): rows r = token*G + g (q head
+// h*G + g) over the 32*HG rows of a workgroup, wave w owning rows 32w .. 32w+31 as two 16-row
+// MFMA blocks.  Each 32-key chunk of kv head h is fetched from HBM once per tile by the whole
+// workgroup (a four-deep register ring, three chunks ahead) into double-buffered LDS: K as key
+// rows with a 272-byte stride (the 16 keys of an A fragment land in distinct banks), V
+// transposed as in compute_unit.  Every wave reads its A fragments from LDS and uses each for
+// both of its row blocks; softmax as in compute_unit.  Tiles come from a queue (an atomic
+// counter in the workspace header, reset by the combine kernel), the last tile of each
+// sequence first.
+constexpr int kPfKRow = kD * 2 + 16;
+constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
+constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
+constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
+constexpr float kPfCost = 0.15f;  // time of a prefill tile chunk / time of a stream-K unit
+
+template <int NP>  // 16-byte pieces of K (and of V) per thread per chunk: 512 / threads
+struct PfRegs {
+  u32x4 k[NP], v[NP];
+};
+
+struct PfPages {
+  int pg[2];  // page ids of this thread's keys (pieces 0 and 1) for one chunk
+};
+
+struct PfTile {
+  int seq, h;
+  int kv_len, q_len, q_start;
+  int tok0, ntok;  // first token (sequence-relative) and tokens of the tile
+  int c_lo, c_hi;  // chunks visited
+};
+
+// Prefill-tile count of a sequence per kv head (0 if it is not a prefill sequence).
+__device__ __forceinline__ int pf_tiles_of(const Params& p, const SeqInfo& si, int pf_min) {
+  if (pf_min <= 0 || si.q_len < pf_min || si.kv_len <= 0) return 0;
+  return (si.q_len + p.pf_tq - 1) / p.pf_tq;
+}
+
+// Page id of key kt of sequence seq (range-checked).
+__device__ __forceinline__ int pf_page(const Params& p, int seq, int kt, int& err) {
+  int pg = p.page_indices[(size_t)seq * p.PPS + page_of(kt, p)];
+  if (pg < 0 || pg >= p.P) {
+    err |= ERR_PAGE;
+    pg = 0;
+  }
+  return pg;
+}
+
+template <int NP>
+__device__ __forceinline__ int pf_key_of(int tid, int i, int nthreads) {
+  return (tid + i * nthreads) >> 4;
+}
+
+template <int NP>
+__device__ __forceinline__ PfPages pf_load_pages(const Params& p, const PfTile& tl, int c, int tid, int nthreads,
+                                                 int& err) {
+  PfPages r;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    int kt = c * KV_CHUNK + pf_key_of<NP>(tid, i, nthreads);
+    kt = kt < tl.kv_len ? kt : tl.kv_len - 1;
+    r.pg[i] = pf_page(p, tl.seq, kt, err);
+  }
+  return r;
+}
+
+template <int NP>
+__device__ __forceinline__ void pf_load_chunk(const Params& p, const PfTile& tl, int c, const PfPages& pg, int tid,
+                                              int nthreads, PfRegs<NP>& r) {
+  const uint16_t* kv = (const uint16_t*)p.kv;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int q = tid + i * nthreads;
+    int kt = c * KV_CHUNK + (q >> 4);
+    kt = kt < tl.kv_len ? kt : tl.kv_len - 1;
+    const size_t e = kv_elem(p, pg.pg[i], kt, 2 * tl.h) + 8 * (q & 15);
+    r.k[i] = *(const u32x4*)(kv + e);
+    r.v[i] = *(const u32x4*)(kv + e + kD);
+  }
+}
+
+template <int NP>
+__device__ __forceinline__ void pf_store_chunk(uint8_t* buf, const PfRegs<NP>& r, int tid, int nthreads) {
+  uint8_t* vt = buf + kPfKBytes;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int q = tid + i * nthreads, key = q >> 4, pc = q & 15;
+    *(u32x4*)(buf + key * kPfKRow + pc * 16) = r.k[i];
+    const int slot_b = 2 * (8 * ((key & 15) >> 2) + 4 * (key >> 4) + (key & 3));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t w = r.v[i][t];
+      const int d = 8 * pc + 2 * t;
+      *(uint16_t*)(vt + d * kVTRow + slot_b) = (uint16_t)(w & 0xffffu);
+      *(uint16_t*)(vt + (d + 1) * kVTRow + slot_b) = (uint16_t)(w >> 16);
+    }
+  }
+}
+
+struct PfRow {
+  f32x4 acc[8];
+  float m, l;
+  int pos;   // last visible key of this lane's row
+  bool ok;   // the row exists (token in the tile, pos >= 0)
+};
+
+// One chunk for one 16-row block: scores sc[kb] (keys 16kb + 4j + rr of row n), softmax update,
+// P^T packed for the PV MFMA.
+__device__ __forceinline__ bf16x8 pf_softmax(const Params& p, const PfTile& tl, int c, bool plain, const f32x4 sc[2],
+                                             PfRow& st, int j) {
+  float xs[2][4];
+  if (plain) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      xs[0][rr] = sc[0][rr] * p.scale_log2;
+      xs[1][rr] = sc[1][rr] * p.scale_log2;
+    }
+  } else {
+    const int key0 = c * KV_CHUNK + 4 * j;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float sv = sc[kb][rr];
+        float xv;
+        if (p.soft_cap > 0.f) {
+          const float t = sv * p.sm_scale;
+          xv = p.soft_cap * tanhf(t / p.soft_cap) * kLog2e;
+        } else {
+          xv = sv * p.scale_log2;
+        }
+        const int kt = key0 + 16 * kb + rr;
+        const bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
+        if (masked) xv += p.mask_log2;
+        if (kt >= tl.kv_len) xv = -INFINITY;
+        xs[kb][rr] = xv;
+      }
+  }
+  float mc = fmaxf(fmaxf(fmaxf(xs[0][0], xs[0][1]), fmaxf(xs[0][2], xs[0][3])),
+                   fmaxf(fmaxf(xs[1][0], xs[1][1]), fmaxf(xs[1][2], xs[1][3])));
+  mc = rows4_max(mc);
+  const bool grow = mc > st.m + kRescaleLog2;
+  if (__ballot(grow)) {
+    const float mn = grow ? mc : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
+    st.l *= alpha;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+    st.m = mn;
+  }
+  const float mu = st.m == -INFINITY ? 0.f : st.m;
+  float pr[2][4];
+  float lsum = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      pr[kb][rr] = __builtin_amdgcn_exp2f(xs[kb][rr] - mu);
+      lsum += pr[kb][rr];
+    }
+  st.l += lsum;
+  u32x4 pw;
+  pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
+  pw[1] = pack_bf16x2(pr[0][2], pr[0][3]);
+  pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
+  pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
+  return __builtin_bit_cast(bf16x8, pw);
+}
+
+// One chunk from LDS buffer buf for the wave's two row blocks.
+__device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, int c, const uint8_t* buf,
+                                           const bf16x8 q[2][4], PfRow st[2], int n, int j) {
+  f32x4 sc[2][2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) sc[rb][0] = sc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const bf16x8 a = *(const bf16x8*)(buf + (16 * kb + n) * kPfKRow + (32 * s + 8 * j) * 2);
+      sc[0][kb] = mfma(a, q[0][s], sc[0][kb]);
+      sc[1][kb] = mfma(a, q[1][s], sc[1][kb]);
+    }
+  // every row of the tile sees this chunk in full: no per-score masking
+  const int pos_min = tl.kv_len - tl.q_len + tl.tok0;
+  const bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 && (c + 1) * KV_CHUNK - 1 <= pos_min &&
+                     (c + 1) * KV_CHUNK <= tl.kv_len;
+  const bf16x8 pb0 = pf_softmax(p, tl, c, plain, sc[0], st[0], j);
+  const bf16x8 pb1 = pf_softmax(p, tl, c, plain, sc[1], st[1], j);
+  const uint8_t* vt = buf + kPfKBytes;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const bf16x8 a = *(const bf16x8*)(vt + (16 * d + n) * kVTRow + 16 * j);
+    st[0].acc[d] = mfma(a, pb0, st[0].acc[d]);
+    st[1].acc[d] = mfma(a, pb1, st[1].acc[d]);
+  }
+}
+
+// Step on chunk c (in LDS buffer c & 1): fetch chunk c + 3 into `ld` (page ids from `pg`, loaded
+// a step earlier), page ids of chunk c + 4 into `pg`, compute chunk c, then chunk c + 1 (in `wr`)
+// goes to the other LDS buffer.
+template <int NP>
+__device__ __forceinline__ void pf_step(const Params& p, const PfTile& tl, int c, uint8_t* lds, const bf16x8 q[2][4],
+                                        PfRow st[2], PfRegs<NP>& ld, const PfRegs<NP>& wr, PfPages& pg, int tid,
+                                        int nthreads, int n, int j, int& err) {
+  const int last = tl.c_hi - 1;
+  pf_load_chunk<NP>(p, tl, c + 3 < last ? c + 3 : last, pg, tid, nthreads, ld);
+  pg = pf_load_pages<NP>(p, tl, c + 4 < last ? c + 4 : last, tid, nthreads, err);
+  pf_compute(p, tl, c, lds + (c & 1) * kPfBufBytes, q, st, n, j);
+  if (c + 1 < tl.c_hi) pf_store_chunk<NP>(lds + ((c + 1) & 1) * kPfBufBytes, wr, tid, nthreads);
+  __syncthreads();
+}
+
+template <int NP>
+__device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8_t* lds, int wv, int n, int j,
+                                        int& err) {
+  const int tid = threadIdx.x, nthreads = 64 * p.HG;
+  // queries: row r = 32*wv + 16*rb + n of the tile; B operand dims 32s + 8j .. +8
+  bf16x8 q[2][4];
+  PfRow st[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int r = 32 * wv + 16 * rb + n;
+    const int tok = r / p.G, g = r - tok * p.G;
+    st[rb].ok = tok < tl.ntok;
+    st[rb].pos = tl.kv_len - tl.q_len + tl.tok0 + tok;
+    st[rb].ok = st[rb].ok && st[rb].pos >= 0;
+    const int qtok = st[rb].ok ? tl.q_start + tl.tok0 + tok : tl.q_start;
+    const uint16_t* qp = p.q + ((size_t)qtok * p.Hq + tl.h * p.G + (st[rb].ok ? g : 0)) * kD + 8 * j;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) q[rb][s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st[rb].acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[rb].m = -INFINITY;
+    st[rb].l = 0.f;
+  }
+
+  // ring prologue: chunks c_lo .. c_lo+2 in flight, c_lo in LDS buffer (c_lo & 1)
+  const int c0 = tl.c_lo, last = tl.c_hi - 1;
+  PfRegs<NP> r0, r1, r2, r3;
+  PfPages pg = pf_load_pages<NP>(p, tl, c0, tid, nthreads, err);
+  pf_load_chunk<NP>(p, tl, c0, pg, tid, nthreads, r0);
+  pg = pf_load_pages<NP>(p, tl, c0 + 1 < last ? c0 + 1 : last, tid, nthreads, err);
+  pf_load_chunk<NP>(p, tl, c0 + 1 < last ? c0 + 1 : last, pg, tid, nthreads, r1);
+  pg = pf_load_pages<NP>(p, tl, c0 + 2 < last ? c0 + 2 : last, tid, nthreads, err);
+  pf_load_chunk<NP>(p, tl, c0 + 2 < last ? c0 + 2 : last, pg, tid, nthreads, r2);
+  pg = pf_load_pages<NP>(p, tl, c0 + 3 < last ? c0 + 3 : last, tid, nthreads, err);
+  __syncthreads();  // the previous tile's last chunk is no longer read
+  pf_store_chunk<NP>(lds + (c0 & 1) * kPfBufBytes, r0, tid, nthreads);
+  __syncthreads();
+
+  // ring slot of chunk c is (c - c0) % 4: r0 holds c0, r1 c0+1, r2 c0+2, r3 is loaded next
+  int c = c0;
+  for (;;) {
+    pf_step<NP>(p, tl, c, lds, q, st, r3, r1, pg, tid, nthreads, n, j, err);
+    if (++c >= tl.c_hi) break;
+    pf_step<NP>(p, tl, c, lds, q, st, r0, r2, pg, tid, nthreads, n, j, err);
+    if (++c >= tl.c_hi) break;
+    pf_step<NP>(p, tl, c, lds, q, st, r1, r3, pg, tid, nthreads, n, j, err);
+    if (++c >= tl.c_hi) break;
+    pf_step<NP>(p, tl, c, lds, q, st, r2, r0, pg, tid, nthreads, n, j, err);
+    if (++c >= tl.c_hi) break;
+  }
+
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const float lt = rows4_sum(st[rb].l);
+    if (!st[rb].ok) continue;
+    const int r = 32 * wv + 16 * rb + n;
+    const int tok = r / p.G, g = r - tok * p.G;
+    const float inv = 1.f / lt;
+    uint16_t* op = p.out + ((size_t)(tl.q_start + tl.tok0 + tok) * p.Hq + tl.h * p.G + g) * kD + 4 * j;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      u32x2 w;
+      w[0] = pack_bf16x2(st[rb].acc[d][0] * inv, st[rb].acc[d][1] * inv);
+      w[1] = pack_bf16x2(st[rb].acc[d][2] * inv, st[rb].acc[d][3] * inv);
+      *(u32x2*)(op + 16 * d) = w;
+    }
+  }
+}
+
+// The prefill role of a workgroup: take tiles from the queue until it runs dry.  wsi: the four
+// metadata windows (nseq <= 256), total: the call's tile count.
+template <int NP>
+__device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], int pf_min, int total, uint8_t* lds,
+                                        int* s_tile, int lane, int wv, int n, int j, int& err) {
+  for (;;) {
+    if (threadIdx.x == 0) *s_tile = atomicAdd(p.err + kQueueWord, 1);
+    __syncthreads();
+    const int ti = uni(*s_tile);
+    __syncthreads();
+    if (ti >= total) break;
+    // the sequence holding tile ti: windows in order, then the lane inside
+    PfTile tl;
+    tl.seq = -1;
+    int off = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int cnt = pf_tiles_of(p, wsi[w], pf_min) * p.Hkv;
+      int tot = cnt;
+      for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+      tot = uni(tot);
+      if (tl.seq < 0 && ti < off + tot) {
+        int incl = cnt;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += y;
+        }
+        const int idx = __popcll(__ballot(off + incl <= ti));
+        const int li = ti - off - rl(incl - cnt, idx);  // tile index inside the sequence
+        tl.seq = 64 * w + idx;
+        tl.kv_len = rl(wsi[w].kv_len, idx);
+        tl.q_len = rl(wsi[w].q_len, idx);
+        tl.q_start = rl(wsi[w].q_start, idx);
+        const int nt = (tl.q_len + p.pf_tq - 1) / p.pf_tq;
+        tl.h = li % p.Hkv;
+        const int t = nt - 1 - li / p.Hkv;  // last tile of the sequence first
+        tl.tok0 = t * p.pf_tq;
+        tl.ntok = tl.q_len - tl.tok0 < p.pf_tq ? tl.q_len - tl.tok0 : p.pf_tq;
+      }
+      off += tot;
+    }
+    if (tl.seq < 0) continue;  // not reached: ti < total
+    const int prior = tl.kv_len - tl.q_len;
+    const int pos_hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
+    if (pos_hi < 0) continue;                           // q_len > kv_len: rows left unwritten
+    int lo = 0;
+    if (p.sliding_window > 0) {
+      lo = prior + tl.tok0 - p.sliding_window + 1;  // keys below are masked for every row
+      lo = lo < 0 ? 0 : lo;
+    }
+    tl.c_lo = lo / KV_CHUNK;
+    tl.c_hi = ((pos_hi < tl.kv_len - 1 ? pos_hi : tl.kv_len - 1) + KV_CHUNK) / KV_CHUNK;
+    pf_tile<NP>(p, tl, lds, wv, n, j, err);
+  }
+}
+
 template <int MODE, bool UPG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x transposed V chunk
@@ -712,7 +1060,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int kWin = 4;
   Window win;
   SeqInfo wsi[kWin];
-  int nseq, tv;
+  int nseq, tv, pf_min;
   {
     int kv[kWin], c0[kWin], c1[kWin];
     const int ns_raw = p.num_seqs[0];
@@ -734,9 +1082,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int w = 0; w < kWin; ++w)
       if (nseq > 64 * w && nseq <= 64 * (w + 1)) tv = rl(c1[w], nseq - 1 - 64 * w);
     if (nseq > 64 * kWin) tv = uni(p.cu_q_lens[nseq]);
+    // prefill tiles need the whole metadata in the four windows
+    pf_min = (MODE == KV_BF16 && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
 #pragma unroll
-    for (int w = 0; w < kWin; ++w) wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, err);
+    for (int w = 0; w < kWin; ++w)
+      wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, pf_min, err);
   }
+  win.pf_min = pf_min;
   long long W = 0, tile[kWin];
   if (nseq <= 64 * kWin) {
 #pragma unroll
@@ -747,9 +1099,44 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   } else {
     W = total_units(p, nseq, lane, err);
   }
-  const Partition pt = make_partition(W, p.grid);
-  const long long u0 = uni64(range_start(b, pt)), u1 = uni64(range_start(b + 1, pt));
-  if (W > 0 && u0 < u1) {
+
+  // Work split: the first gpre workgroups take prefill tiles, the rest run stream-K over the
+  // other sequences.  Every workgroup computes the same split from the same metadata.
+  int gpre = 0, pf_total = 0;
+  if (MODE == KV_BF16 && pf_min > 0) {
+    float steps = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWin; ++w) {
+      const int nt = pf_tiles_of(p, wsi[w], pf_min);
+      const float prior = (float)(wsi[w].kv_len - wsi[w].q_len);
+      // chunks of key positions the tiles visit (causal), summed over the sequence's tiles
+      float st = nt > 0 ? (float)p.Hkv * ((float)nt * prior + (float)p.pf_tq * 0.5f * (float)nt * (float)(nt + 1)) /
+                              (float)KV_CHUNK
+                        : 0.f;
+      int cnt = nt * p.Hkv;
+      for (int o = 32; o > 0; o >>= 1) {
+        st += __shfl_xor(st, o, 64);
+        cnt += __shfl_xor(cnt, o, 64);
+      }
+      steps += __builtin_bit_cast(float, uni(__builtin_bit_cast(int, st)));
+      pf_total += uni(cnt);
+    }
+    if (pf_total > 0) {
+      const float pw = p.pf_cost * steps, dw = (float)W;
+      gpre = (int)((float)p.grid * pw / (pw + dw) + 0.5f);
+      gpre = gpre < 1 ? 1 : gpre;
+      if (W > 0 && gpre > p.grid - 1) gpre = p.grid - 1;
+      if (gpre > pf_total) gpre = pf_total;
+    }
+  }
+  if (MODE == KV_BF16 && b < gpre) {  // (HG == 8: one K and one V piece per thread per chunk)
+    __shared__ int s_tile;
+    pf_role<1>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+  }
+  const int bd = b - gpre, gd = p.grid - gpre;  // stream-K workgroup index and count
+  const Partition pt = make_partition(W, gd > 0 ? gd : 1);
+  const long long u0 = uni64(range_start(bd, pt)), u1 = uni64(range_start(bd + 1, pt));
+  if (bd >= 0 && W > 0 && u0 < u1) {
     int seq;
     long long seq_start;
     if (nseq <= 64 * kWin) {
@@ -803,9 +1190,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
       long long u = u0;
       for (;;) {
-        step<MODE, UPG>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt, wv);
+        step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt, wv);
         if (++u >= u1) break;
-        step<MODE, UPG>(p, nseq, lane, n, j, b, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt, wv);
+        step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt, wv);
         if (++u >= u1) break;
       }
     }
@@ -844,6 +1231,7 @@ __device__ __forceinline__ void merge_in(Merge& a, float mc, float lc, const flo
 // waves' results are merged through LDS in a fixed order, so the output is deterministic.
 __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
   __shared__ float red[4][64][34];
+  if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
   const int b = blockIdx.x / p.HG, hw = blockIdx.x - b * p.HG;  // descriptor, wave (head) of its group
   if (!p.desc[b].valid[hw]) return;
   const SplitDesc d = p.desc[b];
@@ -1159,6 +1547,14 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (opt->has_k_scale || opt->has_v_scale) mode = KV_BF16_SCALED;
   }
   p.grid = d.grid[mode][p.HG];
+  // prefill tiles: bf16 KV without scales, masked keys at weight 0, eight waves (kv heads) per
+  // workgroup
+  if (mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG && !getenv("RPA_NO_PREFILL_TILES")) {
+    p.pf_tq = 32 * p.HG / p.G;
+    p.pf_min = 16;
+    p.pf_cost = kPfCost;
+    if (const char* e = getenv("RPA_PF_COST")) p.pf_cost = (float)atof(e);
+  }
   hipStream_t st = (hipStream_t)stream;
   if (ev_begin && hipEventRecord((hipEvent_t)ev_begin, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");
