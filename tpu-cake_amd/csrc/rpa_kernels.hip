@@ -355,8 +355,10 @@ template <bool UPG>
 __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, int n) {
   Pages r;
   if constexpr (UPG) {
+    // one load at a wave-uniform address; the value is made uniform where it is used (a step
+    // later): a readfirstlane here would wait for every load in flight
     const size_t idx = x.nch > 0 ? (size_t)x.i * p.PPS + page_of(x.c * KV_CHUNK, p) : 0;
-    const int pg = uni(p.page_indices[idx]);
+    const int pg = p.page_indices[idx];
     r.pg[0] = r.pg[1] = pg;
     return r;
   }
@@ -721,13 +723,16 @@ constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
 constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
 constexpr float kPfCost = 0.15f;  // time of a prefill tile chunk / time of a stream-K unit
 
+struct PfPages {
+  int pg[2];  // page ids of this thread's keys (pieces 0 and 1) for one chunk
+};
+
+// One ring slot: a chunk's K and V pieces of this thread, and the page ids of a later chunk
+// (loaded two steps before they address that chunk's data).
 template <int NP>  // 16-byte pieces of K (and of V) per thread per chunk: 512 / threads
 struct PfRegs {
   u32x4 k[NP], v[NP];
-};
-
-struct PfPages {
-  int pg[2];  // page ids of this thread's keys (pieces 0 and 1) for one chunk
+  PfPages pg;
 };
 
 struct PfTile {
@@ -743,65 +748,110 @@ __device__ __forceinline__ int pf_tiles_of(const Params& p, const SeqInfo& si, i
   return (si.q_len + p.pf_tq - 1) / p.pf_tq;
 }
 
-// Page id of key kt of sequence seq (range-checked).
-__device__ __forceinline__ int pf_page(const Params& p, int seq, int kt, int& err) {
-  int pg = p.page_indices[(size_t)seq * p.PPS + page_of(kt, p)];
-  if (pg < 0 || pg >= p.P) {
-    err |= ERR_PAGE;
-    pg = 0;
-  }
-  return pg;
+// Which K/V piece of a chunk thread tid (of 512) carries: wave w, lane l; key group g = w/2
+// (keys tau(g, e) = 16*(e/4) + 4g + e%4, e = l/8: the eight keys one MFMA fragment lane of V^T
+// needs), dims 64*(w%2) + 8*(l%8) .. +8.  Eight lanes l%8 = const hold the same dims of the
+// group's eight keys, so an 8x8 transpose across them (three lane-exchange stages) turns their V
+// pieces into eight keys of one dim each: one 16-byte LDS write per lane.
+struct PfPiece {
+  int key, d0;
+};
+
+__device__ __forceinline__ PfPiece pf_piece(int tid) {
+  const int w = tid >> 6, l = tid & 63, e = l >> 3;
+  PfPiece pc;
+  pc.key = 16 * (e >> 2) + 4 * (w >> 1) + (e & 3);
+  pc.d0 = 64 * (w & 1) + 8 * (l & 7);
+  return pc;
 }
 
-template <int NP>
-__device__ __forceinline__ int pf_key_of(int tid, int i, int nthreads) {
-  return (tid + i * nthreads) >> 4;
-}
-
-template <int NP>
-__device__ __forceinline__ PfPages pf_load_pages(const Params& p, const PfTile& tl, int c, int tid, int nthreads,
-                                                 int& err) {
+// Raw page ids of this thread's key in chunk c; checked and (UPG) made wave-uniform where they
+// are used (pf_load_chunk), two steps later, so that nothing waits for them here.  UPG
+// (page_size a multiple of 32): the chunk lies in one page, loaded at one uniform address.
+template <int NP, bool UPG>
+__device__ __forceinline__ PfPages pf_load_pages(const Params& p, const PfTile& tl, int c, int tid, int nthreads) {
+  static_assert(NP == 1, "prefill tiles use 512-thread workgroups");
   PfPages r;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    int kt = c * KV_CHUNK + pf_key_of<NP>(tid, i, nthreads);
-    kt = kt < tl.kv_len ? kt : tl.kv_len - 1;
-    r.pg[i] = pf_page(p, tl.seq, kt, err);
+  if constexpr (UPG) {
+    r.pg[0] = r.pg[1] = p.page_indices[(size_t)tl.seq * p.PPS + page_of(c * KV_CHUNK, p)];
+    return r;
   }
+  int kt = c * KV_CHUNK + pf_piece(tid).key;
+  kt = kt < tl.kv_len ? kt : tl.kv_len - 1;
+  r.pg[0] = r.pg[1] = p.page_indices[(size_t)tl.seq * p.PPS + page_of(kt, p)];
   return r;
 }
 
-template <int NP>
-__device__ __forceinline__ void pf_load_chunk(const Params& p, const PfTile& tl, int c, const PfPages& pg, int tid,
-                                              int nthreads, PfRegs<NP>& r) {
+// This thread's K and V pieces of chunk c.  Keys past kv_len read key kv_len - 1 (always written
+// data: the scores of such keys are -inf, but their V still meets P = 0 in the PV product).
+template <int NP, bool UPG>
+__device__ __forceinline__ void pf_load_chunk(const Params& p, const PfTile& tl, int c, const PfPages& pages, int tid,
+                                              int nthreads, PfRegs<NP>& r, int& err) {
   const uint16_t* kv = (const uint16_t*)p.kv;
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int q = tid + i * nthreads;
-    int kt = c * KV_CHUNK + (q >> 4);
-    kt = kt < tl.kv_len ? kt : tl.kv_len - 1;
-    const size_t e = kv_elem(p, pg.pg[i], kt, 2 * tl.h) + 8 * (q & 15);
-    r.k[i] = *(const u32x4*)(kv + e);
-    r.v[i] = *(const u32x4*)(kv + e + kD);
+  const PfPiece pc = pf_piece(tid);
+  if constexpr (UPG) {
+    int pg = uni(pages.pg[0]);
+    if (pg < 0 || pg >= p.P) {  // out-of-range page id: never dereferenced
+      err |= ERR_PAGE;
+      pg = 0;
+    }
+    const uint16_t* base = kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h);
+    const int kmax = tl.kv_len - 1 - c * KV_CHUNK;
+    const int off = (pc.key < kmax ? pc.key : kmax) * (2 * p.Hkv * kD) + pc.d0;
+    r.k[0] = *(const u32x4*)(base + off);
+    r.v[0] = *(const u32x4*)(base + off + kD);
+    return;
   }
+  int kt = c * KV_CHUNK + pc.key;
+  kt = kt < tl.kv_len ? kt : tl.kv_len - 1;
+  int pg = pages.pg[0];
+  if (pg < 0 || pg >= p.P) {  // out-of-range page id: never dereferenced
+    err |= ERR_PAGE;
+    pg = 0;
+  }
+  const size_t e = kv_elem(p, pg, kt, 2 * tl.h) + pc.d0;
+  r.k[0] = *(const u32x4*)(kv + e);
+  r.v[0] = *(const u32x4*)(kv + e + kD);
 }
+
+// Column group (16 bytes = 8 key slots) of V^T row `row` holding slot group g: XOR-swizzled by
+// row bits 4-5, so the 8 rows 8 apart that one transposed write touches, and the 8 consecutive rows
+// one fragment read touches, fall in distinct banks.
+__device__ __forceinline__ int pf_vt_group(int row, int g) { return g ^ ((row >> 4) & 3); }
 
 template <int NP>
 __device__ __forceinline__ void pf_store_chunk(uint8_t* buf, const PfRegs<NP>& r, int tid, int nthreads) {
-  uint8_t* vt = buf + kPfKBytes;
+  const PfPiece pc = pf_piece(tid);
+  const int l = tid & 63, g = (tid >> 6) >> 1;
+  *(u32x4*)(buf + pc.key * kPfKRow + pc.d0 * 2) = r.k[0];
+  // 8x8 transpose of bf16 across lanes l%8 = const (row e = l/8 holds key e's 8 dims): exchange
+  // element bit i with lane-group bit i for i = 0 (lanes ^8), 1 (^16), 2 (^32)
+  uint32_t d[4] = {r.v[0][0], r.v[0][1], r.v[0][2], r.v[0][3]};
+  const uint32_t sel = (l & 8) ? 0x03020706u : 0x05040100u;
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int q = tid + i * nthreads, key = q >> 4, pc = q & 15;
-    *(u32x4*)(buf + key * kPfKRow + pc * 16) = r.k[i];
-    const int slot_b = 2 * (8 * ((key & 15) >> 2) + 4 * (key >> 4) + (key & 3));
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t w = r.v[i][t];
-      const int d = 8 * pc + 2 * t;
-      *(uint16_t*)(vt + d * kVTRow + slot_b) = (uint16_t)(w & 0xffffu);
-      *(uint16_t*)(vt + (d + 1) * kVTRow + slot_b) = (uint16_t)(w >> 16);
-    }
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t pv = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[m], 0x128, 0xf, 0xf, false);  // lane ^ 8
+    d[m] = __builtin_amdgcn_perm(pv, d[m], sel);
   }
+  {
+    const auto x = __builtin_amdgcn_permlane16_swap(d[0], d[1], false, false);
+    const auto y = __builtin_amdgcn_permlane16_swap(d[2], d[3], false, false);
+    d[0] = x[0];
+    d[1] = x[1];
+    d[2] = y[0];
+    d[3] = y[1];
+  }
+  {
+    const auto x = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+    const auto y = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+    d[0] = x[0];
+    d[2] = x[1];
+    d[1] = y[0];
+    d[3] = y[1];
+  }
+  // this lane now holds keys tau(g, 0..7) of dim d0 + l/8: slots 8g .. 8g+7 of that V^T row
+  const int row = pc.d0 + (l >> 3);
+  *(u32x4*)(buf + kPfKBytes + row * kVTRow + 16 * pf_vt_group(row, g)) = u32x4{d[0], d[1], d[2], d[3]};
 }
 
 struct PfRow {
@@ -897,28 +947,32 @@ __device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, in
   const uint8_t* vt = buf + kPfKBytes;
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
-    const bf16x8 a = *(const bf16x8*)(vt + (16 * d + n) * kVTRow + 16 * j);
+    const int row = 16 * d + n;
+    const bf16x8 a = *(const bf16x8*)(vt + row * kVTRow + 16 * pf_vt_group(row, j));
     st[0].acc[d] = mfma(a, pb0, st[0].acc[d]);
     st[1].acc[d] = mfma(a, pb1, st[1].acc[d]);
   }
 }
 
-// Step on chunk c (in LDS buffer c & 1): fetch chunk c + 3 into `ld` (page ids from `pg`, loaded
-// a step earlier), page ids of chunk c + 4 into `pg`, compute chunk c, then chunk c + 1 (in `wr`)
-// goes to the other LDS buffer.
-template <int NP>
+// Step on chunk c (in LDS buffer c & 1).  Ring slot x % 4 holds chunk x's data and, from two
+// steps before that data is fetched, its page ids.  Order matters with in-order vmcnt: page ids
+// of chunk c + 5 (into `nx`, whose data, chunk c + 1, is still to be stored), then chunk c + 3's
+// data (into `ld`, with the page ids it received two steps ago); compute chunk c; store chunk
+// c + 1 (`nx`) to the other LDS buffer.  No wait here needs a load younger than the chunk it
+// waits for.
+template <int NP, bool UPG>
 __device__ __forceinline__ void pf_step(const Params& p, const PfTile& tl, int c, uint8_t* lds, const bf16x8 q[2][4],
-                                        PfRow st[2], PfRegs<NP>& ld, const PfRegs<NP>& wr, PfPages& pg, int tid,
-                                        int nthreads, int n, int j, int& err) {
+                                        PfRow st[2], PfRegs<NP>& ld, PfRegs<NP>& nx, int tid, int nthreads, int n,
+                                        int j, int& err) {
   const int last = tl.c_hi - 1;
-  pf_load_chunk<NP>(p, tl, c + 3 < last ? c + 3 : last, pg, tid, nthreads, ld);
-  pg = pf_load_pages<NP>(p, tl, c + 4 < last ? c + 4 : last, tid, nthreads, err);
+  nx.pg = pf_load_pages<NP, UPG>(p, tl, c + 5 < last ? c + 5 : last, tid, nthreads);
+  pf_load_chunk<NP, UPG>(p, tl, c + 3 < last ? c + 3 : last, ld.pg, tid, nthreads, ld, err);
   pf_compute(p, tl, c, lds + (c & 1) * kPfBufBytes, q, st, n, j);
-  if (c + 1 < tl.c_hi) pf_store_chunk<NP>(lds + ((c + 1) & 1) * kPfBufBytes, wr, tid, nthreads);
+  if (c + 1 < tl.c_hi) pf_store_chunk<NP>(lds + ((c + 1) & 1) * kPfBufBytes, nx, tid, nthreads);
   __syncthreads();
 }
 
-template <int NP>
+template <int NP, bool UPG>
 __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8_t* lds, int wv, int n, int j,
                                         int& err) {
   const int tid = threadIdx.x, nthreads = 64 * p.HG;
@@ -942,30 +996,33 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
     st[rb].l = 0.f;
   }
 
-  // ring prologue: chunks c_lo .. c_lo+2 in flight, c_lo in LDS buffer (c_lo & 1)
+  // ring prologue: page ids of chunks c_lo .. c_lo+4, data of c_lo .. c_lo+2 in flight; c_lo goes
+  // to LDS buffer (c_lo & 1)
   const int c0 = tl.c_lo, last = tl.c_hi - 1;
+  auto cl = [&](int c) { return c < last ? c : last; };
   PfRegs<NP> r0, r1, r2, r3;
-  PfPages pg = pf_load_pages<NP>(p, tl, c0, tid, nthreads, err);
-  pf_load_chunk<NP>(p, tl, c0, pg, tid, nthreads, r0);
-  pg = pf_load_pages<NP>(p, tl, c0 + 1 < last ? c0 + 1 : last, tid, nthreads, err);
-  pf_load_chunk<NP>(p, tl, c0 + 1 < last ? c0 + 1 : last, pg, tid, nthreads, r1);
-  pg = pf_load_pages<NP>(p, tl, c0 + 2 < last ? c0 + 2 : last, tid, nthreads, err);
-  pf_load_chunk<NP>(p, tl, c0 + 2 < last ? c0 + 2 : last, pg, tid, nthreads, r2);
-  pg = pf_load_pages<NP>(p, tl, c0 + 3 < last ? c0 + 3 : last, tid, nthreads, err);
+  r0.pg = pf_load_pages<NP, UPG>(p, tl, c0, tid, nthreads);
+  r1.pg = pf_load_pages<NP, UPG>(p, tl, cl(c0 + 1), tid, nthreads);
+  r2.pg = pf_load_pages<NP, UPG>(p, tl, cl(c0 + 2), tid, nthreads);
+  r3.pg = pf_load_pages<NP, UPG>(p, tl, cl(c0 + 3), tid, nthreads);
+  pf_load_chunk<NP, UPG>(p, tl, c0, r0.pg, tid, nthreads, r0, err);
+  pf_load_chunk<NP, UPG>(p, tl, cl(c0 + 1), r1.pg, tid, nthreads, r1, err);
+  pf_load_chunk<NP, UPG>(p, tl, cl(c0 + 2), r2.pg, tid, nthreads, r2, err);
+  r0.pg = pf_load_pages<NP, UPG>(p, tl, cl(c0 + 4), tid, nthreads);
   __syncthreads();  // the previous tile's last chunk is no longer read
   pf_store_chunk<NP>(lds + (c0 & 1) * kPfBufBytes, r0, tid, nthreads);
   __syncthreads();
 
-  // ring slot of chunk c is (c - c0) % 4: r0 holds c0, r1 c0+1, r2 c0+2, r3 is loaded next
+  // chunk c lives in ring slot (c - c0) % 4
   int c = c0;
   for (;;) {
-    pf_step<NP>(p, tl, c, lds, q, st, r3, r1, pg, tid, nthreads, n, j, err);
+    pf_step<NP, UPG>(p, tl, c, lds, q, st, r3, r1, tid, nthreads, n, j, err);
     if (++c >= tl.c_hi) break;
-    pf_step<NP>(p, tl, c, lds, q, st, r0, r2, pg, tid, nthreads, n, j, err);
+    pf_step<NP, UPG>(p, tl, c, lds, q, st, r0, r2, tid, nthreads, n, j, err);
     if (++c >= tl.c_hi) break;
-    pf_step<NP>(p, tl, c, lds, q, st, r1, r3, pg, tid, nthreads, n, j, err);
+    pf_step<NP, UPG>(p, tl, c, lds, q, st, r1, r3, tid, nthreads, n, j, err);
     if (++c >= tl.c_hi) break;
-    pf_step<NP>(p, tl, c, lds, q, st, r2, r0, pg, tid, nthreads, n, j, err);
+    pf_step<NP, UPG>(p, tl, c, lds, q, st, r2, r0, tid, nthreads, n, j, err);
     if (++c >= tl.c_hi) break;
   }
 
@@ -989,7 +1046,7 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
 
 // The prefill role of a workgroup: take tiles from the queue until it runs dry.  wsi: the four
 // metadata windows (nseq <= 256), total: the call's tile count.
-template <int NP>
+template <int NP, bool UPG>
 __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], int pf_min, int total, uint8_t* lds,
                                         int* s_tile, int lane, int wv, int n, int j, int& err) {
   for (;;) {
@@ -1039,7 +1096,7 @@ __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], i
     }
     tl.c_lo = lo / KV_CHUNK;
     tl.c_hi = ((pos_hi < tl.kv_len - 1 ? pos_hi : tl.kv_len - 1) + KV_CHUNK) / KV_CHUNK;
-    pf_tile<NP>(p, tl, lds, wv, n, j, err);
+    pf_tile<NP, UPG>(p, tl, lds, wv, n, j, err);
   }
 }
 
@@ -1131,7 +1188,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   if (MODE == KV_BF16 && b < gpre) {  // (HG == 8: one K and one V piece per thread per chunk)
     __shared__ int s_tile;
-    pf_role<1>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+    pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
   const int bd = b - gpre, gd = p.grid - gpre;  // stream-K workgroup index and count
   const Partition pt = make_partition(W, gd > 0 ? gd : 1);
