@@ -162,6 +162,15 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A zero the compiler cannot see through.  Added to a wave-uniform load index it keeps the loaded
+// value in a VGPR: a value the compiler proves uniform is copied to an SGPR right after its load,
+// and that copy waits (in-order vmcnt) for every load in flight, including the prefetches.
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -355,10 +364,9 @@ template <bool UPG>
 __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, int n) {
   Pages r;
   if constexpr (UPG) {
-    // one load at a wave-uniform address; the value is made uniform where it is used (a step
-    // later): a readfirstlane here would wait for every load in flight
+    // one load at a wave-uniform address, kept per lane until it is used (a step later)
     const size_t idx = x.nch > 0 ? (size_t)x.i * p.PPS + page_of(x.c * KV_CHUNK, p) : 0;
-    const int pg = p.page_indices[idx];
+    const int pg = p.page_indices[idx + opaque_zero()];
     r.pg[0] = r.pg[1] = pg;
     return r;
   }
@@ -389,7 +397,7 @@ struct HalfRegs<KV_BF16_SCALED> {
 template <>
 struct HalfRegs<KV_FP8> {
   u32x2 w[2][4];
-  float sc[2];  // per-(page, kv head) scale of each of the lane's two keys
+  float sc[2];  // per-(page, kv head) scale of each of the lane's two keys (k_scale/v_scale not applied)
 };
 
 // Where this lane's two keys of unit x live (element index of their K row) and their pages.
@@ -430,9 +438,9 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
       const uint8_t* kp = p.kv + e;
 #pragma unroll
       for (int s = 0; s < 4; ++s) r.w[blk][s] = *(const u32x2*)(kp + 32 * s);
-      float sc = which ? p.v_scale : p.k_scale;
-      if (p.kv_scales) sc *= p.kv_scales[((size_t)a.pg[blk] * p.Hkv + a.h) * 2 + which];
-      r.sc[blk] = sc;
+      // the raw per-(page, head) scale; multiplied in where it is used (to_bf16x8), a step later,
+      // so that nothing waits for this load here
+      r.sc[blk] = p.kv_scales ? p.kv_scales[((size_t)a.pg[blk] * p.Hkv + a.h) * 2 + which] : 1.f;
     } else {
       const uint16_t* kp = (const uint16_t*)p.kv + e;
 #pragma unroll
@@ -483,7 +491,7 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 w, float sc) {
 template <int MODE>
 __device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which) {
   if constexpr (MODE == KV_FP8) {
-    return fp8x8_to_bf16x8(r.w[blk][s], r.sc[blk]);
+    return fp8x8_to_bf16x8(r.w[blk][s], (which ? p.v_scale : p.k_scale) * r.sc[blk]);
   } else if constexpr (MODE == KV_BF16_SCALED) {
     return scale_bf16x8(r.w[blk][s], which ? p.v_scale : p.k_scale);
   } else {
@@ -721,7 +729,7 @@ constexpr int kPfKRow = kD * 2 + 16;
 constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
 constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
 constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
-constexpr float kPfCost = 0.15f;  // time of a prefill tile chunk / time of a stream-K unit
+constexpr float kPfCost = 0.35f;  // time of a prefill tile chunk / time of a stream-K unit (measured)
 
 struct PfPages {
   int pg[2];  // page ids of this thread's keys (pieces 0 and 1) for one chunk
@@ -773,7 +781,7 @@ __device__ __forceinline__ PfPages pf_load_pages(const Params& p, const PfTile& 
   static_assert(NP == 1, "prefill tiles use 512-thread workgroups");
   PfPages r;
   if constexpr (UPG) {
-    r.pg[0] = r.pg[1] = p.page_indices[(size_t)tl.seq * p.PPS + page_of(c * KV_CHUNK, p)];
+    r.pg[0] = r.pg[1] = p.page_indices[(size_t)tl.seq * p.PPS + page_of(c * KV_CHUNK, p) + opaque_zero()];
     return r;
   }
   int kt = c * KV_CHUNK + pf_piece(tid).key;
