@@ -5,19 +5,26 @@
 // 2h+1, fp32 scores and softmax, optional sliding window / soft cap / mask value / K,V scales).
 //
 // Structure (one call = two launches on the caller's stream):
-//   rpa_attn_kernel     stream-K over (sequence, kv-head group, row block, 32-key chunk) units
-//                       (see rpa_schedule.h).  A workgroup is one wave per kv head of a group of
-//                       HG heads (HG = the largest divisor of Hkv that is <= 8): its waves walk
-//                       the same units in step, wave w computing kv head group*HG + w, so the
-//                       HG heads' slices of each key's 2*Hkv*D row are fetched together (full
-//                       rows reach HBM far better than isolated per-head slices); QK^T and PV on
-//                       v_mfma_f32_16x16x32_bf16; online softmax in fp32 (exp2 domain).  A row
-//                       block finished inside one workgroup is written directly; a row block
-//                       split across workgroups leaves one partial (m, l, acc) per workgroup,
-//                       and the workgroup owning its last unit leaves a descriptor of it.
+//   rpa_attn_kernel     persistent grid with two roles, split by a cost model every workgroup
+//                       evaluates identically from the metadata:
+//                       * prefill tiles (sequences with many query tokens): 256-row tiles of one
+//                         kv head, K/V chunks staged once per workgroup in LDS (see the prefill
+//                         section below);
+//                       * stream-K over (sequence, kv-head group, row block, 32-key chunk) units
+//                         (see rpa_schedule.h) for the other sequences.  A workgroup is one wave
+//                         per kv head of a group of HG heads (HG = the largest divisor of Hkv that
+//                         is <= 8): its waves walk the same units in step, wave w computing kv
+//                         head group*HG + w, so the HG heads' slices of each key's 2*Hkv*D row are
+//                         fetched together (full rows reach HBM far better than isolated per-head
+//                         slices); QK^T and PV on v_mfma_f32_16x16x32_bf16; online softmax in fp32
+//                         (exp2 domain).  A row block finished inside one workgroup is written
+//                         directly; a row block split across workgroups leaves one partial
+//                         (m, l, acc) per workgroup, and the workgroup owning its last unit leaves
+//                         a descriptor of it.
 //   rpa_combine_kernel  one 4-wave workgroup per descriptor: log-sum-exp merge of the row
-//                       block's partials (the waves take every 4th contributor, four at a
-//                       time, then merge through LDS), writes the rows, clears the descriptor.
+//                       block's partials (the waves take every 4th contributor, then merge
+//                       through LDS), writes the rows, clears the descriptor; resets the
+//                       prefill tile queue for the next call.
 //
 // MFMA operand layouts (16x16x32 bf16, wave64): A[i][k] and B[k][j] place row i / column j
 // at lane%16 and the 32 k-slots at (lane/16, element 0..7); D[i][j] sits at lane
