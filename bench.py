@@ -78,19 +78,29 @@ def cpu_baseline(case, budget_s: float = 20.0) -> dict:
     }
 
 
+def kernel_source_digest() -> str:
+    """sha256[:16] of the kernel sources with comments and blank space removed (so that editing
+    a comment does not orphan a measurement)."""
+    import hashlib
+    import re
+
+    csrc = ROOT / "tpu-cake_amd" / "csrc"
+    text = "".join((csrc / f).read_text() for f in ("rpa_kernels.hip", "rpa_schedule.h"))
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    text = re.sub(r"\s+", " ", text).strip()
+    return hashlib.sha256(text.encode()).hexdigest()[:16]
+
+
 def measured_traffic(cfg: str):
     """HBM bytes per attention-kernel dispatch from the committed rocprofv3 PMC summary
     (profiles/pmc_traffic.json: FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's
     reading for a 1 GiB copy), used only if it was measured on the current kernel sources."""
-    import hashlib
-
     path = ROOT / "profiles" / "pmc_traffic.json"
     if not path.exists():
         return None
     data = json.loads(path.read_text())
-    csrc = ROOT / "tpu-cake_amd" / "csrc"
-    digest = hashlib.sha256(b"".join((csrc / f).read_bytes() for f in ("rpa_kernels.hip", "rpa_schedule.h")))
-    if digest.hexdigest()[:16] != data.get("source_sha256_16") or cfg not in data.get("configs", {}):
+    if kernel_source_digest() != data.get("source_sha256_16") or cfg not in data.get("configs", {}):
         return None
     return data["configs"][cfg]["traffic_bytes"]
 
