@@ -60,12 +60,13 @@ def bf16_from_f32(x: np.ndarray) -> np.ndarray:
     used by the reference's input builders (``inkling_rpa.py:416-418``).
     """
     f = np.ascontiguousarray(x, dtype=np.float32)
-    u = f.view(np.uint32).astype(np.uint64)
-    rounding_bias = ((u >> 16) & 1) + 0x7FFF
-    r = ((u + rounding_bias) >> 16).astype(np.uint16)
+    u = f.view(np.uint32)
+    # no overflow for non-NaN patterns (at most 0xFF800000 + 0x8000); NaNs are replaced below
+    rounding_bias = ((u >> np.uint32(16)) & np.uint32(1)) + np.uint32(0x7FFF)
+    r = ((u + rounding_bias) >> np.uint32(16)).astype(np.uint16)
     nan = np.isnan(f)
     if nan.any():
-        r = np.where(nan, ((u >> 16).astype(np.uint16) | 0x0040), r).astype(np.uint16)
+        r = np.where(nan, ((u >> np.uint32(16)).astype(np.uint16) | np.uint16(0x0040)), r).astype(np.uint16)
     return r
 
 
