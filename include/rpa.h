@@ -139,6 +139,55 @@ int rpa_gather_kv(const rpa_shape_t* shape, const void* kv_pages, const int32_t*
 int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* host_word,
                         void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Fused Inkling decode (v3 semantics): write each sequence's new K/V token into the paged
+ * cache, then attend over the updated cache with an additive relative-position bias.
+ * Replaces FusedRpaPlan.invoke / run_preflighted (src/tpu_cake/rpa_lowering.py:232-288) over
+ * the fused kernel whose semantics the reference pins in inkling_fused_rpa_reference
+ * (src/tpu_cake/workloads/inkling_rpa.py:471-589):
+ *   * decode only: one query token per sequence (cu_q_lens = 0..B, distribution = (B, B, B));
+ *   * sequence s's pages are page_indices[cu_kv_lens[s] / S ...] (cu_kv_lens page-aligned);
+ *   * K of kv head h goes to combined row 2h, V to 2h+1, at slot (kv_len-1) % S of page
+ *     page_indices[cu_kv_lens[s]/S + (kv_len-1)/S]; rows are zero-padded to cache_width;
+ *   * score = (q . k) * sm_scale + relative_states[s,h,:] . relative_projection[:, d]
+ *     for distances d = kv_len-1-key < relative_extent (else no bias); fp32 softmax.
+ * The cache is updated in place (the reference aliases it to an output).  Metadata must have
+ * passed the reference's preflight (rpa_lowering.py:71-128; the Python wrapper runs it);
+ * the device still range-checks what it dereferences (error word).  cu_q_lens and
+ * distribution are part of the reference's input list and are validated by that preflight;
+ * the device does not read them.  head_dim <= cache_width = 128.
+ * --------------------------------------------------------------------------------------- */
+typedef struct rpa_fused_shape {
+  int32_t num_seqs;          /* B */
+  int32_t num_q_heads;       /* Hq */
+  int32_t num_kv_heads;      /* Hkv */
+  int32_t head_dim;          /* D: width of queries, new K/V and the output (<= cache_width) */
+  int32_t total_pages;       /* P */
+  int32_t page_size;         /* S */
+  int32_t cache_width;       /* padded row width of the cache (128) */
+  int32_t page_entries;      /* length of the flat page_indices list */
+  int32_t pages_per_seq;     /* max over sequences of ceil(kv_len / S) */
+  int32_t relative_dim;      /* R (0: no relative bias) */
+  int32_t relative_extent;   /* E */
+} rpa_fused_shape_t;
+
+/* Workspace bytes for rpa_inkling_fused_decode on the current device (0 on a bad shape). */
+size_t rpa_fused_workspace_size(const rpa_fused_shape_t* shape);
+
+/* queries bf16 [B, Hq, D]; keys, values bf16 [B, Hkv, D] (the new token); cache bf16
+ * [P, S, 2*Hkv, cache_width] (the reference's [P, S, 2*Hkv/packing, packing, width]);
+ * kv_lens int32 [B] (including the new token); page_indices int32 [page_entries];
+ * cu_q_lens int32 [B+1]; cu_kv_lens int32 [B+1]; distribution int32 [3];
+ * relative_states bf16 [B, Hq, R]; relative_projection bf16 [R, E] (both NULL when R = 0);
+ * out bf16 [B, Hq, D].  The workspace is initialised with rpa_workspace_init like the
+ * operator's. */
+int rpa_inkling_fused_decode(const rpa_fused_shape_t* shape, float sm_scale, const void* queries,
+                             const void* keys, const void* values, void* cache, const int32_t* kv_lens,
+                             const int32_t* page_indices, const int32_t* cu_q_lens, const int32_t* cu_kv_lens,
+                             const int32_t* distribution, const void* relative_states,
+                             const void* relative_projection, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,14 +51,16 @@ def test_struct_layout_matches_c(tmp_path):
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "rpa.h"\n'
         "int main(void){\n"
-        '  printf("%zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t), offsetof(rpa_shape_t, kv_dtype),\n'
+        '  printf("%zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t), offsetof(rpa_shape_t, kv_dtype),\n'
         "         sizeof(rpa_options_t), offsetof(rpa_options_t, mask_value), offsetof(rpa_options_t, v_scale),\n"
-        "         offsetof(rpa_options_t, has_k_scale));\n  return 0; }\n")
+        "         offsetof(rpa_options_t, has_k_scale), sizeof(rpa_fused_shape_t),\n"
+        "         offsetof(rpa_fused_shape_t, relative_extent));\n  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [ctypes.sizeof(_lib.RpaShape), _lib.RpaShape.kv_dtype.offset, ctypes.sizeof(_lib.RpaOptions),
-            _lib.RpaOptions.mask_value.offset, _lib.RpaOptions.v_scale.offset, _lib.RpaOptions.has_k_scale.offset]
+            _lib.RpaOptions.mask_value.offset, _lib.RpaOptions.v_scale.offset, _lib.RpaOptions.has_k_scale.offset,
+            ctypes.sizeof(_lib.RpaFusedShape), _lib.RpaFusedShape.relative_extent.offset]
     assert got == want
 
 
@@ -100,3 +102,15 @@ def test_schedule_math_host_checker(tmp_path):
                     str(ROOT / "tests" / "sched_check.cpp"), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and out.stdout.startswith("OK"), out.stdout + out.stderr
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every declared entry point's ctypes argtypes count equals its C parameter count
+    (an undeclared trailing argument would be marshalled as a C int)."""
+    import re
+    text = HEADER.read_text()
+    lib = _lib.load()
+    for name in declared_functions():
+        m = re.search(r"\b" + name + r"\s*\(([^)]*)\)", text)
+        params = [x for x in m.group(1).split(",") if x.strip() and x.strip() != "void"]
+        assert len(getattr(lib, name).argtypes) == len(params), name

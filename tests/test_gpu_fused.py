@@ -1,0 +1,97 @@
+"""GPU parity of the fused Inkling decode (rpa_inkling_fused_decode through tpu_cake_amd.fused)
+against the fused oracle, with the reference's gate (rpa_runner.py:112-122): output allclose at
+0.02/0.02 and the updated cache bit-exact."""
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rpa_fused_oracle as fo
+from oracle import rpa_oracle as orc
+from tpu_cake_amd import fused
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _to_device(inp):
+    out = []
+    for name in fused.INPUT_NAMES:
+        a = inp[name]
+        if a.dtype == np.uint16:
+            t = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        else:
+            t = torch.from_numpy(np.ascontiguousarray(a))
+        out.append(t.cuda())
+    return out
+
+
+def _bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _run_and_check(inp):
+    expected = fo.inkling_fused_rpa_reference(inp)
+    args = _to_device(inp)
+    out, cache = fused.run_preflighted(*args)
+    torch.cuda.synchronize()
+    got = (_bits(out), _bits(cache).reshape(inp["cache"].shape))
+    err = orc.errors(orc.bf16_to_f32(got[0]), orc.bf16_to_f32(expected[0]))
+    same_cache = np.array_equal(got[1], expected[1])
+    print(f"  max_abs={err['max_abs']:.3e} cache_exact={same_cache}")
+    assert same_cache
+    assert fo.fused_rpa_outputs_pass(got, expected)
+    assert fused.read_error_word() == 0
+    return got
+
+
+@pytest.mark.parametrize("seed", [97, 83, 0])
+def test_reference_fixture(cuda, seed):
+    _say(f"fused fixture seed {seed}")
+    _run_and_check(fo.inkling_fused_rpa_inputs(seed=seed))
+
+
+@pytest.mark.parametrize("hq,hkv,d,page,lens", [
+    (32, 8, 128, 64, [1, 63, 64, 65, 511, 512, 513, 700, 2048, 3000]),   # Inkling decode shapes, D = 128
+    (16, 4, 64, 16, [5, 16, 17, 300, 1000]),                             # narrower rows (D < 128)
+    (8, 8, 128, 32, [2, 33, 100]),                                       # G = 1
+])
+def test_decode_shapes(cuda, hq, hkv, d, page, lens):
+    _say(f"fused decode hq={hq} hkv={hkv} d={d} page={page}")
+    pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(len(lens) * 7 + hq, nseq=len(lens), hq=hq, hkv=hkv, d=d, page_size=page,
+                               pool_pages=pool, lengths=lens, rel_dim=16, extent=512)
+    _run_and_check(inp)
+
+
+def test_rejected_metadata_never_reaches_the_kernel(cuda):
+    _say("fused preflight before the kernel")
+    inp = fo.inkling_fused_rpa_inputs(seed=97)
+    pages = inp["page_indices"].copy()
+    pages[2] = pages[0]
+    inp["page_indices"] = pages
+    args = _to_device(inp)
+    before = _bits(args[3]).copy()
+    with pytest.raises(ValueError, match="updates collide"):
+        fused.run_preflighted(*args)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(args[3]), before)
+
+
+def test_repeat_is_idempotent(cuda):
+    """Writing the same token twice leaves the same cache and output."""
+    _say("fused repeat")
+    inp = fo.inkling_fused_rpa_inputs(seed=3)
+    args = _to_device(inp)
+    out1, cache1 = fused.run_preflighted(*args)
+    o1, c1 = _bits(out1).copy(), _bits(cache1).copy()
+    out2, cache2 = fused.run_preflighted(*args)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out2), o1) and np.array_equal(_bits(cache2), c1)

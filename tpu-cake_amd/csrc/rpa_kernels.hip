@@ -67,7 +67,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-enum KvMode { KV_BF16 = 0, KV_BF16_SCALED = 1, KV_FP8 = 2 };
+// KV_BF16_BIAS: bf16 KV plus an additive relative-position bias table (the fused Inkling decode).
+enum KvMode { KV_BF16 = 0, KV_BF16_SCALED = 1, KV_FP8 = 2, KV_BF16_BIAS = 3 };
+constexpr int kModes = 4;
 
 enum ErrBits { ERR_PAGE = 1, ERR_QROW = 2, ERR_KVLEN = 4, ERR_QLEN = 8 };
 
@@ -101,6 +103,9 @@ struct Params {
   float k_scale, v_scale;
   int grid;
   bool skip_masked;  // mask value so negative that masked keys get weight exactly 0
+  const float* rel_bias;  // KV_BF16_BIAS: [num_seqs, Hq, rel_extent] fp32, added to the scaled score of a
+                          // key at distance d = pos - key < rel_extent from its query row
+  int rel_extent;
   int pf_tq;         // tokens per prefill tile (0 = prefill tiles off)
   int pf_min;        // sequences with at least this many query tokens take prefill tiles
   float pf_cost;     // cost of one prefill tile chunk in stream-K units (work split model)
@@ -403,6 +408,11 @@ struct HalfRegs<KV_BF16_SCALED> {
   u32x4 w[2][4];
 };
 template <>
+struct HalfRegs<KV_BF16_BIAS> {
+  u32x4 w[2][4];
+  float bias[2][4];  // K half only: raw table values for keys 16*blk + 4j + rr (validated at use)
+};
+template <>
 struct HalfRegs<KV_FP8> {
   u32x2 w[2][4];
   float sc[2];  // per-(page, kv head) scale of each of the lane's two keys (k_scale/v_scale not applied)
@@ -413,6 +423,8 @@ struct UnitAddr {
   size_t e[2];
   int pg[2];
   int h;
+  long long bias_at;  // KV_BF16_BIAS: table index of this lane's key c*32 + 4j (distance bias_d)
+  int bias_d;
 };
 
 __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
@@ -433,6 +445,13 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
     a.pg[blk] = pg;
     a.e[blk] = kv_elem(p, pg, kt, 2 * a.h) + 8 * j;
   }
+  // relative-bias table position of the scores this lane holds: row n, keys c*32 + 4j (+16*blk + rr)
+  const int row = x.rb * ROW_BLOCK + n;
+  const int tok = row / p.G;
+  const int pos = x.kv_len - x.q_len + tok;
+  a.bias_d = live ? pos - (x.c * KV_CHUNK + 4 * j) : -KV_CHUNK;
+  a.bias_at = live ? ((long long)x.i * p.Hq + (x.h * p.HG + wv) * p.G + (row - tok * p.G)) * p.rel_extent + a.bias_d
+                   : 0;
   return a;
 }
 
@@ -442,6 +461,18 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     const size_t e = a.e[blk] + (size_t)which * kD;
+    if constexpr (MODE == KV_BF16_BIAS) {
+      if (which == 0) {
+        // the lane's 8 bias values: unpredicated loads at clamped indices (always inside the
+        // table), zeroed at use when the distance is outside [0, rel_extent)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int d = a.bias_d - 16 * blk - rr;
+          const bool in = d >= 0 && d < p.rel_extent;
+          r.bias[blk][rr] = p.rel_bias[in ? a.bias_at - 16 * blk - rr : 0];
+        }
+      }
+    }
     if constexpr (MODE == KV_FP8) {
       const uint8_t* kp = p.kv + e;
 #pragma unroll
@@ -557,8 +588,10 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   // of the block sees in full (no window, no soft cap) needs no per-score masking.
   float xs[2][4];
   const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
-  const bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
-                     (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
+  bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
+               (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
+  // relative bias: a chunk whose keys are all at distance >= rel_extent from every row has none
+  if constexpr (MODE == KV_BF16_BIAS) plain = plain && (x.c + 1) * KV_CHUNK <= first_row_limit - p.rel_extent;
   if (plain) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -580,6 +613,10 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
           xv = sv * p.scale_log2;
         }
         int kt = key0 + 16 * blk + rr;
+        if constexpr (MODE == KV_BF16_BIAS) {
+          const int d = st.pos - kt;
+          if (d >= 0 && d < p.rel_extent) xv += kr.bias[blk][rr] * kLog2e;
+        }
         bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
         if (masked) xv += p.mask_log2;
         if (kt >= x.kv_len) xv = -INFINITY;
@@ -1432,7 +1469,7 @@ constexpr size_t kHeaderBytes = 256;
 
 struct DeviceInfo {
   int cus = 0;
-  int grid[3][9] = {};  // workgroups per launch, by kv mode and heads per workgroup (1..8)
+  int grid[kModes][9] = {};  // workgroups per launch, by kv mode and heads per workgroup (1..8)
 };
 
 std::mutex g_mu;
@@ -1481,6 +1518,7 @@ int device_info(DeviceInfo& out) {
       d.grid[KV_BF16][hg] = occupancy_grid<KV_BF16>(cus, hg);
       d.grid[KV_BF16_SCALED][hg] = occupancy_grid<KV_BF16_SCALED>(cus, hg);
       d.grid[KV_FP8][hg] = occupancy_grid<KV_FP8>(cus, hg);
+      d.grid[KV_BF16_BIAS][hg] = occupancy_grid<KV_BF16_BIAS>(cus, hg);
     }
     d.cus = cus;
   }
@@ -1526,6 +1564,93 @@ int check_shape(const rpa_shape_t* s) {
   return RPA_OK;
 }
 
+// ---------------------------------------------------------------------------------------------
+// fused Inkling decode: cache write, metadata expansion, bias table (small launches around the
+// attention kernel; src/tpu_cake/workloads/inkling_rpa.py:471-589)
+// ---------------------------------------------------------------------------------------------
+struct FusedArgs {
+  const uint16_t* q;        // [B, Hq, D]
+  const uint16_t* keys;     // [B, Hkv, D]
+  const uint16_t* values;   // [B, Hkv, D]
+  uint16_t* cache;          // [P, S, 2*Hkv, W]
+  const int32_t* kv_lens;   // [B]
+  const int32_t* pages;     // [page_entries]
+  const int32_t* cu_kv;     // [B+1]
+  const uint16_t* rel_states;  // [B, Hq, R]
+  const uint16_t* rel_proj;    // [R, E]
+  int32_t* table;           // [B, PPS]
+  int32_t* cu_q;            // [B+1]
+  int32_t* nseq;            // [1]
+  float* bias;              // [B, Hq, E]
+  uint16_t* qpad;           // [B, Hq, W] (when D < W)
+  int32_t* err;
+  int B, Hq, Hkv, D, P, S, W, entries, pps, R, E;
+};
+
+__device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// Block (s, combined row 2h + kv): the new token's K (kv = 0) or V row, zero-padded to W, at slot
+// (kv_len-1) % S of page pages[cu_kv[s]/S + (kv_len-1)/S].  Anything out of range is skipped and
+// flagged (the host preflight rejects such metadata before the launch).
+__global__ __launch_bounds__(128) void rpa_fused_write_kernel(FusedArgs a) {
+  const int s = blockIdx.x / (2 * a.Hkv), r = blockIdx.x - s * (2 * a.Hkv);
+  const int len = a.kv_lens[s], base = a.cu_kv[s];
+  const int pos = len - 1;
+  const long long entry = (long long)(base / a.S) + pos / a.S;
+  bool ok = len >= 1 && len <= a.pps * a.S && base >= 0 && base % a.S == 0 && entry < a.entries;
+  const int page = ok ? a.pages[entry] : 0;
+  ok = ok && page >= 0 && page < a.P;
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(a.err, ERR_PAGE);
+    return;
+  }
+  uint16_t* row = a.cache + (((size_t)page * a.S + pos % a.S) * (2 * a.Hkv) + r) * a.W;
+  const uint16_t* src = ((r & 1) ? a.values : a.keys) + ((size_t)s * a.Hkv + (r >> 1)) * a.D;
+  for (int d = threadIdx.x; d < a.W; d += blockDim.x) row[d] = d < a.D ? src[d] : (uint16_t)0;
+}
+
+// Grid-stride: the [B, pages_per_seq] page table, cu_q = 0..B, num_seqs = B, the padded queries
+// and the bias table bias[s, h, d] = sum_r states[s, h, r] * proj[r, d] (fp32).
+__global__ __launch_bounds__(256) void rpa_fused_prep_kernel(FusedArgs a) {
+  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x, stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = tid; i < (long long)a.B * a.pps; i += stride) {
+    const int s = (int)(i / a.pps), pg = (int)(i - (long long)s * a.pps);
+    const int len = a.kv_lens[s];
+    const long long e = (long long)(a.cu_kv[s] / a.S) + pg;
+    a.table[i] = (pg < (len + a.S - 1) / a.S && e >= 0 && e < a.entries) ? a.pages[e] : 0;
+  }
+  for (long long i = tid; i <= a.B; i += stride) a.cu_q[i] = (int32_t)i;
+  if (tid == 0) a.nseq[0] = a.B;
+  if (a.qpad)
+    for (long long i = tid; i < (long long)a.B * a.Hq * a.W; i += stride) {
+      const long long row = i / a.W;
+      const int d = (int)(i - row * a.W);
+      a.qpad[i] = d < a.D ? a.q[row * a.D + d] : (uint16_t)0;
+    }
+  if (a.bias)
+    for (long long i = tid; i < (long long)a.B * a.Hq * a.E; i += stride) {
+      const long long sh = i / a.E;
+      const int d = (int)(i - sh * a.E);
+      float acc = 0.f;
+      for (int r = 0; r < a.R; ++r) acc += bf16f(a.rel_states[sh * a.R + r]) * bf16f(a.rel_proj[(size_t)r * a.E + d]);
+      a.bias[i] = acc;
+    }
+}
+
+// out[s, h, :D] = padded[s, h, :D]
+__global__ __launch_bounds__(256) void rpa_fused_unpad_kernel(const uint16_t* padded, uint16_t* out, long long rows,
+                                                             int D, int W) {
+  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x, stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = tid; i < rows * D; i += stride) {
+    const long long row = i / D;
+    out[i] = padded[row * W + (i - row * D)];
+  }
+}
+
+struct FusedLayout {
+  size_t table, cu_q, nseq, bias, qpad, opad, total;
+};
+
 Params base_params(const rpa_shape_t* s) {
   Params p;
   memset(&p, 0, sizeof(p));
@@ -1542,6 +1667,56 @@ Params base_params(const rpa_shape_t* s) {
   p.HG = heads_per_group(p.Hkv);
   p.NG = p.Hkv / p.HG;
   return p;
+}
+
+// hipGetLastError reports the last failure of ANY runtime call on this thread (a caller's, or
+// the framework's); clear it before launching so a launch check reports this library's own.
+void clear_stale_error() { (void)hipGetLastError(); }
+
+int check_fused(const rpa_fused_shape_t* f) {
+  if (!f) return fail(RPA_E_INVALID, "fused shape is NULL");
+  if (f->num_seqs < 1 || f->num_q_heads < 1 || f->num_kv_heads < 1 || f->num_q_heads % f->num_kv_heads)
+    return fail(RPA_E_INVALID, "fused: bad sequence or head counts");
+  if (f->cache_width != kD) return fail(RPA_E_UNSUPPORTED, "fused: cache_width must be 128");
+  if (f->head_dim < 1 || f->head_dim > f->cache_width) return fail(RPA_E_INVALID, "fused: head_dim must be in [1, cache_width]");
+  if (f->total_pages < 1 || f->page_size < 1 || f->page_entries < 1 || f->pages_per_seq < 1)
+    return fail(RPA_E_INVALID, "fused: bad page counts");
+  if (f->relative_dim < 0 || (f->relative_dim > 0 && f->relative_extent < 1))
+    return fail(RPA_E_INVALID, "fused: bad relative bias shape");
+  if ((long long)f->pages_per_seq * f->page_size > INT32_MAX ||
+      (long long)f->num_seqs * f->pages_per_seq > INT32_MAX ||
+      (long long)f->num_seqs * f->num_q_heads * (f->relative_dim > 0 ? f->relative_extent : 1) > INT32_MAX)
+    return fail(RPA_E_INVALID, "fused: sizes overflow int32");
+  return RPA_OK;
+}
+
+rpa_shape_t fused_rpa_shape(const rpa_fused_shape_t* f) {
+  rpa_shape_t r;
+  r.num_tokens = f->num_seqs;
+  r.num_q_heads = f->num_q_heads;
+  r.num_kv_heads = f->num_kv_heads;
+  r.head_dim = kD;
+  r.total_pages = f->total_pages;
+  r.page_size = f->page_size;
+  r.max_num_seqs = f->num_seqs;
+  r.pages_per_seq = f->pages_per_seq;
+  r.kv_dtype = RPA_KV_BF16;
+  return r;
+}
+
+// [operator workspace][page table][cu_q][num_seqs][bias table][padded q][padded out]
+FusedLayout fused_layout(const DeviceInfo& d, const rpa_fused_shape_t* f) {
+  FusedLayout l;
+  const size_t B = (size_t)f->num_seqs, rows = B * f->num_q_heads;
+  const size_t pad = f->head_dim < kD ? rows * kD * 2 : 0;
+  l.table = round256(ws_layout(d).total);
+  l.cu_q = l.table + round256(B * f->pages_per_seq * 4);
+  l.nseq = l.cu_q + round256((B + 1) * 4);
+  l.bias = l.nseq + 256;
+  l.qpad = l.bias + round256(f->relative_dim > 0 ? rows * f->relative_extent * 4 : 0);
+  l.opad = l.qpad + round256(pad);
+  l.total = l.opad + pad;
+  return l;
 }
 
 }  // namespace
@@ -1585,7 +1760,8 @@ int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* 
 static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const void* q, const void* kv_pages,
                       const float* kv_scales, const int32_t* kv_lens, const int32_t* page_indices,
                       const int32_t* cu_q_lens, const int32_t* num_seqs, void* out, void* workspace,
-                      size_t workspace_bytes, void* stream, void* ev_begin, void* ev_end) {
+                      size_t workspace_bytes, void* stream, void* ev_begin, void* ev_end,
+                      const float* rel_bias = nullptr, int rel_extent = 0) {
   int rc = check_shape(shape);
   if (rc) return rc;
   if (!opt) return fail(RPA_E_INVALID, "options is NULL");
@@ -1603,6 +1779,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     return fail(RPA_E_WORKSPACE, "workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
                                      std::to_string(need));
 
+  clear_stale_error();
   Params p = base_params(shape);
   p.q = (const uint16_t*)q;
   p.kv = (const uint8_t*)kv_pages;
@@ -1627,7 +1804,13 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   p.v_scale = opt->has_v_scale ? opt->v_scale : 1.f;
 
   int mode = KV_BF16;
-  if (shape->kv_dtype == RPA_KV_FP8_E4M3) {
+  if (rel_bias) {
+    if (shape->kv_dtype != RPA_KV_BF16 || kv_scales || opt->has_k_scale || opt->has_v_scale || rel_extent <= 0)
+      return fail(RPA_E_INVALID, "a relative bias needs bf16 kv_pages without scales and a positive extent");
+    mode = KV_BF16_BIAS;
+    p.rel_bias = rel_bias;
+    p.rel_extent = rel_extent;
+  } else if (shape->kv_dtype == RPA_KV_FP8_E4M3) {
     mode = KV_FP8;
     p.kv_scales = kv_scales;
   } else {
@@ -1649,7 +1832,10 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   const bool upg = p.S % KV_CHUNK == 0;
   const dim3 grid(p.grid), block(64 * p.HG);
   const size_t lds = (size_t)p.HG * kVtBytes;
-  if (mode == KV_FP8) {
+  if (mode == KV_BF16_BIAS) {
+    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, true>), grid, block, lds, st, p);
+    else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, false>), grid, block, lds, st, p);
+  } else if (mode == KV_FP8) {
     if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, false>), grid, block, lds, st, p);
   } else if (mode == KV_BF16_SCALED) {
@@ -1706,6 +1892,95 @@ int rpa_gather_kv(const rpa_shape_t* shape, const void* kv_pages, const int32_t*
                      (uint8_t*)dense_out, (long long)dense_rows, elem);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("gather launch failed: ") + hipGetErrorString(e));
+  return RPA_OK;
+}
+
+size_t rpa_fused_workspace_size(const rpa_fused_shape_t* shape) {
+  if (check_fused(shape) != RPA_OK) return 0;
+  DeviceInfo d;
+  if (device_info(d) != RPA_OK) return 0;
+  return fused_layout(d, shape).total;
+}
+
+int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const void* queries, const void* keys,
+                             const void* values, void* cache, const int32_t* kv_lens, const int32_t* page_indices,
+                             const int32_t* cu_q_lens, const int32_t* cu_kv_lens, const int32_t* distribution,
+                             const void* relative_states, const void* relative_projection, void* out,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_fused(f);
+  if (rc) return rc;
+  clear_stale_error();
+  (void)cu_q_lens;     // decode-only contract: validated by the host preflight
+  (void)distribution;
+  if (!queries || !keys || !values || !cache || !kv_lens || !page_indices || !cu_kv_lens || !out)
+    return fail(RPA_E_INVALID, "fused: NULL pointer");
+  if (f->relative_dim > 0 && (!relative_states || !relative_projection))
+    return fail(RPA_E_INVALID, "fused: NULL relative bias tensors");
+  DeviceInfo d;
+  rc = device_info(d);
+  if (rc) return rc;
+  const FusedLayout l = fused_layout(d, f);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(RPA_E_WORKSPACE, "fused workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
+                                     std::to_string(l.total));
+  uint8_t* ws = (uint8_t*)workspace;
+  FusedArgs a;
+  a.q = (const uint16_t*)queries;
+  a.keys = (const uint16_t*)keys;
+  a.values = (const uint16_t*)values;
+  a.cache = (uint16_t*)cache;
+  a.kv_lens = kv_lens;
+  a.pages = page_indices;
+  a.cu_kv = cu_kv_lens;
+  a.rel_states = (const uint16_t*)relative_states;
+  a.rel_proj = (const uint16_t*)relative_projection;
+  a.table = (int32_t*)(ws + l.table);
+  a.cu_q = (int32_t*)(ws + l.cu_q);
+  a.nseq = (int32_t*)(ws + l.nseq);
+  a.bias = f->relative_dim > 0 ? (float*)(ws + l.bias) : nullptr;
+  a.qpad = f->head_dim < kD ? (uint16_t*)(ws + l.qpad) : nullptr;
+  a.err = (int32_t*)workspace;
+  a.B = f->num_seqs;
+  a.Hq = f->num_q_heads;
+  a.Hkv = f->num_kv_heads;
+  a.D = f->head_dim;
+  a.P = f->total_pages;
+  a.S = f->page_size;
+  a.W = f->cache_width;
+  a.entries = f->page_entries;
+  a.pps = f->pages_per_seq;
+  a.R = f->relative_dim;
+  a.E = f->relative_dim > 0 ? f->relative_extent : 0;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(rpa_fused_write_kernel, dim3(a.B * 2 * a.Hkv), dim3(128), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(RPA_E_HIP, std::string("fused write launch failed: ") + hipGetErrorString(e));
+  long long work = (long long)a.B * a.pps;
+  if (a.qpad) work = work > (long long)a.B * a.Hq * a.W ? work : (long long)a.B * a.Hq * a.W;
+  if (a.bias) work = work > (long long)a.B * a.Hq * a.E ? work : (long long)a.B * a.Hq * a.E;
+  long long blocks = (work + 255) / 256;
+  blocks = blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks);
+  hipLaunchKernelGGL(rpa_fused_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(RPA_E_HIP, std::string("fused prep launch failed: ") + hipGetErrorString(e));
+
+  const rpa_shape_t rs = fused_rpa_shape(f);
+  rpa_options_t o;
+  memset(&o, 0, sizeof(o));
+  o.sm_scale = sm_scale;
+  void* attn_out = a.qpad ? (void*)(ws + l.opad) : out;
+  rc = launch_rpa(&rs, &o, a.qpad ? (const void*)a.qpad : queries, cache, nullptr, kv_lens, a.table, a.cu_q, a.nseq,
+                  attn_out, workspace, workspace_bytes, stream, nullptr, nullptr, a.bias, a.E);
+  if (rc) return rc;
+  if (a.qpad) {
+    const long long rows = (long long)a.B * a.Hq;
+    long long ub = (rows * a.D + 255) / 256;
+    ub = ub < 1 ? 1 : (ub > 2048 ? 2048 : ub);
+    hipLaunchKernelGGL(rpa_fused_unpad_kernel, dim3((unsigned)ub), dim3(256), 0, st, (const uint16_t*)attn_out,
+                       (uint16_t*)out, rows, a.D, kD);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(RPA_E_HIP, std::string("fused unpad launch failed: ") + hipGetErrorString(e));
+  }
   return RPA_OK;
 }
 

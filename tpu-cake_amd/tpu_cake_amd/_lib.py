@@ -29,6 +29,8 @@ EXPORTED_SYMBOLS = (
     "rpa_ragged_paged_attention_timed",
     "rpa_gather_kv",
     "rpa_read_error_word",
+    "rpa_fused_workspace_size",
+    "rpa_inkling_fused_decode",
 )
 
 
@@ -57,6 +59,22 @@ class RpaOptions(ctypes.Structure):
         ("k_scale", ctypes.c_float),
         ("has_v_scale", ctypes.c_int32),
         ("v_scale", ctypes.c_float),
+    ]
+
+
+class RpaFusedShape(ctypes.Structure):
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("total_pages", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("cache_width", ctypes.c_int32),
+        ("page_entries", ctypes.c_int32),
+        ("pages_per_seq", ctypes.c_int32),
+        ("relative_dim", ctypes.c_int32),
+        ("relative_extent", ctypes.c_int32),
     ]
 
 
@@ -111,6 +129,11 @@ def load() -> ctypes.CDLL:
         lib.rpa_gather_kv.argtypes = [ctypes.POINTER(RpaShape), vp, vp, vp, vp, vp, ctypes.c_int64, vp, sz, vp]
         lib.rpa_read_error_word.restype = ctypes.c_int
         lib.rpa_read_error_word.argtypes = [vp, sz, i32p, vp]
+        lib.rpa_fused_workspace_size.restype = sz
+        lib.rpa_fused_workspace_size.argtypes = [ctypes.POINTER(RpaFusedShape)]
+        lib.rpa_inkling_fused_decode.restype = ctypes.c_int
+        # shape, sm_scale, 12 tensors (queries .. out), workspace, workspace_bytes, stream
+        lib.rpa_inkling_fused_decode.argtypes = [ctypes.POINTER(RpaFusedShape), ctypes.c_float] + [vp] * 13 + [sz, vp]
         version = lib.rpa_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{path}: ABI version {version}, expected {ABI_VERSION}")
