@@ -105,12 +105,124 @@ def measured_traffic(cfg: str):
     return data["configs"][cfg]["traffic_bytes"]
 
 
+def fused_cpu_baseline(case, budget_s: float = 20.0) -> dict:
+    """The fused-decode oracle (oracle/rpa_fused_oracle.py) on the first sequences of the step."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import rpa_fused_oracle as fo
+
+    a = case.arrays
+    n = len(a["kv_lengths"])
+    S = a["cache"].shape[1]
+
+    def subset(k):
+        pages = int(a["cu_kv_lens"][k]) // S
+        sub = dict(a)
+        for key in ("queries", "keys", "values", "kv_lengths", "relative_states"):
+            sub[key] = a[key][:k]
+        sub["cu_kv_lens"] = a["cu_kv_lens"][: k + 1]
+        sub["cu_q_lens"] = np.arange(k + 1, dtype=np.int32)
+        sub["distribution"] = np.full((3,), k, dtype=np.int32)
+        sub["page_indices"] = a["page_indices"][:pages]
+        sub["cache"] = a["cache"].reshape(a["cache"].shape[0], S, -1, 2, a["cache"].shape[-1])
+        return sub
+
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        fo.inkling_fused_rpa_reference(subset(1))
+        per_seq = max(time.perf_counter() - t0, 1e-3) / max(int(a["kv_lengths"][0]), 1)
+        k = 1
+        while k < n and per_seq * int(a["kv_lengths"][: k + 1].sum()) < budget_s:
+            k += 1
+        t0 = time.perf_counter()
+        fo.inkling_fused_rpa_reference(subset(k))
+        dt = time.perf_counter() - t0
+    toks = int(a["kv_lengths"][:k].sum())
+    kv_bytes = toks * a["keys"].shape[1] * 2 * 128 * 2
+    return {"value": round(kv_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "tokens_per_s": round(k / dt, 2), "seconds": round(dt, 3),
+            "sample": f"first {k} of {n} sequences ({toks} KV tokens, {k} decode steps) of the same step"}
+
+
+def fused_bench(args, dev) -> int:
+    """One step = one fused Inkling decode call (cache write + prep + attention + combine)."""
+    import numpy as np
+    import torch
+
+    from tpu_cake_amd import fused
+    from tpu_cake_amd.workloads import FUSED_DESCRIPTION, make_fused_case
+
+    t0 = time.perf_counter()
+    case = make_fused_case(seed=args.seed if args.seed is not None else 102)
+    log(f"built inkling in {time.perf_counter() - t0:.1f}s")
+    a = case.arrays
+    tensors = []
+    for name in fused.INPUT_NAMES:
+        x = a[name]
+        t = torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16) if x.dtype == np.uint16 else \
+            torch.from_numpy(np.ascontiguousarray(x))
+        tensors.append(t.to(dev))
+    fused.preflight(*tensors)  # the reference's run_preflighted check, once per metadata layout
+    cache_bytes = tensors[3].numel() * 2
+    copies = max(2, math.ceil(args.rotate_bytes / cache_bytes))
+    caches = [tensors[3]] + [tensors[3].clone() for _ in range(copies - 1)]
+    S = tensors[3].shape[1]
+    pps = int(((a["kv_lengths"].astype(np.int64) + S - 1) // S).max())
+    out = torch.empty_like(tensors[0])
+
+    def call(i):
+        xs = list(tensors)
+        xs[3] = caches[i % copies]
+        fused.invoke(*xs, sm_scale=case.sm_scale, pages_per_seq=pps, out=out)
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        call(i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = start.elapsed_time(stop) / args.steps
+    nseq, hq = a["queries"].shape[:2]
+    kv_bytes = case.kv_read_bytes()
+    moved = kv_bytes + 2 * nseq * hq * 128 * 2 + 2 * a["keys"].size * 2 * 2
+    value = kv_bytes / (ms_step * 1e-3) / 1e9
+    achieved = moved / (ms_step * 1e-3) / 1e9
+    result = {
+        "metric": "Inkling fused decode KV-read GB/s (% of HBM peak) + tokens/s, 64-seq bf16 GQA, 1 GPU",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: seeded N(0,1) queries / new K,V, N(0,0.25) cache, N(0,0.4) relative tensors",
+        "config": {"workload": f"inkling: {FUSED_DESCRIPTION}", "num_seqs": int(nseq),
+                   "sum_kv_len": int(a["kv_lengths"].sum()), "kv_bytes_per_step": kv_bytes,
+                   "cache_copies_rotated": copies},
+        "tokens_per_s": round(nseq / (ms_step * 1e-3), 1),
+        "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
+        "wall_s_timed_region": round(wall, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "basis": "whole step (cache write, metadata and bias-table kernels, attention, combine)"},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (fused oracle) ...")
+        result["cpu_baseline"] = fused_cpu_baseline(case)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "inkling"],
+                    help="c1..c5: the RPA operator configurations; inkling: the fused decode step "
+                         "(KV-cache write + relative-bias attention)")
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--rotate-bytes", type=float, default=2.0e9,
                     help="KV pool copies rotated so that at least this many bytes separate reuses")
@@ -147,6 +259,9 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
         return 0
+
+    if args.config == "inkling":
+        return fused_bench(args, dev)
 
     t0 = time.perf_counter()
     case = make_config(args.config, seed=args.seed)

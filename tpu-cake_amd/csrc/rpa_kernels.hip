@@ -103,8 +103,9 @@ struct Params {
   float k_scale, v_scale;
   int grid;
   bool skip_masked;  // mask value so negative that masked keys get weight exactly 0
-  const float* rel_bias;  // KV_BF16_BIAS: [num_seqs, Hq, rel_extent] fp32, added to the scaled score of a
-                          // key at distance d = pos - key < rel_extent from its query row
+  const float* rel_bias;  // KV_BF16_BIAS: per (sequence, q head) row of bias_row_len(E) fp32 by KEY
+                          // position (bias_key_base): the bias of key kt, 0 outside the window of the
+                          // rel_extent keys nearest the (single) query row, added to its scaled score
   int rel_extent;
   int pf_tq;         // tokens per prefill tile (0 = prefill tiles off)
   int pf_min;        // sequences with at least this many query tokens take prefill tiles
@@ -410,8 +411,19 @@ struct HalfRegs<KV_BF16_SCALED> {
 template <>
 struct HalfRegs<KV_BF16_BIAS> {
   u32x4 w[2][4];
-  float bias[2][4];  // K half only: raw table values for keys 16*blk + 4j + rr (validated at use)
+  f32x4 bias[2];  // K half only: bias of keys 16*blk + 4j + rr (0 outside the window)
 };
+
+// Relative-bias table layout (decode rows: one query position pos = kv_len - 1 per sequence):
+// row (s, h) holds the bias of key kt at index kt - bias_key_base(kv_len, E), where the base is a
+// multiple of 4 at least 4 below the first key of the window (kv_len - E), so each lane's 4
+// consecutive keys (a multiple-of-4 start) are one aligned 16-byte load; indices outside the row
+// and the entries for keys outside the window are 0.
+__host__ __device__ __forceinline__ int bias_row_len(int E) { return (E + 12 + 3) / 4 * 4; }
+__host__ __device__ __forceinline__ int bias_key_base(int kv_len, int E) {
+  const int lo = kv_len - E;
+  return ((lo >> 2) << 2) - 4;  // arithmetic shift: floors negative values too
+}
 template <>
 struct HalfRegs<KV_FP8> {
   u32x2 w[2][4];
@@ -423,8 +435,7 @@ struct UnitAddr {
   size_t e[2];
   int pg[2];
   int h;
-  long long bias_at;  // KV_BF16_BIAS: table index of this lane's key c*32 + 4j (distance bias_d)
-  int bias_d;
+  long long bias_at[2];  // KV_BF16_BIAS: table index of this lane's keys c*32 + 16*blk + 4j .. +3
 };
 
 __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
@@ -445,13 +456,17 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
     a.pg[blk] = pg;
     a.e[blk] = kv_elem(p, pg, kt, 2 * a.h) + 8 * j;
   }
-  // relative-bias table position of the scores this lane holds: row n, keys c*32 + 4j (+16*blk + rr)
+  // relative-bias table position of the scores this lane holds: row n, keys c*32 + 16*blk + 4j .. +3
   const int row = x.rb * ROW_BLOCK + n;
   const int tok = row / p.G;
-  const int pos = x.kv_len - x.q_len + tok;
-  a.bias_d = live ? pos - (x.c * KV_CHUNK + 4 * j) : -KV_CHUNK;
-  a.bias_at = live ? ((long long)x.i * p.Hq + (x.h * p.HG + wv) * p.G + (row - tok * p.G)) * p.rel_extent + a.bias_d
-                   : 0;
+  const int len = bias_row_len(p.rel_extent);
+  const long long row_base =
+      ((long long)x.i * p.Hq + (x.h * p.HG + wv) * p.G + (row - tok * p.G)) * len;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk) {
+    const int t = x.c * KV_CHUNK + 16 * blk + 4 * j - bias_key_base(x.kv_len, p.rel_extent);
+    a.bias_at[blk] = (live && t >= 0 && t + 4 <= len) ? row_base + t : 0;  // 0: the first row's zero head
+  }
   return a;
 }
 
@@ -462,16 +477,7 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
   for (int blk = 0; blk < 2; ++blk) {
     const size_t e = a.e[blk] + (size_t)which * kD;
     if constexpr (MODE == KV_BF16_BIAS) {
-      if (which == 0) {
-        // the lane's 8 bias values: unpredicated loads at clamped indices (always inside the
-        // table), zeroed at use when the distance is outside [0, rel_extent)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int d = a.bias_d - 16 * blk - rr;
-          const bool in = d >= 0 && d < p.rel_extent;
-          r.bias[blk][rr] = p.rel_bias[in ? a.bias_at - 16 * blk - rr : 0];
-        }
-      }
+      if (which == 0) r.bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at[blk]);  // unpredicated, aligned
     }
     if constexpr (MODE == KV_FP8) {
       const uint8_t* kp = p.kv + e;
@@ -590,13 +596,15 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
   bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
                (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
-  // relative bias: a chunk whose keys are all at distance >= rel_extent from every row has none
-  if constexpr (MODE == KV_BF16_BIAS) plain = plain && (x.c + 1) * KV_CHUNK <= first_row_limit - p.rel_extent;
   if (plain) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       xs[0][rr] = s0[rr] * p.scale_log2;
       xs[1][rr] = s1[rr] * p.scale_log2;
+      if constexpr (MODE == KV_BF16_BIAS) {  // the table holds 0 for keys outside the window
+        xs[0][rr] += kr.bias[0][rr] * kLog2e;
+        xs[1][rr] += kr.bias[1][rr] * kLog2e;
+      }
     }
   } else {
     const int key0 = x.c * KV_CHUNK + 4 * j;
@@ -613,10 +621,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
           xv = sv * p.scale_log2;
         }
         int kt = key0 + 16 * blk + rr;
-        if constexpr (MODE == KV_BF16_BIAS) {
-          const int d = st.pos - kt;
-          if (d >= 0 && d < p.rel_extent) xv += kr.bias[blk][rr] * kLog2e;
-        }
+        if constexpr (MODE == KV_BF16_BIAS) xv += kr.bias[blk][rr] * kLog2e;
         bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
         if (masked) xv += p.mask_log2;
         if (kt >= x.kv_len) xv = -INFINITY;
@@ -1568,6 +1573,8 @@ int check_shape(const rpa_shape_t* s) {
 // fused Inkling decode: cache write, metadata expansion, bias table (small launches around the
 // attention kernel; src/tpu_cake/workloads/inkling_rpa.py:471-589)
 // ---------------------------------------------------------------------------------------------
+constexpr int kMaxRelDim = 256;
+
 struct FusedArgs {
   const uint16_t* q;        // [B, Hq, D]
   const uint16_t* keys;     // [B, Hkv, D]
@@ -1589,11 +1596,11 @@ struct FusedArgs {
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-// Block (s, combined row 2h + kv): the new token's K (kv = 0) or V row, zero-padded to W, at slot
-// (kv_len-1) % S of page pages[cu_kv[s]/S + (kv_len-1)/S].  Anything out of range is skipped and
-// flagged (the host preflight rejects such metadata before the launch).
-__global__ __launch_bounds__(128) void rpa_fused_write_kernel(FusedArgs a) {
-  const int s = blockIdx.x / (2 * a.Hkv), r = blockIdx.x - s * (2 * a.Hkv);
+// Block index blk = (s, combined row 2h + kv): the new token's K (kv = 0) or V row, zero-padded to
+// W, at slot (kv_len-1) % S of page pages[cu_kv[s]/S + (kv_len-1)/S].  Anything out of range is
+// skipped and flagged (the host preflight rejects such metadata before the launch).
+__device__ __forceinline__ void fused_write_row(const FusedArgs& a, int blk) {
+  const int s = blk / (2 * a.Hkv), r = blk - s * (2 * a.Hkv);
   const int len = a.kv_lens[s], base = a.cu_kv[s];
   const int pos = len - 1;
   const long long entry = (long long)(base / a.S) + pos / a.S;
@@ -1609,10 +1616,35 @@ __global__ __launch_bounds__(128) void rpa_fused_write_kernel(FusedArgs a) {
   for (int d = threadIdx.x; d < a.W; d += blockDim.x) row[d] = d < a.D ? src[d] : (uint16_t)0;
 }
 
-// Grid-stride: the [B, pages_per_seq] page table, cu_q = 0..B, num_seqs = B, the padded queries
-// and the bias table bias[s, h, d] = sum_r states[s, h, r] * proj[r, d] (fp32).
-__global__ __launch_bounds__(256) void rpa_fused_prep_kernel(FusedArgs a) {
-  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x, stride = (long long)gridDim.x * blockDim.x;
+// One launch before the attention kernel: blocks [0, B*2*Hkv) write the new tokens' rows, the next
+// B*Hq blocks the bias table rows (bias of key at distance d = sum_r states[s, h, r] * proj[r, d],
+// fp32), the rest, grid-stride, the [B, pages_per_seq] page table, cu_q = 0..B, num_seqs = B and
+// the padded queries.
+__global__ __launch_bounds__(256) void rpa_fused_prep_kernel(FusedArgs a, int write_blocks, int bias_blocks) {
+  __shared__ float states[kMaxRelDim];
+  if ((int)blockIdx.x < write_blocks) {
+    fused_write_row(a, blockIdx.x);
+    return;
+  }
+  if ((int)blockIdx.x < write_blocks + bias_blocks) {
+    // bias table row (s, h), by key position (bias_key_base)
+    const int sh = blockIdx.x - write_blocks, s = sh / a.Hq;
+    for (int r = threadIdx.x; r < a.R; r += blockDim.x) states[r] = bf16f(a.rel_states[(size_t)sh * a.R + r]);
+    __syncthreads();
+    const int len = bias_row_len(a.E), kv_len = a.kv_lens[s], base = bias_key_base(kv_len, a.E);
+    float* row = a.bias + (size_t)sh * len;
+    for (int t = threadIdx.x; t < len; t += blockDim.x) {
+      const int d = (kv_len - 1) - (base + t);
+      float acc = 0.f;
+      if (d >= 0 && d < a.E)
+        for (int r = 0; r < a.R; ++r) acc += states[r] * bf16f(a.rel_proj[(size_t)r * a.E + d]);
+      row[t] = acc;
+    }
+    return;
+  }
+  const int first = write_blocks + bias_blocks;
+  const long long tid = (long long)(blockIdx.x - first) * blockDim.x + threadIdx.x,
+                  stride = (long long)(gridDim.x - first) * blockDim.x;
   for (long long i = tid; i < (long long)a.B * a.pps; i += stride) {
     const int s = (int)(i / a.pps), pg = (int)(i - (long long)s * a.pps);
     const int len = a.kv_lens[s];
@@ -1626,14 +1658,6 @@ __global__ __launch_bounds__(256) void rpa_fused_prep_kernel(FusedArgs a) {
       const long long row = i / a.W;
       const int d = (int)(i - row * a.W);
       a.qpad[i] = d < a.D ? a.q[row * a.D + d] : (uint16_t)0;
-    }
-  if (a.bias)
-    for (long long i = tid; i < (long long)a.B * a.Hq * a.E; i += stride) {
-      const long long sh = i / a.E;
-      const int d = (int)(i - sh * a.E);
-      float acc = 0.f;
-      for (int r = 0; r < a.R; ++r) acc += bf16f(a.rel_states[sh * a.R + r]) * bf16f(a.rel_proj[(size_t)r * a.E + d]);
-      a.bias[i] = acc;
     }
 }
 
@@ -1681,8 +1705,8 @@ int check_fused(const rpa_fused_shape_t* f) {
   if (f->head_dim < 1 || f->head_dim > f->cache_width) return fail(RPA_E_INVALID, "fused: head_dim must be in [1, cache_width]");
   if (f->total_pages < 1 || f->page_size < 1 || f->page_entries < 1 || f->pages_per_seq < 1)
     return fail(RPA_E_INVALID, "fused: bad page counts");
-  if (f->relative_dim < 0 || (f->relative_dim > 0 && f->relative_extent < 1))
-    return fail(RPA_E_INVALID, "fused: bad relative bias shape");
+  if (f->relative_dim < 0 || f->relative_dim > kMaxRelDim || (f->relative_dim > 0 && f->relative_extent < 1))
+    return fail(RPA_E_INVALID, "fused: relative_dim must be in [0, 256] with a positive extent");
   if ((long long)f->pages_per_seq * f->page_size > INT32_MAX ||
       (long long)f->num_seqs * f->pages_per_seq > INT32_MAX ||
       (long long)f->num_seqs * f->num_q_heads * (f->relative_dim > 0 ? f->relative_extent : 1) > INT32_MAX)
@@ -1713,7 +1737,7 @@ FusedLayout fused_layout(const DeviceInfo& d, const rpa_fused_shape_t* f) {
   l.cu_q = l.table + round256(B * f->pages_per_seq * 4);
   l.nseq = l.cu_q + round256((B + 1) * 4);
   l.bias = l.nseq + 256;
-  l.qpad = l.bias + round256(f->relative_dim > 0 ? rows * f->relative_extent * 4 : 0);
+  l.qpad = l.bias + round256(f->relative_dim > 0 ? rows * bias_row_len(f->relative_extent) * 4 : 0);
   l.opad = l.qpad + round256(pad);
   l.total = l.opad + pad;
   return l;
@@ -1952,16 +1976,14 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
   a.R = f->relative_dim;
   a.E = f->relative_dim > 0 ? f->relative_extent : 0;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(rpa_fused_write_kernel, dim3(a.B * 2 * a.Hkv), dim3(128), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(RPA_E_HIP, std::string("fused write launch failed: ") + hipGetErrorString(e));
+  const int write_blocks = a.B * 2 * a.Hkv, bias_blocks = a.bias ? a.B * a.Hq : 0;
   long long work = (long long)a.B * a.pps;
   if (a.qpad) work = work > (long long)a.B * a.Hq * a.W ? work : (long long)a.B * a.Hq * a.W;
-  if (a.bias) work = work > (long long)a.B * a.Hq * a.E ? work : (long long)a.B * a.Hq * a.E;
   long long blocks = (work + 255) / 256;
   blocks = blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks);
-  hipLaunchKernelGGL(rpa_fused_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
-  e = hipGetLastError();
+  hipLaunchKernelGGL(rpa_fused_prep_kernel, dim3((unsigned)(write_blocks + bias_blocks + blocks)), dim3(256), 0, st, a,
+                     write_blocks, bias_blocks);
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("fused prep launch failed: ") + hipGetErrorString(e));
 
   const rpa_shape_t rs = fused_rpa_shape(f);

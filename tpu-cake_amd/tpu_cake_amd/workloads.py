@@ -247,3 +247,63 @@ def make_custom(*, kv_lens, q_lens, num_q_heads, num_kv_heads, head_dim=128, pag
     if kv_dtype == "fp8":
         case = quantize_fp8(case)
     return case
+
+
+# ---------------------------------------------------------------------------------------------
+# the fused Inkling decode step (v3 contract, src/tpu_cake/workloads/inkling_rpa.py:413-589)
+# ---------------------------------------------------------------------------------------------
+FUSED_DESCRIPTION = ("inkling fused decode: C2 lengths (64 seqs, lognormal median 2048) incl. the new token, "
+                     "Hq 32 / Hkv 8, D 128, page 64, relative bias R 16 / E 512, cache write + attention")
+
+
+@dataclasses.dataclass
+class FusedCase:
+    """Inputs of one fused decode step in the reference's order (``fused.INPUT_NAMES``): bf16
+    tensors as uint16 bits, metadata int32."""
+    arrays: dict
+    sm_scale: float
+
+    def kv_read_bytes(self) -> int:
+        n_kv = self.arrays["keys"].shape[1]
+        return int(self.arrays["kv_lengths"].astype(np.int64).sum()) * n_kv * 2 * 128 * 2
+
+
+def make_fused_case(seed: int = 102, *, nseq: int = 64, num_q_heads: int = 32, num_kv_heads: int = 8,
+                    head_dim: int = 128, page_size: int = 64, relative_dim: int = 16, relative_extent: int = 512,
+                    values: str = "auto", lengths=None) -> FusedCase:
+    """A fused decode step at Inkling decode shapes: page-aligned cumulative KV lengths and a
+    seeded permutation of a 1.25x pool as the flat page list (each sequence's pages consecutive
+    in it), N(0,1) queries / new K,V, N(0, 0.25) cache, N(0, 0.4) relative tensors (the
+    reference fixture's scales, inkling_rpa.py:413-424)."""
+    rng = np.random.default_rng(seed)
+    if lengths is None:
+        z = rng.standard_normal(nseq)
+        lengths = np.clip(np.round(np.exp(math.log(2048.0) + LOGNORMAL_SIGMA * z)), 128, 8192)
+    lengths = np.asarray(lengths, dtype=np.int32)
+    pages_needed = -(-lengths // page_size)
+    pool = int(math.ceil(POOL_FACTOR * int(pages_needed.sum())))
+    perm = rng.permutation(pool).astype(np.int32)
+    cu_kv = np.concatenate(([0], np.cumsum(pages_needed * page_size))).astype(np.int32)
+    v = _resolve_values(values)
+
+    def normal(shape, scale, stream):  # N(0, scale^2) float32 rounded to bf16
+        if v == "cuda":
+            g = torch.Generator(device="cuda").manual_seed(int(seed) * 16 + stream)
+            x = torch.randn(shape, generator=g, device="cuda", dtype=torch.float32) * scale
+            return x.to(torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+        return f32_to_bf16_bits(rng.standard_normal(size=shape, dtype=np.float32) * np.float32(scale))
+
+    arrays = {
+        "queries": normal((nseq, num_q_heads, head_dim), 1.0, 3),
+        "keys": normal((nseq, num_kv_heads, head_dim), 1.0, 4),
+        "values": normal((nseq, num_kv_heads, head_dim), 1.0, 5),
+        "cache": normal((pool, page_size, 2 * num_kv_heads, 128), 0.25, 6),
+        "kv_lengths": lengths,
+        "page_indices": perm[: int(pages_needed.sum())].copy(),
+        "cu_q_lens": np.arange(nseq + 1, dtype=np.int32),
+        "cu_kv_lens": cu_kv,
+        "distribution": np.full((3,), nseq, dtype=np.int32),
+        "relative_states": normal((nseq, num_q_heads, relative_dim), 0.4, 7),
+        "relative_projection": normal((relative_dim, relative_extent), 0.4, 8),
+    }
+    return FusedCase(arrays=arrays, sm_scale=1.0 / head_dim)
