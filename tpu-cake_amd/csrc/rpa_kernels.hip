@@ -103,9 +103,9 @@ struct Params {
   float k_scale, v_scale;
   int grid;
   bool skip_masked;  // mask value so negative that masked keys get weight exactly 0
-  const float* rel_bias;  // KV_BF16_BIAS: per (sequence, q head) row of bias_row_len(E) fp32 by KEY
-                          // position (bias_key_base): the bias of key kt, 0 outside the window of the
-                          // rel_extent keys nearest the (single) query row, added to its scaled score
+  const float* rel_bias;  // KV_BF16_BIAS: fp32 table by KEY position (bias_chunk_lo): the bias of each
+                          // key, 0 outside the window of the rel_extent keys nearest the (single)
+                          // query row, added to its scaled score
   int rel_extent;
   int pf_tq;         // tokens per prefill tile (0 = prefill tiles off)
   int pf_min;        // sequences with at least this many query tokens take prefill tiles
@@ -415,15 +415,14 @@ struct HalfRegs<KV_BF16_BIAS> {
 };
 
 // Relative-bias table layout (decode rows: one query position pos = kv_len - 1 per sequence):
-// row (s, h) holds the bias of key kt at index kt - bias_key_base(kv_len, E), where the base is a
-// multiple of 4 at least 4 below the first key of the window (kv_len - E), so each lane's 4
-// consecutive keys (a multiple-of-4 start) are one aligned 16-byte load; indices outside the row
-// and the entries for keys outside the window are 0.
-__host__ __device__ __forceinline__ int bias_row_len(int E) { return (E + 12 + 3) / 4 * 4; }
-__host__ __device__ __forceinline__ int bias_key_base(int kv_len, int E) {
-  const int lo = kv_len - E;
-  return ((lo >> 2) << 2) - 4;  // arithmetic shift: floors negative values too
-}
+// kBiasHead zeros, then one row of bias_row_len(E) entries per (sequence s, q head h).  Entry t of
+// a row is the bias of key 32 * bias_chunk_lo(kv_len, E) + t: the first 32-key chunk that holds a
+// key of the window [kv_len - E, kv_len - 1], so every chunk from there to the end of the sequence
+// lies inside the row, and entries of keys outside the window are 0.  A lane's 4 consecutive keys
+// (a multiple-of-4 start) are one aligned 16-byte load; chunks before the window read the zero head.
+constexpr int kBiasHead = 32;
+__host__ __device__ __forceinline__ int bias_row_len(int E) { return ((E + 31) / 32 + 1) * 32; }
+__host__ __device__ __forceinline__ int bias_chunk_lo(int kv_len, int E) { return kv_len > E ? (kv_len - E) / 32 : 0; }
 template <>
 struct HalfRegs<KV_FP8> {
   u32x2 w[2][4];
@@ -435,7 +434,7 @@ struct UnitAddr {
   size_t e[2];
   int pg[2];
   int h;
-  long long bias_at[2];  // KV_BF16_BIAS: table index of this lane's keys c*32 + 16*blk + 4j .. +3
+  int bias_at;  // KV_BF16_BIAS: table index of this lane's keys c*32 + 4j .. +3 (+16 for the second block)
 };
 
 __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
@@ -456,17 +455,13 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
     a.pg[blk] = pg;
     a.e[blk] = kv_elem(p, pg, kt, 2 * a.h) + 8 * j;
   }
-  // relative-bias table position of the scores this lane holds: row n, keys c*32 + 16*blk + 4j .. +3
+  // relative-bias table position of the scores this lane holds: row n, keys c*32 + 4j .. +3 (the
+  // host keeps every index below 2^31); chunks before the window read the zero head
   const int row = x.rb * ROW_BLOCK + n;
-  const int tok = row / p.G;
-  const int len = bias_row_len(p.rel_extent);
-  const long long row_base =
-      ((long long)x.i * p.Hq + (x.h * p.HG + wv) * p.G + (row - tok * p.G)) * len;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const int t = x.c * KV_CHUNK + 16 * blk + 4 * j - bias_key_base(x.kv_len, p.rel_extent);
-    a.bias_at[blk] = (live && t >= 0 && t + 4 <= len) ? row_base + t : 0;  // 0: the first row's zero head
-  }
+  const int lo = bias_chunk_lo(x.kv_len, p.rel_extent);
+  const int at = kBiasHead + (x.i * p.Hq + (x.h * p.HG + wv) * p.G + row % p.G) * bias_row_len(p.rel_extent) +
+                 (x.c - lo) * KV_CHUNK + 4 * j;
+  a.bias_at = live && x.c >= lo ? at : 0;
   return a;
 }
 
@@ -477,7 +472,7 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
   for (int blk = 0; blk < 2; ++blk) {
     const size_t e = a.e[blk] + (size_t)which * kD;
     if constexpr (MODE == KV_BF16_BIAS) {
-      if (which == 0) r.bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at[blk]);  // unpredicated, aligned
+      if (which == 0) r.bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at + 16 * blk);  // aligned
     }
     if constexpr (MODE == KV_FP8) {
       const uint8_t* kp = p.kv + e;
@@ -1574,6 +1569,8 @@ int check_shape(const rpa_shape_t* s) {
 // attention kernel; src/tpu_cake/workloads/inkling_rpa.py:471-589)
 // ---------------------------------------------------------------------------------------------
 constexpr int kMaxRelDim = 256;
+constexpr int kBiasHeads = 4;    // q heads per bias-table block
+constexpr int kBiasSlab = 256;   // table entries per bias-table block (one per thread)
 
 struct FusedArgs {
   const uint16_t* q;        // [B, Hq, D]
@@ -1588,19 +1585,19 @@ struct FusedArgs {
   int32_t* table;           // [B, PPS]
   int32_t* cu_q;            // [B+1]
   int32_t* nseq;            // [1]
-  float* bias;              // [B, Hq, E]
+  float* bias;              // kBiasHead zeros + [B, Hq, bias_row_len(E)]
   uint16_t* qpad;           // [B, Hq, W] (when D < W)
   int32_t* err;
   int B, Hq, Hkv, D, P, S, W, entries, pps, R, E;
+  int vec;  // cache, keys and values 16-byte aligned and D % 8 == 0: rows written 8 elements at a time
 };
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-// Block index blk = (s, combined row 2h + kv): the new token's K (kv = 0) or V row, zero-padded to
-// W, at slot (kv_len-1) % S of page pages[cu_kv[s]/S + (kv_len-1)/S].  Anything out of range is
+// Block s: the new token's 2*Hkv rows (K of kv head h at combined row 2h, V at 2h+1), zero-padded
+// to W, at slot (kv_len-1) % S of page pages[cu_kv[s]/S + (kv_len-1)/S].  Anything out of range is
 // skipped and flagged (the host preflight rejects such metadata before the launch).
-__device__ __forceinline__ void fused_write_row(const FusedArgs& a, int blk) {
-  const int s = blk / (2 * a.Hkv), r = blk - s * (2 * a.Hkv);
+__device__ __forceinline__ void fused_write_rows(const FusedArgs& a, int s) {
   const int len = a.kv_lens[s], base = a.cu_kv[s];
   const int pos = len - 1;
   const long long entry = (long long)(base / a.S) + pos / a.S;
@@ -1611,35 +1608,56 @@ __device__ __forceinline__ void fused_write_row(const FusedArgs& a, int blk) {
     if (threadIdx.x == 0) atomicOr(a.err, ERR_PAGE);
     return;
   }
-  uint16_t* row = a.cache + (((size_t)page * a.S + pos % a.S) * (2 * a.Hkv) + r) * a.W;
-  const uint16_t* src = ((r & 1) ? a.values : a.keys) + ((size_t)s * a.Hkv + (r >> 1)) * a.D;
-  for (int d = threadIdx.x; d < a.W; d += blockDim.x) row[d] = d < a.D ? src[d] : (uint16_t)0;
+  uint16_t* rows = a.cache + ((size_t)page * a.S + pos % a.S) * (2 * a.Hkv) * a.W;
+  const int n = 2 * a.Hkv * a.W;
+  if (a.vec) {
+    for (int i = 8 * threadIdx.x; i < n; i += 8 * blockDim.x) {
+      const int r = i / a.W, d = i - r * a.W;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (d < a.D) v = *(const u32x4*)(((r & 1) ? a.values : a.keys) + ((size_t)s * a.Hkv + (r >> 1)) * a.D + d);
+      *(u32x4*)(rows + i) = v;
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int r = i / a.W, d = i - r * a.W;
+      rows[i] = d < a.D ? ((r & 1) ? a.values : a.keys)[((size_t)s * a.Hkv + (r >> 1)) * a.D + d] : (uint16_t)0;
+    }
+  }
 }
 
-// One launch before the attention kernel: blocks [0, B*2*Hkv) write the new tokens' rows, the next
-// B*Hq blocks the bias table rows (bias of key at distance d = sum_r states[s, h, r] * proj[r, d],
-// fp32), the rest, grid-stride, the [B, pages_per_seq] page table, cu_q = 0..B, num_seqs = B and
-// the padded queries.
+// One launch before the attention kernel (256 threads a block): blocks [0, B) write the new
+// tokens' rows; the next B * ceil(Hq/kBiasHeads) * ceil(len/kBiasSlab) blocks the bias table
+// (entry t of rows (s, h0..h0+3): the bias of the key at distance d = sum_r states[s, h, r] *
+// proj[r, d] in fp32, 0 outside the window); the rest, grid-stride, the zero head, the
+// [B, pages_per_seq] page table, cu_q = 0..B, num_seqs = B and the padded queries.
 __global__ __launch_bounds__(256) void rpa_fused_prep_kernel(FusedArgs a, int write_blocks, int bias_blocks) {
-  __shared__ float states[kMaxRelDim];
+  __shared__ float states[kBiasHeads * kMaxRelDim];
   if ((int)blockIdx.x < write_blocks) {
-    fused_write_row(a, blockIdx.x);
+    fused_write_rows(a, blockIdx.x);
     return;
   }
   if ((int)blockIdx.x < write_blocks + bias_blocks) {
-    // bias table row (s, h), by key position (bias_key_base)
-    const int sh = blockIdx.x - write_blocks, s = sh / a.Hq;
-    for (int r = threadIdx.x; r < a.R; r += blockDim.x) states[r] = bf16f(a.rel_states[(size_t)sh * a.R + r]);
+    const int len = bias_row_len(a.E), slabs = (len + kBiasSlab - 1) / kBiasSlab;
+    const int hgroups = (a.Hq + kBiasHeads - 1) / kBiasHeads;
+    const int nb = blockIdx.x - write_blocks, s = nb / (hgroups * slabs), rem = nb - s * hgroups * slabs;
+    const int h0 = (rem / slabs) * kBiasHeads, t = (rem - (rem / slabs) * slabs) * kBiasSlab + threadIdx.x;
+    for (int i = threadIdx.x; i < kBiasHeads * a.R; i += blockDim.x)
+      states[i] = h0 + i / a.R < a.Hq ? bf16f(a.rel_states[((size_t)s * a.Hq + h0) * a.R + i]) : 0.f;
     __syncthreads();
-    const int len = bias_row_len(a.E), kv_len = a.kv_lens[s], base = bias_key_base(kv_len, a.E);
-    float* row = a.bias + (size_t)sh * len;
-    for (int t = threadIdx.x; t < len; t += blockDim.x) {
-      const int d = (kv_len - 1) - (base + t);
-      float acc = 0.f;
-      if (d >= 0 && d < a.E)
-        for (int r = 0; r < a.R; ++r) acc += states[r] * bf16f(a.rel_proj[(size_t)r * a.E + d]);
-      row[t] = acc;
+    const int kv_len = a.kv_lens[s], d = (kv_len - 1) - (32 * bias_chunk_lo(kv_len, a.E) + t);
+    float acc[kBiasHeads] = {};
+    if (t < len && d >= 0 && d < a.E) {
+#pragma unroll 16
+      for (int r = 0; r < a.R; ++r) {
+        const float pv = bf16f(a.rel_proj[(size_t)r * a.E + d]);
+#pragma unroll
+        for (int h = 0; h < kBiasHeads; ++h) acc[h] += states[h * a.R + r] * pv;
+      }
     }
+    if (t < len)
+#pragma unroll
+      for (int h = 0; h < kBiasHeads; ++h)
+        if (h0 + h < a.Hq) a.bias[kBiasHead + ((size_t)s * a.Hq + h0 + h) * len + t] = acc[h];
     return;
   }
   const int first = write_blocks + bias_blocks;
@@ -1652,6 +1670,8 @@ __global__ __launch_bounds__(256) void rpa_fused_prep_kernel(FusedArgs a, int wr
     a.table[i] = (pg < (len + a.S - 1) / a.S && e >= 0 && e < a.entries) ? a.pages[e] : 0;
   }
   for (long long i = tid; i <= a.B; i += stride) a.cu_q[i] = (int32_t)i;
+  if (a.bias)
+    for (long long i = tid; i < kBiasHead; i += stride) a.bias[i] = 0.f;
   if (tid == 0) a.nseq[0] = a.B;
   if (a.qpad)
     for (long long i = tid; i < (long long)a.B * a.Hq * a.W; i += stride) {
@@ -1705,8 +1725,12 @@ int check_fused(const rpa_fused_shape_t* f) {
   if (f->head_dim < 1 || f->head_dim > f->cache_width) return fail(RPA_E_INVALID, "fused: head_dim must be in [1, cache_width]");
   if (f->total_pages < 1 || f->page_size < 1 || f->page_entries < 1 || f->pages_per_seq < 1)
     return fail(RPA_E_INVALID, "fused: bad page counts");
-  if (f->relative_dim < 0 || f->relative_dim > kMaxRelDim || (f->relative_dim > 0 && f->relative_extent < 1))
-    return fail(RPA_E_INVALID, "fused: relative_dim must be in [0, 256] with a positive extent");
+  if (f->relative_dim < 0 || f->relative_dim > kMaxRelDim ||
+      (f->relative_dim > 0 && (f->relative_extent < 1 || f->relative_extent > (1 << 24))))
+    return fail(RPA_E_INVALID, "fused: relative_dim must be in [0, 256] with an extent in [1, 2^24]");
+  if (f->relative_dim > 0 &&
+      kBiasHead + (long long)f->num_seqs * f->num_q_heads * bias_row_len(f->relative_extent) >= (1LL << 31))
+    return fail(RPA_E_INVALID, "fused: relative bias table exceeds 2^31 entries");
   if ((long long)f->pages_per_seq * f->page_size > INT32_MAX ||
       (long long)f->num_seqs * f->pages_per_seq > INT32_MAX ||
       (long long)f->num_seqs * f->num_q_heads * (f->relative_dim > 0 ? f->relative_extent : 1) > INT32_MAX)
@@ -1737,7 +1761,7 @@ FusedLayout fused_layout(const DeviceInfo& d, const rpa_fused_shape_t* f) {
   l.cu_q = l.table + round256(B * f->pages_per_seq * 4);
   l.nseq = l.cu_q + round256((B + 1) * 4);
   l.bias = l.nseq + 256;
-  l.qpad = l.bias + round256(f->relative_dim > 0 ? rows * bias_row_len(f->relative_extent) * 4 : 0);
+  l.qpad = l.bias + round256(f->relative_dim > 0 ? (kBiasHead + rows * bias_row_len(f->relative_extent)) * 4 : 0);
   l.opad = l.qpad + round256(pad);
   l.total = l.opad + pad;
   return l;
@@ -1976,7 +2000,11 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
   a.R = f->relative_dim;
   a.E = f->relative_dim > 0 ? f->relative_extent : 0;
   hipStream_t st = (hipStream_t)stream;
-  const int write_blocks = a.B * 2 * a.Hkv, bias_blocks = a.bias ? a.B * a.Hq : 0;
+  a.vec = ((uintptr_t)cache | (uintptr_t)keys | (uintptr_t)values) % 16 == 0 && a.D % 8 == 0 && a.W % 8 == 0;
+  const int write_blocks = a.B,
+            bias_blocks = a.bias ? a.B * ((a.Hq + kBiasHeads - 1) / kBiasHeads) *
+                                       ((bias_row_len(a.E) + kBiasSlab - 1) / kBiasSlab)
+                                 : 0;
   long long work = (long long)a.B * a.pps;
   if (a.qpad) work = work > (long long)a.B * a.Hq * a.W ? work : (long long)a.B * a.Hq * a.W;
   long long blocks = (work + 255) / 256;
