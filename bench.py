@@ -93,9 +93,10 @@ def kernel_source_digest() -> str:
 
 
 def measured_traffic(cfg: str):
-    """HBM bytes per attention-kernel dispatch from the committed rocprofv3 PMC summary
-    (profiles/pmc_traffic.json: FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's
-    reading for a 1 GiB copy), used only if it was measured on the current kernel sources."""
+    """HBM bytes per attention-kernel dispatch (for "inkling": per step, all three kernels) from
+    the committed rocprofv3 PMC summary (profiles/pmc_traffic.json: FETCH_SIZE and WRITE_SIZE,
+    each scaled by the same counter's reading for a 1 GiB copy), used only if it was measured on
+    the current kernel sources."""
     path = ROOT / "profiles" / "pmc_traffic.json"
     if not path.exists():
         return None
@@ -205,7 +206,7 @@ def fused_bench(args, dev) -> int:
         "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic("inkling"),
                      "basis": "whole step (cache write, metadata and bias-table kernels, attention, combine)"},
     }
     if not args.no_cpu_baseline:

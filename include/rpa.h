@@ -167,8 +167,8 @@ typedef struct rpa_fused_shape {
   int32_t cache_width;       /* padded row width of the cache (128) */
   int32_t page_entries;      /* length of the flat page_indices list */
   int32_t pages_per_seq;     /* max over sequences of ceil(kv_len / S) */
-  int32_t relative_dim;      /* R (0: no relative bias) */
-  int32_t relative_extent;   /* E */
+  int32_t relative_dim;      /* R in [0, 256] (0: no relative bias) */
+  int32_t relative_extent;   /* E in [1, 2^24] when R > 0; B * Hq * (E + 63) must stay below 2^31 */
 } rpa_fused_shape_t;
 
 /* Workspace bytes for rpa_inkling_fused_decode on the current device (0 on a bad shape). */

@@ -22,10 +22,9 @@
 //                         (m, l, acc) per workgroup, and the workgroup owning its last unit leaves
 //                         a descriptor of it.
 //   rpa_combine_kernel  one 4-wave workgroup per descriptor: log-sum-exp merge of the row
-//                       block's partials (lanes = row x dim quarter x contributor subset, so
-//                       row blocks with few rows spread their contributors over more lanes;
-//                       stream results merged through LDS), writes the rows, clears the
-//                       descriptor; resets the prefill tile queue for the next call.
+//                       block's partials (the waves take every 4th contributor, then merge
+//                       through LDS), writes the rows, clears the descriptor; resets the
+//                       prefill tile queue for the next call.
 //
 // MFMA operand layouts (16x16x32 bf16, wave64): A[i][k] and B[k][j] place row i / column j
 // at lane%16 and the 32 k-slots at (lane/16, element 0..7); D[i][j] sits at lane
@@ -1336,12 +1335,9 @@ __device__ __forceinline__ void merge_in(Merge& a, float mc, float lc, const flo
 }
 
 // Workgroup b merges the row block described by desc[b]: contributors b0..b, b0's share in slot
-// 2*b0+1 and every later one's in slot 2*bb.  Lanes are (row n, 32-dim quarter, contributor
-// subset): with rp = the row count rounded up to a power of two, lane = n + rp*(quarter + 4*sub),
-// so a row block with few rows (decode: G rows) puts its spare lanes on other contributors.  The
-// 4*(16/rp) streams (wave, subset) take contributors stream, stream + streams, ... two per
-// iteration (loads issued together); stream results are merged through LDS in a fixed order, so
-// the output is deterministic.
+// 2*b0+1 and every later one's in slot 2*bb.  Wave w takes contributors w, w+4, ... (two per
+// iteration, loads issued together); lane (row n = lane%16, dims 32*(lane/16) .. +32).  The four
+// waves' results are merged through LDS in a fixed order, so the output is deterministic.
 __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
   __shared__ float red[4][64][34];
   if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
@@ -1349,16 +1345,10 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
   if (!p.desc[b].valid[hw]) return;
   const SplitDesc d = p.desc[b];
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
-  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
-  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
-  int rp = 1;
-  while (rp < nrows) rp <<= 1;
-  const int nsub = ROW_BLOCK / rp;
-  const int n = lane & (rp - 1), quarter = (lane / rp) & 3, sub = lane / (4 * rp);
+  const int n = lane & 15, quarter = lane >> 4;
   const int row = d.rb * ROW_BLOCK + n;
-  const bool row_ok = n < nrows;
+  const bool row_ok = row < d.q_len * p.G;
   const int ncontrib = (int)(b - d.b0 + 1);
-  const int streams = 4 * nsub, stream = wv * nsub + sub;
 
   Merge acc;
   acc.m = -INFINITY;
@@ -1366,10 +1356,10 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
 #pragma unroll
   for (int k = 0; k < 32; ++k) acc.o[k] = 0.f;
   if (row_ok) {
-    for (int k = stream; k < ncontrib; k += 2 * streams) {
-      const bool two = k + streams < ncontrib;
+    for (int k = wv; k < ncontrib; k += 8) {
+      const bool two = k + 4 < ncontrib;
       const size_t s0 = (size_t)partial_slot(d.b0 + k, k == 0) * p.HG + hw;
-      const size_t s1 = (size_t)partial_slot(d.b0 + k + streams, false) * p.HG + hw;
+      const size_t s1 = (size_t)partial_slot(d.b0 + k + 4, false) * p.HG + hw;
       const float* ml0 = p.part_ml + (s0 * ROW_BLOCK + n) * 2;
       const float* ml1 = p.part_ml + ((two ? s1 : s0) * ROW_BLOCK + n) * 2;
       const f32x4* a0 = (const f32x4*)(p.part_acc + (s0 * ROW_BLOCK + n) * kD + 32 * quarter);
@@ -1394,15 +1384,9 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
 #pragma unroll
   for (int k = 0; k < 32; ++k) red[wv][lane][2 + k] = acc.o[k];
   __syncthreads();
-  if (wv == 0 && sub == 0) {
+  if (wv == 0) {
     if (row_ok) {
-      // streams in order (wave, subset), this lane's own (0, 0) first
-      for (int w = 0; w < 4; ++w)
-        for (int sb = 0; sb < nsub; ++sb) {
-          if (w == 0 && sb == 0) continue;
-          const int l2 = n + rp * (quarter + 4 * sb);
-          merge_in(acc, red[w][l2][0], red[w][l2][1], &red[w][l2][2]);
-        }
+      for (int w = 1; w < 4; ++w) merge_in(acc, red[w][lane][0], red[w][lane][1], &red[w][lane][2]);
       const int tok = row / p.G;
       const int head = (d.h * p.HG + hw) * p.G + (row - tok * p.G);
       const float inv = 1.f / acc.l;
@@ -1416,8 +1400,8 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
         *(u32x2*)(op + 4 * k) = w;
       }
     }
+    if (lane == 0) p.desc[b].valid[hw] = 0;
   }
-  if (t == 0) p.desc[b].valid[hw] = 0;
 }
 
 // ---------------------------------------------------------------------------------------------

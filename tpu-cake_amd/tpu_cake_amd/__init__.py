@@ -2,8 +2,12 @@
 
 The hot path of sdrshn-nmbr/tpu-cake's Inkling RPA workload, rebuilt as
 hand-written gfx950 HIP kernels (``librpa.so``, C ABI in ``include/rpa.h``)
-behind the reference operator's Python surface (``tpu_cake_amd.ops``).
+behind the reference operator's Python surface (``tpu_cake_amd.ops``), and the
+fused Inkling decode step (KV-cache write + relative-bias attention) behind the
+reference's fused-plan surface (``tpu_cake_amd.fused``).
 """
+
+from . import fused  # noqa: F401
 
 from .ops import (  # noqa: F401
     DEFAULT_MASK_VALUE,
@@ -16,6 +20,7 @@ from .ops import (  # noqa: F401
 
 __all__ = [
     "DEFAULT_MASK_VALUE",
+    "fused",
     "dynamic_validate_inputs",
     "gather_kv",
     "ragged_paged_attention",
