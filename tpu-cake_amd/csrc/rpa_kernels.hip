@@ -21,9 +21,10 @@
 //                         directly; a row block split across workgroups leaves one partial
 //                         (m, l, acc) per workgroup, and the workgroup owning its last unit leaves
 //                         a descriptor of it.
-//   rpa_combine_kernel  one 4-wave workgroup per descriptor: log-sum-exp merge of the row
-//                       block's partials (the waves take every 4th contributor, then merge
-//                       through LDS), writes the rows, clears the descriptor; resets the
+//   rpa_combine_kernel  one 4-wave workgroup per (descriptor, head): the rows' global max and
+//                       denominator from the partials' (m, l), then the weighted sum of their
+//                       acc rows with coalesced loads (waves take every 4th contributor, sums
+//                       added through LDS); writes the rows, clears the descriptor; resets the
 //                       prefill tile queue for the next call.
 //
 // MFMA operand layouts (16x16x32 bf16, wave64): A[i][k] and B[k][j] place row i / column j
@@ -1320,84 +1321,151 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ---------------------------------------------------------------------------------------------
 // split-K combine
 // ---------------------------------------------------------------------------------------------
-struct Merge {
-  float m, l, o[32];
-};
-
-__device__ __forceinline__ void merge_in(Merge& a, float mc, float lc, const float* oc) {
-  const float mn = fmaxf(a.m, mc);
-  const float mu = mn == -INFINITY ? 0.f : mn;
-  const float wa = __builtin_amdgcn_exp2f(a.m - mu), wc = __builtin_amdgcn_exp2f(mc - mu);
-  a.l = a.l * wa + lc * wc;
-#pragma unroll
-  for (int k = 0; k < 32; ++k) a.o[k] = a.o[k] * wa + oc[k] * wc;
-  a.m = mn;
+// Partial of contributor k (0-based) of descriptor d for head hw: (m, l) pairs [16 rows][2] and
+// acc [16 rows][kD], row-major.
+__device__ __forceinline__ size_t combine_slot(const Params& p, const SplitDesc& d, int hw, int k) {
+  return (size_t)partial_slot(d.b0 + k, k == 0) * p.HG + hw;
 }
 
-// Workgroup b merges the row block described by desc[b]: contributors b0..b, b0's share in slot
-// 2*b0+1 and every later one's in slot 2*bb.  Wave w takes contributors w, w+4, ... (two per
-// iteration, loads issued together); lane (row n = lane%16, dims 32*(lane/16) .. +32).  The four
-// waves' results are merged through LDS in a fixed order, so the output is deterministic.
-__global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
-  __shared__ float red[4][64][34];
-  if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
-  const int b = blockIdx.x / p.HG, hw = blockIdx.x - b * p.HG;  // descriptor, wave (head) of its group
-  if (!p.desc[b].valid[hw]) return;
-  const SplitDesc d = p.desc[b];
-  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
-  const int n = lane & 15, quarter = lane >> 4;
-  const int row = d.rb * ROW_BLOCK + n;
-  const bool row_ok = row < d.q_len * p.G;
-  const int ncontrib = (int)(b - d.b0 + 1);
-
-  Merge acc;
-  acc.m = -INFINITY;
-  acc.l = 0.f;
+// Pass 2 of the combine for row blocks of up to 2*NP rows: lane = (rows 2i + half for i < NP,
+// dims 4*(lane%32) .. +3), so one load instruction reads two whole 512-byte rows (coalesced).
+// Wave wv takes contributors wv, wv+4, ..., U at a time with all their loads issued first; each
+// is weighted by exp2(m - M[row]) with the row's global maximum M from pass 1 (no rescaling).
+template <int NP, int U>
+__device__ __forceinline__ void combine_rows(const Params& p, const SplitDesc& d, int hw, int ncontrib, int wv,
+                                             int lane, const float* mrow_lds, f32x4 (&o)[8]) {
+  const int half = lane >> 5, c4 = 4 * (lane & 31);
+  float mref[NP];
 #pragma unroll
-  for (int k = 0; k < 32; ++k) acc.o[k] = 0.f;
-  if (row_ok) {
-    for (int k = wv; k < ncontrib; k += 8) {
-      const bool two = k + 4 < ncontrib;
-      const size_t s0 = (size_t)partial_slot(d.b0 + k, k == 0) * p.HG + hw;
-      const size_t s1 = (size_t)partial_slot(d.b0 + k + 4, false) * p.HG + hw;
-      const float* ml0 = p.part_ml + (s0 * ROW_BLOCK + n) * 2;
-      const float* ml1 = p.part_ml + ((two ? s1 : s0) * ROW_BLOCK + n) * 2;
-      const f32x4* a0 = (const f32x4*)(p.part_acc + (s0 * ROW_BLOCK + n) * kD + 32 * quarter);
-      const f32x4* a1 = (const f32x4*)(p.part_acc + ((two ? s1 : s0) * ROW_BLOCK + n) * kD + 32 * quarter);
-      float o0[32], o1[32];
-      const float m0 = ml0[0], l0 = ml0[1], m1 = ml1[0], l1 = ml1[1];
-#pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        const f32x4 x0 = a0[v], x1 = a1[v];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          o0[4 * v + r] = x0[r];
-          o1[4 * v + r] = x1[r];
-        }
-      }
-      merge_in(acc, m0, l0, o0);
-      if (two) merge_in(acc, m1, l1, o1);
-    }
+  for (int i = 0; i < NP; ++i) {
+    const float m = mrow_lds[2 * i + half];
+    mref[i] = m == -INFINITY ? 0.f : m;
   }
-  red[wv][lane][0] = acc.m;
-  red[wv][lane][1] = acc.l;
+#pragma unroll 1
+  for (int k = wv; k < ncontrib; k += 4 * U) {
+    f32x4 x[U][NP];
+    float mc[U][NP];
 #pragma unroll
-  for (int k = 0; k < 32; ++k) red[wv][lane][2 + k] = acc.o[k];
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 4 * u < ncontrib ? k + 4 * u : k;  // past the end: a valid slot, weight 0
+      const size_t sc = combine_slot(p, d, hw, kk);
+      const float* ml = p.part_ml + sc * ROW_BLOCK * 2;
+      const float* a = p.part_acc + sc * ROW_BLOCK * kD + c4;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        mc[u][i] = ml[2 * (2 * i + half)];
+        x[u][i] = *(const f32x4*)(a + (2 * i + half) * kD);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the U contributors issued before any use
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        const float w = k + 4 * u < ncontrib ? __builtin_amdgcn_exp2f(mc[u][i] - mref[i]) : 0.f;
+        o[i] += w * x[u][i];
+      }
+  }
+}
+
+// Workgroup b merges the row block described by desc[b] for head hw: contributors b0..b, b0's
+// share in slot 2*b0+1 and every later one's in slot 2*bb.  Pass 1 (all 256 threads; thread =
+// (row t%16, contributors t/16, t/16 + 16, ...)): each row's global maximum M and denominator
+// L = sum l * exp2(m - M), merged through LDS.  Pass 2 (combine_rows): the weighted sum of the
+// contributors' acc rows, the four waves' sums added through LDS in a fixed order (deterministic),
+// divided by L and written as bf16.
+__global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
+  __shared__ float red[3][64][33];   // waves 1..3's sums (33: conflict-free row stride)
+  __shared__ float mlred[16][16][2];  // pass 1: (m, l) per (thread group, row)
+  __shared__ float rowm[16], rowl[16];
+  if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
+  // descriptor (last first: long splits end in late workgroups), wave (head) of its group
+  const int bi = blockIdx.x / p.HG, hw = blockIdx.x - bi * p.HG, b = gridDim.x / p.HG - 1 - bi;
+  // the flag and the fields in one round trip (the empty asm keeps the compiler from moving the
+  // field loads behind the flag test)
+  int valid = p.desc[b].valid[hw];
+  SplitDesc d = p.desc[b];
+  asm volatile("" : "+v"(valid), "+v"(d.nch), "+v"(d.q_start), "+v"(d.q_len), "+v"(d.h), "+v"(d.rb), "+v"(d.b0));
+  if (!__builtin_amdgcn_readfirstlane(valid)) return;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const int ncontrib = (int)(b - d.b0 + 1);
+  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
+  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
+
+  // pass 1: per-row (M, L) over all contributors
+  {
+    const int r = t & 15, g = t >> 4;
+    float m = -INFINITY, l = 0.f;
+#pragma unroll 1
+    for (int k = g; k < ncontrib; k += 64) {
+      float mc[4], lc[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int kk = k + 16 * u < ncontrib ? k + 16 * u : k;
+        const float* ml = p.part_ml + (combine_slot(p, d, hw, kk) * ROW_BLOCK + r) * 2;
+        mc[u] = ml[0];
+        lc[u] = ml[1];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float mcu = k + 16 * u < ncontrib ? mc[u] : -INFINITY;
+        const float mn = fmaxf(m, mcu), mu = mn == -INFINITY ? 0.f : mn;
+        l = l * __builtin_amdgcn_exp2f(m - mu) + lc[u] * __builtin_amdgcn_exp2f(mcu - mu);
+        m = mn;
+      }
+    }
+    mlred[g][r][0] = m;
+    mlred[g][r][1] = l;
+    __syncthreads();
+    if (t < 16) {
+      float M = -INFINITY;
+      for (int gg = 0; gg < 16; ++gg) M = fmaxf(M, mlred[gg][t][0]);
+      const float mu = M == -INFINITY ? 0.f : M;
+      float L = 0.f;
+      for (int gg = 0; gg < 16; ++gg) L += mlred[gg][t][1] * __builtin_amdgcn_exp2f(mlred[gg][t][0] - mu);
+      rowm[t] = M;
+      rowl[t] = L;
+    }
+    __syncthreads();
+  }
+
+  // pass 2: weighted sums of the acc rows
+  f32x4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (nrows <= 4)
+    combine_rows<2, 4>(p, d, hw, ncontrib, wv, lane, rowm, o);
+  else if (nrows <= 8)
+    combine_rows<4, 3>(p, d, hw, ncontrib, wv, lane, rowm, o);
+  else
+    combine_rows<8, 1>(p, d, hw, ncontrib, wv, lane, rowm, o);
+  const int np = nrows <= 4 ? 2 : nrows <= 8 ? 4 : 8;
+  if (wv > 0)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < np)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[wv - 1][lane][4 * i + e] = o[i][e];
   __syncthreads();
   if (wv == 0) {
-    if (row_ok) {
-      for (int w = 1; w < 4; ++w) merge_in(acc, red[w][lane][0], red[w][lane][1], &red[w][lane][2]);
-      const int tok = row / p.G;
-      const int head = (d.h * p.HG + hw) * p.G + (row - tok * p.G);
-      const float inv = 1.f / acc.l;
-      // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
-      uint16_t* op = p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + 32 * quarter;
+    const int half = lane >> 5, c4 = 4 * (lane & 31);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        u32x2 w;
-        w[0] = pack_bf16x2(acc.o[4 * k + 0] * inv, acc.o[4 * k + 1] * inv);
-        w[1] = pack_bf16x2(acc.o[4 * k + 2] * inv, acc.o[4 * k + 3] * inv);
-        *(u32x2*)(op + 4 * k) = w;
+    for (int i = 0; i < 8; ++i) {
+      const int row = 2 * i + half;
+      if (i < np && row < nrows) {
+        f32x4 v = o[i];
+        for (int w = 0; w < 3; ++w)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += red[w][lane][4 * i + e];
+        const float inv = 1.f / rowl[row];
+        const int grow = d.rb * ROW_BLOCK + row;  // row of the sequence's (token, head) rows
+        const int tok = grow / p.G;
+        const int head = (d.h * p.HG + hw) * p.G + (grow - tok * p.G);
+        // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
+        u32x2 w2;
+        w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
+        w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
+        *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + c4) = w2;
       }
     }
     if (lane == 0) p.desc[b].valid[hw] = 0;
