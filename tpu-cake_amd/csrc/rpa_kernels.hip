@@ -145,6 +145,69 @@ __device__ __forceinline__ long long wave_incl_scan64(long long x, int lane) {
   return x;
 }
 
+// 32-bit wave sum and inclusive scan with DPP moves inside 16-lane rows (VALU, a few cycles a
+// step, where a shuffle is an LDS round trip) and the row totals read out with readlane.
+// Every lane of the wave must be active.
+template <int CTRL, bool BOUND_ZERO>
+__device__ __forceinline__ int dpp(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, BOUND_ZERO);
+}
+
+__device__ __forceinline__ int wave_sum32(int x) {
+  x += dpp<0xB1, false>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E, false>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x124, false>(x);  // row_ror:4
+  x += dpp<0x128, false>(x);  // row_ror:8: every lane holds its row's total
+  return rl(x, 0) + rl(x, 16) + rl(x, 32) + rl(x, 48);
+}
+
+__device__ __forceinline__ float wave_sumf(float v) {
+  int x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, dpp<0xB1, false>(x));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, dpp<0x4E, false>(x));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, dpp<0x124, false>(x));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, dpp<0x128, false>(x));
+  x = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, rl(x, 0)) + __builtin_bit_cast(float, rl(x, 16))) +
+         (__builtin_bit_cast(float, rl(x, 32)) + __builtin_bit_cast(float, rl(x, 48)));
+}
+
+__device__ __forceinline__ int wave_incl_scan32(int x, int lane) {
+  x += dpp<0x111, true>(x);  // row_shr:1 (lanes shifted in from outside the row read 0)
+  x += dpp<0x112, true>(x);  // row_shr:2
+  x += dpp<0x114, true>(x);  // row_shr:4
+  x += dpp<0x118, true>(x);  // row_shr:8: inclusive scan inside each row
+  const int r0 = rl(x, 15), r1 = rl(x, 31), r2 = rl(x, 47), row = lane >> 4;
+  return x + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+}
+
+// The balanced partition (rpa_schedule.h) with a 32-bit division when the total fits.
+__device__ __forceinline__ Partition make_partition_fast(long long total, int grid) {
+  if (total < (1ll << 31)) {
+    Partition pt;
+    pt.q = (int)total / grid;
+    pt.r = total - pt.q * grid;
+    return pt;
+  }
+  return make_partition(total, grid);
+}
+
+// Per-lane unit counts below 2^24 (every realistic batch) take the 32-bit DPP paths.
+constexpr long long kSmallUnits = 1ll << 24;
+
+__device__ __forceinline__ long long wave_sum_units(long long x) {
+  if (__ballot(x >= kSmallUnits) == 0) return (long long)wave_sum32((int)x);
+  return wave_sum64(x);
+}
+
+__device__ __forceinline__ long long wave_incl_scan_units(long long x, int lane) {
+  if (__ballot(x >= kSmallUnits) == 0) return (long long)wave_incl_scan32((int)x, lane);
+  return wave_incl_scan64(x, lane);
+}
+
 // Reduce a per-lane value over lanes {l, l^16, l^32, l^48} -- the four 16-lane rows that hold
 // one query row's keys -- with gfx950's v_permlane16_swap / v_permlane32_swap (VALU, no LDS).
 // permlane16_swap(x, x) returns rows (0,0,2,2) and (1,1,3,3); permlane32_swap returns
@@ -253,7 +316,7 @@ __device__ __forceinline__ long long total_units(const Params& p, int nseq, int 
   long long w = 0;
   for (int base = 0; base < nseq; base += 64) {
     SeqInfo s = load_seq(p, base + lane, nseq, 0, err);
-    w += wave_sum64((long long)s.units * p.NG);
+    w += wave_sum_units((long long)s.units * p.NG);
   }
   return w;
 }
@@ -265,7 +328,7 @@ __device__ __forceinline__ void locate_seq(const Params& p, int nseq, int lane, 
   for (int base = 0; base < nseq; base += 64) {
     SeqInfo s = load_seq(p, base + lane, nseq, 0, err);
     long long cnt = (long long)s.units * p.NG;
-    long long incl = wave_incl_scan64(cnt, lane);
+    long long incl = wave_incl_scan_units(cnt, lane);
     long long tile = rl64(incl, 63);
     if (u < off + tile) {
       unsigned long long below = __ballot(off + incl <= u);
@@ -312,7 +375,7 @@ __device__ __forceinline__ Cursor cursor_at(const Params& p, const Window& w, in
   Cursor x;
   cursor_load_seq(p, w, seq, x);
   int per_head = rl(w.s.units, seq - w.base);
-  x.h = (int)(ul / per_head);
+  x.h = ul < (1ll << 31) ? (int)ul / per_head : (int)(ul / per_head);  // 32-bit division when it fits
   int rem = (int)(ul - (long long)x.h * per_head);
   x.rb = 0;
   for (;;) {
@@ -1203,7 +1266,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (nseq <= 64 * kWin) {
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
-      tile[w] = wave_sum64((long long)wsi[w].units * p.NG);
+      tile[w] = wave_sum_units((long long)wsi[w].units * p.NG);
       W += tile[w];
     }
   } else {
@@ -1214,22 +1277,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // other sequences.  Every workgroup computes the same split from the same metadata.
   int gpre = 0, pf_total = 0;
   if (MODE == KV_BF16 && pf_min > 0) {
-    float steps = 0.f;
+    // per lane over the four windows, then one wave sum each (skipped when no sequence is a
+    // prefill sequence)
+    float st = 0.f;
+    int cnt = 0;
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
       const int nt = pf_tiles_of(p, wsi[w], pf_min);
       const float prior = (float)(wsi[w].kv_len - wsi[w].q_len);
       // chunks of key positions the tiles visit (causal), summed over the sequence's tiles
-      float st = nt > 0 ? (float)p.Hkv * ((float)nt * prior + (float)p.pf_tq * 0.5f * (float)nt * (float)(nt + 1)) /
-                              (float)KV_CHUNK
-                        : 0.f;
-      int cnt = nt * p.Hkv;
-      for (int o = 32; o > 0; o >>= 1) {
-        st += __shfl_xor(st, o, 64);
-        cnt += __shfl_xor(cnt, o, 64);
-      }
-      steps += __builtin_bit_cast(float, uni(__builtin_bit_cast(int, st)));
-      pf_total += uni(cnt);
+      st += nt > 0 ? (float)p.Hkv * ((float)nt * prior + (float)p.pf_tq * 0.5f * (float)nt * (float)(nt + 1)) /
+                         (float)KV_CHUNK
+                   : 0.f;
+      cnt += nt * p.Hkv;
+    }
+    float steps = 0.f;
+    if (__ballot(cnt > 0) != 0) {
+      steps = wave_sumf(st);
+      pf_total = wave_sum32(cnt);
     }
     if (pf_total > 0) {
       const float pw = p.pf_cost * steps, dw = (float)W;
@@ -1244,7 +1309,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
   const int bd = b - gpre, gd = p.grid - gpre;  // stream-K workgroup index and count
-  const Partition pt = make_partition(W, gd > 0 ? gd : 1);
+  const Partition pt = make_partition_fast(W, gd > 0 ? gd : 1);
   const long long u0 = uni64(range_start(bd, pt)), u1 = uni64(range_start(bd + 1, pt));
   if (bd >= 0 && W > 0 && u0 < u1) {
     int seq;
@@ -1270,7 +1335,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int w = 1; w < kWin; ++w) select_seq(win.s, wsi[w], wsel == w);
         const long long cnt = (long long)win.s.units * p.NG;
-        const long long incl = wave_incl_scan64(cnt, lane);
+        const long long incl = wave_incl_scan_units(cnt, lane);
         const int idx = __popcll(__ballot(off_sel + incl <= u0));
         seq = uni(win.base + idx);
         seq_start = uni64(off_sel + rl64(incl - cnt, idx));
