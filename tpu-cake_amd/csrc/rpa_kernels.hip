@@ -591,9 +591,26 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 w, float sc) {
   return o;
 }
 
-template <int MODE>
+// 8 OCP e4m3 codes -> bf16, exactly (every finite e4m3 value is a bf16 value): gfx950's scaled
+// conversion with scale 1 (it applies only the scale's power of two), two codes per instruction.
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8_exact(u32x2 w) {
+  u32x4 o;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    o[2 * t] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[t], 1.f, false));
+    o[2 * t + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[t], 1.f, true));
+  }
+  return o;
+}
+
+// UPG fp8 K: a unit's 32 keys share one page, hence one K scale, applied to the unit's fp32
+// scores (compute_unit) instead of to every element.  V keeps the reference's bf16(v * scale).
+template <int MODE, bool UPG>
 __device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which) {
-  if constexpr (MODE == KV_FP8) {
+  if constexpr (MODE == KV_FP8 && UPG) {
+    if (which) return fp8x8_to_bf16x8(r.w[blk][s], p.v_scale * r.sc[blk]);
+    return fp8x8_to_bf16x8_exact(r.w[blk][s]);
+  } else if constexpr (MODE == KV_FP8) {
     return fp8x8_to_bf16x8(r.w[blk][s], (which ? p.v_scale : p.k_scale) * r.sc[blk]);
   } else if constexpr (MODE == KV_BF16_SCALED) {
     return scale_bf16x8(r.w[blk][s], which ? p.v_scale : p.k_scale);
@@ -615,7 +632,7 @@ struct RowState {
 // One unit.  S = K Q^T; then the next unit's queries are loaded into q (their registers are
 // free once QK^T has issued); V^T goes to LDS, after which the next unit's V is loaded into the
 // registers just released; then softmax and O^T += V^T P^T.
-template <int MODE>
+template <int MODE, bool UPG>
 __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const HalfRegs<MODE>& kr,
                                              const HalfRegs<MODE>& vr, bf16x8 q[4], const Cursor& nx,
                                              const UnitAddr& nx_addr, HalfRegs<MODE>& v_next, RowState& st,
@@ -624,8 +641,13 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    s0 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE>(kr, p, 0, s, 0)), q[s], s0);
-    s1 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE>(kr, p, 1, s, 0)), q[s], s1);
+    s0 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE, UPG>(kr, p, 0, s, 0)), q[s], s0);
+    s1 = mfma(__builtin_bit_cast(bf16x8, to_bf16x8<MODE, UPG>(kr, p, 1, s, 0)), q[s], s1);
+  }
+  if constexpr (MODE == KV_FP8 && UPG) {  // the unit's K scale (one page), on the fp32 scores
+    const float ks = p.k_scale * kr.sc[0];
+    s0 *= ks;
+    s1 *= ks;
   }
   load_q(p, nx, n, j, wv, q);
 
@@ -636,7 +658,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     const int slot_b = 2 * (8 * (n >> 2) + 4 * blk + (n & 3));
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 vw = to_bf16x8<MODE>(vr, p, blk, s, 1);
+      const u32x4 vw = to_bf16x8<MODE, UPG>(vr, p, blk, s, 1);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         uint32_t w = vw[t];
@@ -796,7 +818,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   load_half<MODE>(p, nx_addr, 0, k_nxt);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit<MODE>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j, wv);
+  compute_unit<MODE, UPG>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j, wv);
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
