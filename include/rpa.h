@@ -188,6 +188,40 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* shape, float sm_scale, con
                              const void* relative_projection, void* out, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Inkling decode, v1 contract: the workload the reference renders as `experiment inkling-rpa`
+ * (src/tpu_cake/workloads/inkling_rpa.py:87-143, contract :693-723) with the semantics of its
+ * numpy oracle inkling_rpa_reference (:37-73), executed here:
+ *   out[b, h] = softmax_l( q[b, h] . k[l, h/G] * sm_scale + bias[h, l] ) @ v[l, h/G]
+ * over the keys l < sequence_lengths[b] of pages page_table[b, :]; the oracle's scale is 1/D.
+ * Separate key and value caches; bias indexed by key position (bias_len >= every length).
+ * The reference's `experiment inkling-rpa` renders the experiment artifact for this workload
+ * (cli.py:667-676); this entry executes it.  The caches are packed into the operator's
+ * combined layout in the workspace on every call (a copy of the whole cache: this entry serves
+ * the contract's shapes; a serving cache belongs in the combined layout of
+ * rpa_ragged_paged_attention).
+ * --------------------------------------------------------------------------------------- */
+typedef struct rpa_inkling_shape {
+  int32_t num_seqs;       /* B */
+  int32_t num_q_heads;    /* H */
+  int32_t num_kv_heads;   /* Hkv: key and value heads (H % Hkv == 0) */
+  int32_t head_dim;       /* D <= 128 (queries, keys, values, output) */
+  int32_t total_pages;    /* P */
+  int32_t page_size;      /* S */
+  int32_t pages_per_seq;  /* MP: page_table row length */
+  int32_t bias_len;       /* L: bias columns, in [1, 2^24] */
+} rpa_inkling_shape_t;
+
+/* Workspace bytes for rpa_inkling_decode on the current device (0 on a bad shape). */
+size_t rpa_inkling_workspace_size(const rpa_inkling_shape_t* shape);
+
+/* query bf16 [B, H, D]; key_cache, value_cache bf16 [P, S, Hkv, D]; page_table int32 [B, MP];
+ * sequence_lengths int32 [B] (each in [1, min(MP * S, L)]); bias bf16 [H, L]; out bf16 [B, H, D].
+ * The workspace is initialised with rpa_workspace_init like the operator's. */
+int rpa_inkling_decode(const rpa_inkling_shape_t* shape, float sm_scale, const void* query, const void* key_cache,
+                       const void* value_cache, const int32_t* page_table, const int32_t* sequence_lengths,
+                       const void* bias, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

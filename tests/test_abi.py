@@ -51,16 +51,18 @@ def test_struct_layout_matches_c(tmp_path):
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "rpa.h"\n'
         "int main(void){\n"
-        '  printf("%zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t), offsetof(rpa_shape_t, kv_dtype),\n'
+        '  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t), offsetof(rpa_shape_t, kv_dtype),\n'
         "         sizeof(rpa_options_t), offsetof(rpa_options_t, mask_value), offsetof(rpa_options_t, v_scale),\n"
         "         offsetof(rpa_options_t, has_k_scale), sizeof(rpa_fused_shape_t),\n"
-        "         offsetof(rpa_fused_shape_t, relative_extent));\n  return 0; }\n")
+        "         offsetof(rpa_fused_shape_t, relative_extent), sizeof(rpa_inkling_shape_t),\n"
+        "         offsetof(rpa_inkling_shape_t, bias_len));\n  return 0; }\n")
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-std=c99", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [ctypes.sizeof(_lib.RpaShape), _lib.RpaShape.kv_dtype.offset, ctypes.sizeof(_lib.RpaOptions),
             _lib.RpaOptions.mask_value.offset, _lib.RpaOptions.v_scale.offset, _lib.RpaOptions.has_k_scale.offset,
-            ctypes.sizeof(_lib.RpaFusedShape), _lib.RpaFusedShape.relative_extent.offset]
+            ctypes.sizeof(_lib.RpaFusedShape), _lib.RpaFusedShape.relative_extent.offset,
+            ctypes.sizeof(_lib.RpaInklingShape), _lib.RpaInklingShape.bias_len.offset]
     assert got == want
 
 
@@ -114,3 +116,25 @@ def test_ctypes_signatures_match_the_header():
         m = re.search(r"\b" + name + r"\s*\(([^)]*)\)", text)
         params = [x for x in m.group(1).split(",") if x.strip() and x.strip() != "void"]
         assert len(getattr(lib, name).argtypes) == len(params), name
+
+
+def _v1_shape(**kw):
+    base = dict(num_seqs=4, num_q_heads=4, num_kv_heads=4, head_dim=32, total_pages=32, page_size=16,
+                pages_per_seq=8, bias_len=128)
+    base.update(kw)
+    return _lib.RpaInklingShape(**base)
+
+
+@pytest.mark.parametrize("bad,msg", [(dict(num_q_heads=6, num_kv_heads=4), b"divide evenly"),
+                                     (dict(head_dim=160), b"head_dim"),
+                                     (dict(page_size=0), b"page counts"),
+                                     (dict(bias_len=0), b"bias_len")])
+def test_v1_invalid_shapes_rejected_before_launch(lib, bad, msg):
+    rc = lib.rpa_inkling_decode(ctypes.byref(_v1_shape(**bad)), 1.0, *([None] * 8), 0, None)
+    assert rc != 0 and msg in lib.rpa_last_error()
+    assert lib.rpa_inkling_workspace_size(ctypes.byref(_v1_shape(**bad))) == 0
+
+
+def test_v1_null_pointers_rejected(lib):
+    rc = lib.rpa_inkling_decode(ctypes.byref(_v1_shape()), 1.0, *([None] * 8), 0, None)
+    assert rc == -1 and b"NULL" in lib.rpa_last_error()

@@ -1830,6 +1830,73 @@ __global__ __launch_bounds__(256) void rpa_fused_unpad_kernel(const uint16_t* pa
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Inkling decode, v1 contract (src/tpu_cake/workloads/inkling_rpa.py:37-73): separate K and V
+// caches [P, S, Hkv, D], a [B, MP] page table, a bias [H, L] indexed by key position, scale 1/D.
+// One prep launch packs the caches into the operator's combined layout and builds the metadata
+// and the bias table; then the operator's kernels in bias mode.
+// ---------------------------------------------------------------------------------------------
+struct V1Args {
+  const uint16_t* q;       // [B, H, D]
+  const uint16_t* kc;      // [P, S, Hkv, D]
+  const uint16_t* vc;      // [P, S, Hkv, D]
+  const uint16_t* bias;    // [H, L]
+  uint16_t* cache;         // [P, S, 2*Hkv, kD]
+  float* table;            // kBiasHead zeros + [B, H, bias_row_len(L)]
+  int32_t* cu_q;           // [B+1]
+  int32_t* nseq;           // [1]
+  uint16_t* qpad;          // [B, H, kD] when D < kD
+  int B, H, Hkv, D, P, S, L;
+  int vec;                 // caches 16-byte aligned and D % 8 == 0
+};
+
+// Grid-stride roles: the combined cache rows (8 elements a thread), the bias table, the
+// metadata and the padded queries.
+__global__ __launch_bounds__(256) void rpa_inkling_v1_prep_kernel(V1Args a) {
+  const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x, stride = (long long)gridDim.x * blockDim.x;
+  const long long rows = (long long)a.P * a.S * 2 * a.Hkv;
+  for (long long i = tid; i < rows * (kD / 8); i += stride) {
+    const long long row = i / (kD / 8);
+    const int d8 = (int)(i - row * (kD / 8)) * 8;
+    const int comb = (int)(row % (2 * a.Hkv));
+    const long long ps = row / (2 * a.Hkv);  // page * S + slot
+    const uint16_t* src = ((comb & 1) ? a.vc : a.kc) + (ps * a.Hkv + (comb >> 1)) * a.D;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (a.vec) {
+      if (d8 < a.D) v = *(const u32x4*)(src + d8);
+    } else {
+      uint16_t e[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) e[k] = d8 + k < a.D ? src[d8 + k] : (uint16_t)0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] = (uint32_t)e[2 * k] | ((uint32_t)e[2 * k + 1] << 16);
+    }
+    *(u32x4*)(a.cache + row * kD + d8) = v;
+  }
+  const int len = bias_row_len(a.L);
+  for (long long i = tid; i < kBiasHead + (long long)a.B * a.H * len; i += stride) {
+    float v = 0.f;
+    if (i >= kBiasHead) {
+      const long long k = i - kBiasHead, r = k / len;
+      const int t = (int)(k - r * len), h = (int)(r % a.H);
+      if (t < a.L) v = bf16f(a.bias[(size_t)h * a.L + t]);  // entry t = key t (the window starts at key 0)
+    }
+    a.table[i] = v;
+  }
+  for (long long i = tid; i <= a.B; i += stride) a.cu_q[i] = (int32_t)i;
+  if (tid == 0) a.nseq[0] = a.B;
+  if (a.qpad)
+    for (long long i = tid; i < (long long)a.B * a.H * kD; i += stride) {
+      const long long row = i / kD;
+      const int d = (int)(i - row * kD);
+      a.qpad[i] = d < a.D ? a.q[row * a.D + d] : (uint16_t)0;
+    }
+}
+
+struct V1Layout {
+  size_t cache, table, cu_q, nseq, qpad, opad, total;
+};
+
 struct FusedLayout {
   size_t table, cu_q, nseq, bias, qpad, opad, total;
 };
@@ -1901,6 +1968,49 @@ FusedLayout fused_layout(const DeviceInfo& d, const rpa_fused_shape_t* f) {
   l.nseq = l.cu_q + round256((B + 1) * 4);
   l.bias = l.nseq + 256;
   l.qpad = l.bias + round256(f->relative_dim > 0 ? (kBiasHead + rows * bias_row_len(f->relative_extent)) * 4 : 0);
+  l.opad = l.qpad + round256(pad);
+  l.total = l.opad + pad;
+  return l;
+}
+
+int check_v1(const rpa_inkling_shape_t* f) {
+  if (!f) return fail(RPA_E_INVALID, "inkling shape is NULL");
+  if (f->num_seqs < 1 || f->num_q_heads < 1 || f->num_kv_heads < 1 || f->num_q_heads % f->num_kv_heads)
+    return fail(RPA_E_INVALID, "inkling: query heads must divide evenly across key and value heads");
+  if (f->head_dim < 1 || f->head_dim > kD) return fail(RPA_E_UNSUPPORTED, "inkling: head_dim must be in [1, 128]");
+  if (f->total_pages < 1 || f->page_size < 1 || f->pages_per_seq < 1)
+    return fail(RPA_E_INVALID, "inkling: bad page counts");
+  if (f->bias_len < 1 || f->bias_len > (1 << 24)) return fail(RPA_E_INVALID, "inkling: bias_len must be in [1, 2^24]");
+  if (kBiasHead + (long long)f->num_seqs * f->num_q_heads * bias_row_len(f->bias_len) >= (1LL << 31) ||
+      (long long)f->pages_per_seq * f->page_size > INT32_MAX || (long long)f->num_seqs * f->pages_per_seq > INT32_MAX)
+    return fail(RPA_E_INVALID, "inkling: sizes overflow int32");
+  return RPA_OK;
+}
+
+rpa_shape_t v1_rpa_shape(const rpa_inkling_shape_t* f) {
+  rpa_shape_t r;
+  r.num_tokens = f->num_seqs;
+  r.num_q_heads = f->num_q_heads;
+  r.num_kv_heads = f->num_kv_heads;
+  r.head_dim = kD;
+  r.total_pages = f->total_pages;
+  r.page_size = f->page_size;
+  r.max_num_seqs = f->num_seqs;
+  r.pages_per_seq = f->pages_per_seq;
+  r.kv_dtype = RPA_KV_BF16;
+  return r;
+}
+
+// [operator workspace][combined cache][bias table][cu_q][num_seqs][padded q][padded out]
+V1Layout v1_layout(const DeviceInfo& d, const rpa_inkling_shape_t* f) {
+  V1Layout l;
+  const size_t B = (size_t)f->num_seqs, rows = B * f->num_q_heads;
+  const size_t pad = f->head_dim < kD ? rows * kD * 2 : 0;
+  l.cache = round256(ws_layout(d).total);
+  l.table = l.cache + round256((size_t)f->total_pages * f->page_size * 2 * f->num_kv_heads * kD * 2);
+  l.cu_q = l.table + round256((kBiasHead + rows * bias_row_len(f->bias_len)) * 4);
+  l.nseq = l.cu_q + round256((B + 1) * 4);
+  l.qpad = l.nseq + 256;
   l.opad = l.qpad + round256(pad);
   l.total = l.opad + pad;
   return l;
@@ -2087,6 +2197,75 @@ size_t rpa_fused_workspace_size(const rpa_fused_shape_t* shape) {
   DeviceInfo d;
   if (device_info(d) != RPA_OK) return 0;
   return fused_layout(d, shape).total;
+}
+
+size_t rpa_inkling_workspace_size(const rpa_inkling_shape_t* shape) {
+  if (check_v1(shape) != RPA_OK) return 0;
+  DeviceInfo d;
+  if (device_info(d) != RPA_OK) return 0;
+  return v1_layout(d, shape).total;
+}
+
+int rpa_inkling_decode(const rpa_inkling_shape_t* f, float sm_scale, const void* query, const void* key_cache,
+                       const void* value_cache, const int32_t* page_table, const int32_t* sequence_lengths,
+                       const void* bias, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_stale_error();
+  int rc = check_v1(f);
+  if (rc) return rc;
+  if (!query || !key_cache || !value_cache || !page_table || !sequence_lengths || !bias || !out)
+    return fail(RPA_E_INVALID, "inkling: NULL pointer");
+  DeviceInfo d;
+  rc = device_info(d);
+  if (rc) return rc;
+  const V1Layout l = v1_layout(d, f);
+  if (!workspace || workspace_bytes < l.total)
+    return fail(RPA_E_WORKSPACE, "inkling workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
+                                     std::to_string(l.total));
+  uint8_t* ws = (uint8_t*)workspace;
+  V1Args a;
+  a.q = (const uint16_t*)query;
+  a.kc = (const uint16_t*)key_cache;
+  a.vc = (const uint16_t*)value_cache;
+  a.bias = (const uint16_t*)bias;
+  a.cache = (uint16_t*)(ws + l.cache);
+  a.table = (float*)(ws + l.table);
+  a.cu_q = (int32_t*)(ws + l.cu_q);
+  a.nseq = (int32_t*)(ws + l.nseq);
+  a.qpad = f->head_dim < kD ? (uint16_t*)(ws + l.qpad) : nullptr;
+  a.B = f->num_seqs;
+  a.H = f->num_q_heads;
+  a.Hkv = f->num_kv_heads;
+  a.D = f->head_dim;
+  a.P = f->total_pages;
+  a.S = f->page_size;
+  a.L = f->bias_len;
+  a.vec = ((uintptr_t)key_cache | (uintptr_t)value_cache) % 16 == 0 && a.D % 8 == 0;
+  hipStream_t st = (hipStream_t)stream;
+  const long long work = (long long)a.P * a.S * 2 * a.Hkv * (kD / 8);
+  long long blocks = (work + 255) / 256;
+  blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+  hipLaunchKernelGGL(rpa_inkling_v1_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(RPA_E_HIP, std::string("inkling prep launch failed: ") + hipGetErrorString(e));
+
+  const rpa_shape_t rs = v1_rpa_shape(f);
+  rpa_options_t o;
+  memset(&o, 0, sizeof(o));
+  o.sm_scale = sm_scale;
+  void* attn_out = a.qpad ? (void*)(ws + l.opad) : out;
+  rc = launch_rpa(&rs, &o, a.qpad ? (const void*)a.qpad : query, a.cache, nullptr, sequence_lengths, page_table,
+                  a.cu_q, a.nseq, attn_out, workspace, workspace_bytes, stream, nullptr, nullptr, a.table, a.L);
+  if (rc) return rc;
+  if (a.qpad) {
+    const long long rows = (long long)a.B * a.H;
+    long long ub = (rows * a.D + 255) / 256;
+    ub = ub < 1 ? 1 : (ub > 2048 ? 2048 : ub);
+    hipLaunchKernelGGL(rpa_fused_unpad_kernel, dim3((unsigned)ub), dim3(256), 0, st, (const uint16_t*)attn_out,
+                       (uint16_t*)out, rows, a.D, kD);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(RPA_E_HIP, std::string("inkling unpad launch failed: ") + hipGetErrorString(e));
+  }
+  return RPA_OK;
 }
 
 int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const void* queries, const void* keys,

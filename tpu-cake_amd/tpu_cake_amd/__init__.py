@@ -4,10 +4,11 @@ The hot path of sdrshn-nmbr/tpu-cake's Inkling RPA workload, rebuilt as
 hand-written gfx950 HIP kernels (``librpa.so``, C ABI in ``include/rpa.h``)
 behind the reference operator's Python surface (``tpu_cake_amd.ops``), and the
 fused Inkling decode step (KV-cache write + relative-bias attention) behind the
-reference's fused-plan surface (``tpu_cake_amd.fused``).
+reference's fused-plan surface (``tpu_cake_amd.fused``); the v1 Inkling decode
+contract (``experiment inkling-rpa``) runs through ``tpu_cake_amd.inkling``.
 """
 
-from . import fused  # noqa: F401
+from . import fused, inkling  # noqa: F401
 
 from .ops import (  # noqa: F401
     DEFAULT_MASK_VALUE,
@@ -21,6 +22,7 @@ from .ops import (  # noqa: F401
 __all__ = [
     "DEFAULT_MASK_VALUE",
     "fused",
+    "inkling",
     "dynamic_validate_inputs",
     "gather_kv",
     "ragged_paged_attention",

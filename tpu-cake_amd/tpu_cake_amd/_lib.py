@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "rpa_read_error_word",
     "rpa_fused_workspace_size",
     "rpa_inkling_fused_decode",
+    "rpa_inkling_workspace_size",
+    "rpa_inkling_decode",
 )
 
 
@@ -75,6 +77,21 @@ class RpaFusedShape(ctypes.Structure):
         ("pages_per_seq", ctypes.c_int32),
         ("relative_dim", ctypes.c_int32),
         ("relative_extent", ctypes.c_int32),
+    ]
+
+
+class RpaInklingShape(ctypes.Structure):
+    """include/rpa.h: rpa_inkling_shape_t (the v1 Inkling decode contract)."""
+
+    _fields_ = [
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("total_pages", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("pages_per_seq", ctypes.c_int32),
+        ("bias_len", ctypes.c_int32),
     ]
 
 
@@ -134,6 +151,10 @@ def load() -> ctypes.CDLL:
         lib.rpa_inkling_fused_decode.restype = ctypes.c_int
         # shape, sm_scale, 12 tensors (queries .. out), workspace, workspace_bytes, stream
         lib.rpa_inkling_fused_decode.argtypes = [ctypes.POINTER(RpaFusedShape), ctypes.c_float] + [vp] * 13 + [sz, vp]
+        lib.rpa_inkling_workspace_size.restype = sz
+        lib.rpa_inkling_workspace_size.argtypes = [ctypes.POINTER(RpaInklingShape)]
+        lib.rpa_inkling_decode.restype = ctypes.c_int
+        lib.rpa_inkling_decode.argtypes = [ctypes.POINTER(RpaInklingShape), ctypes.c_float] + [vp] * 8 + [sz, vp]
         version = lib.rpa_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"{path}: ABI version {version}, expected {ABI_VERSION}")
