@@ -80,16 +80,10 @@ def cpu_baseline(case, budget_s: float = 20.0) -> dict:
 
 def kernel_source_digest() -> str:
     """sha256[:16] of the kernel sources with comments and blank space removed (so that editing
-    a comment does not orphan a measurement)."""
-    import hashlib
-    import re
+    a comment does not orphan a measurement); tpu_cake_amd.evidence.kernel_source_digest."""
+    from tpu_cake_amd.evidence import kernel_source_digest as digest
 
-    csrc = ROOT / "tpu-cake_amd" / "csrc"
-    text = "".join((csrc / f).read_text() for f in ("rpa_kernels.hip", "rpa_schedule.h"))
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    text = re.sub(r"//[^\n]*", "", text)
-    text = re.sub(r"\s+", " ", text).strip()
-    return hashlib.sha256(text.encode()).hexdigest()[:16]
+    return digest()
 
 
 def measured_traffic(cfg: str):

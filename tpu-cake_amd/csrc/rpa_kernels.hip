@@ -1624,8 +1624,7 @@ int heads_per_group(int hkv) {
 constexpr int kVtBytes = kD * kVTRow;
 
 // Workgroups for the persistent grid: the kernel's occupancy (2 waves per SIMD) in workgroups
-// of hg waves, capped so no CU holds more than kMaxWavesPerCU waves; RPA_WAVES_PER_CU (1..8)
-// lowers the cap -- a tuning knob, like the reference's block-size parameters.
+// of hg waves, capped so no CU holds more than kMaxWavesPerCU waves.
 template <int MODE>
 int occupancy_grid(int cus, int hg) {
   int per_cu = 0;
@@ -1633,15 +1632,24 @@ int occupancy_grid(int cus, int hg) {
           hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
-  int cap = kMaxWavesPerCU;
-  if (const char* env = getenv("RPA_WAVES_PER_CU")) {
-    const int v = atoi(env);
-    if (v >= 1 && v < cap) cap = v;
-  }
-  int max_groups = cap / hg;
+  int max_groups = kMaxWavesPerCU / hg;
   if (max_groups < 1) max_groups = 1;
   if (per_cu > max_groups) per_cu = max_groups;
   return cus * per_cu;
+}
+
+// RPA_WAVES_PER_CU (1..kMaxWavesPerCU, read per call) lowers the waves per CU of the grid -- a
+// tuning knob, like the reference's block-size parameters.
+int grid_for_call(const DeviceInfo& d, int mode, int hg) {
+  int grid = d.grid[mode][hg];
+  if (const char* env = getenv("RPA_WAVES_PER_CU")) {
+    const int v = atoi(env);
+    if (v >= 1 && v < kMaxWavesPerCU) {
+      const int per_cu = v / hg > 0 ? v / hg : 1;
+      if (grid > d.cus * per_cu) grid = d.cus * per_cu;
+    }
+  }
+  return grid;
 }
 
 int device_info(DeviceInfo& out) {
@@ -2114,7 +2122,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (kv_scales) return fail(RPA_E_INVALID, "kv_scales is only used with fp8 kv_pages");
     if (opt->has_k_scale || opt->has_v_scale) mode = KV_BF16_SCALED;
   }
-  p.grid = d.grid[mode][p.HG];
+  p.grid = grid_for_call(d, mode, p.HG);
   // prefill tiles: bf16 KV without scales, masked keys at weight 0, eight waves (kv heads) per
   // workgroup
   if (mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG && !getenv("RPA_NO_PREFILL_TILES")) {

@@ -28,6 +28,7 @@ def _runtime():
         lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         _hip = lib
     return _hip
 
@@ -43,6 +44,16 @@ class KernelEvent:
             raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
         self._hip = hip
         self.cuda_event = handle.value
+
+    def record(self, stream=None) -> None:
+        """Record on ``stream`` (a HIP stream handle; default: torch's current stream)."""
+        if stream is None:
+            import torch
+
+            stream = torch.cuda.current_stream().cuda_stream
+        rc = self._hip.hipEventRecord(self.cuda_event, stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
 
     def elapsed_time(self, end: "KernelEvent") -> float:
         """Milliseconds from this event to ``end`` (both recorded and complete)."""
