@@ -859,7 +859,7 @@ constexpr int kPfKRow = kD * 2 + 16;
 constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
 constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
 constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
-constexpr float kPfCost = 0.35f;  // time of a prefill tile chunk / time of a stream-K unit (measured)
+constexpr float kPfCost = 0.45f;  // prefill chunk-step cost in stream-K units (Latin-square search on C3)
 
 struct PfPages {
   int pg[2];  // page ids of this thread's keys (pieces 0 and 1) for one chunk
