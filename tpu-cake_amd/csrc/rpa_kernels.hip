@@ -488,15 +488,26 @@ __host__ __device__ __forceinline__ int bias_row_len(int E) { return ((E + 31) /
 __host__ __device__ __forceinline__ int bias_chunk_lo(int kv_len, int E) { return kv_len > E ? (kv_len - E) / 32 : 0; }
 template <>
 struct HalfRegs<KV_FP8> {
-  u32x2 w[2][4];
-  float sc[2];  // per-(page, kv head) scale of each of the lane's two keys (k_scale/v_scale not applied)
+  u32x4 w[2][2];  // 16 codes per load: dims kdim(j, 2i) .. +7 and kdim(j, 2i+1) .. +7 (see kdim)
+  float sc[2];    // per-(page, kv head) scale of each of the lane's two keys (k_scale/v_scale not applied)
 };
+
+// The 8 dims lane group j holds in MFMA k-step s (QK^T; the same for K, Q and V^T rows).  bf16:
+// 8j + 32s.  fp8: one 16-byte load covers two k-steps, so lane group j reads bytes 16j .. 16j+15 of
+// each 64-byte half of a row -- 64 bytes per row per load instruction, half the requests per byte
+// of 8-byte loads.
+template <int MODE>
+__device__ __forceinline__ int kdim(int j, int s) {
+  if constexpr (MODE == KV_FP8) return 16 * j + 64 * (s >> 1) + 8 * (s & 1);
+  return 8 * j + 32 * s;
+}
 
 // Where this lane's two keys of unit x live (element index of their K row) and their pages.
 struct UnitAddr {
-  size_t e[2];
+  size_t e[2];  // + 8j: dims 8j of the 8-dims-per-lane layout
   int pg[2];
   int h;
+  int j8;       // 8j (fp8 adds it again: 16 dims per lane)
   int bias_at;  // KV_BF16_BIAS: table index of this lane's keys c*32 + 4j .. +3 (+16 for the second block)
 };
 
@@ -506,6 +517,7 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
   a.h = live ? x.h * p.HG + wv : 0;
+  a.j8 = 8 * j;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.c * KV_CHUNK + 16 * blk + n;
@@ -538,9 +550,9 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
       if (which == 0) r.bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at + 16 * blk);  // aligned
     }
     if constexpr (MODE == KV_FP8) {
-      const uint8_t* kp = p.kv + e;
+      const uint8_t* kp = p.kv + e + a.j8;  // bytes 16j (+64) of the row: kdim<KV_FP8>
 #pragma unroll
-      for (int s = 0; s < 4; ++s) r.w[blk][s] = *(const u32x2*)(kp + 32 * s);
+      for (int i = 0; i < 2; ++i) r.w[blk][i] = *(const u32x4*)(kp + 64 * i);
       // the raw per-(page, head) scale; multiplied in where it is used (to_bf16x8), a step later,
       // so that nothing waits for this load here
       r.sc[blk] = p.kv_scales ? p.kv_scales[((size_t)a.pg[blk] * p.Hkv + a.h) * 2 + which] : 1.f;
@@ -554,6 +566,7 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 
 // Query rows of cursor x as the B operand of QK^T.  Rows past q_len * G read row 0 of the
 // sequence instead: their columns of S and O are never stored, and MFMA columns are independent.
+template <int MODE>
 __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, int wv, bf16x8 q[4]) {
   const bool live = x.nch > 0;
   int row = x.rb * ROW_BLOCK + n;
@@ -561,9 +574,9 @@ __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, 
   const int tok = row / p.G;
   const int g = row - tok * p.G;
   const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)(x.h * p.HG + wv) * p.G : 0;
-  const uint16_t* qp = p.q + ((size_t)tok * p.Hq + base + g) * kD + 8 * j;
+  const uint16_t* qp = p.q + ((size_t)tok * p.Hq + base + g) * kD;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
+  for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + kdim<MODE>(j, s)));
 }
 
 // bf16(float(x) * scale) for 8 packed bf16 values (the reference's k_scale formula, :124-129).
@@ -607,11 +620,15 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8_exact(u32x2 w) {
 // scores (compute_unit) instead of to every element.  V keeps the reference's bf16(v * scale).
 template <int MODE, bool UPG>
 __device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which) {
-  if constexpr (MODE == KV_FP8 && UPG) {
-    if (which) return fp8x8_to_bf16x8(r.w[blk][s], p.v_scale * r.sc[blk]);
-    return fp8x8_to_bf16x8_exact(r.w[blk][s]);
-  } else if constexpr (MODE == KV_FP8) {
-    return fp8x8_to_bf16x8(r.w[blk][s], (which ? p.v_scale : p.k_scale) * r.sc[blk]);
+  if constexpr (MODE == KV_FP8) {
+    const u32x4 w4 = r.w[blk][s >> 1];
+    const u32x2 c8 = (s & 1) ? u32x2{w4[2], w4[3]} : u32x2{w4[0], w4[1]};  // the codes of k-step s
+    if constexpr (UPG) {
+      if (which) return fp8x8_to_bf16x8(c8, p.v_scale * r.sc[blk]);
+      return fp8x8_to_bf16x8_exact(c8);
+    } else {
+      return fp8x8_to_bf16x8(c8, (which ? p.v_scale : p.k_scale) * r.sc[blk]);
+    }
   } else if constexpr (MODE == KV_BF16_SCALED) {
     return scale_bf16x8(r.w[blk][s], which ? p.v_scale : p.k_scale);
   } else {
@@ -649,7 +666,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     s0 *= ks;
     s1 *= ks;
   }
-  load_q(p, nx, n, j, wv, q);
+  load_q<MODE>(p, nx, n, j, wv, q);
 
   // V^T into LDS: key t = 16*blk + n goes to slot pos = 8*(n/4) + 4*blk + n%4 of each dim row
   wave_lds_fence();
@@ -662,7 +679,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         uint32_t w = vw[t];
-        int d = 32 * s + 8 * j + 2 * t;
+        int d = kdim<MODE>(j, s) + 2 * t;
         *(uint16_t*)(vt + d * kVTRow + slot_b) = (uint16_t)(w & 0xffffu);
         *(uint16_t*)(vt + (d + 1) * kVTRow + slot_b) = (uint16_t)(w >> 16);
       }
@@ -1382,7 +1399,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         load_half<MODE>(p, a0, 0, ka);
         load_half<MODE>(p, a0, 1, va);
       }
-      load_q(p, cur, n, j, wv, q);
+      load_q<MODE>(p, cur, n, j, wv, q);
       RowState st;
 
       long long u = u0;
