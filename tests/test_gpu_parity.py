@@ -159,6 +159,16 @@ def test_fp8_kv_per_page_scales(cuda):
     assert err["max_abs"] <= TOL_FP8_VS_SOURCE
 
 
+@pytest.mark.parametrize("page", [16, 24])
+def test_fp8_kv_unaligned_pages(cuda, page):
+    # page sizes that are not a multiple of 32: each key of a 32-key unit carries its own page id
+    # and scales (the per-key path); several keys per sequence, so the K dims of the scores are
+    # checked too (a single key's weight is 1 whatever its score)
+    _say(f"fp8 KV, page size {page}")
+    _check(make_custom(kv_lens=[2, 31, 70, 333], q_lens=[1, 1, 1, 4], num_q_heads=16, num_kv_heads=4,
+                       page_size=page, seed=33 + page, kv_dtype="fp8"))
+
+
 def test_fp8_decode_matches_format_definition(cuda):
     _say("fp8 codes decode per the OCP E4M3FN definition")
     # one page per sequence, every finite code in some V position; a single-key sequence
