@@ -1,0 +1,126 @@
+"""Workload contracts (``render-workload`` / ``experiment``) on the CPU.
+
+The experiment id and schedule hash are recomputed independently from the artifacts, the launch
+plan's stream-K unit counts are recounted row by row, and the contracts' tensors are checked
+against the generated benchmark cases."""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+import pathlib
+import re
+
+import numpy as np
+import pytest
+
+from tpu_cake_amd import contracts
+from tpu_cake_amd.workloads import config_meta, make_config
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+KERNEL_SRC = (ROOT / "tpu-cake_amd" / "csrc" / "rpa_kernels.hip").read_text()
+
+
+@pytest.mark.parametrize("name", sorted(contracts.WORKLOADS))
+def test_artifacts_are_deterministic_and_self_consistent(name):
+    text = contracts.render_workload(name)
+    assert text == contracts.render_workload(name)
+    exp = contracts.experiment(name)
+    assert exp.schedule_sha256 == hashlib.sha256(text.encode()).hexdigest()
+    art = json.loads(contracts.experiment_artifact_json(exp))
+    # the id is sha256 of the artifact without it: sorted keys, compact separators
+    body = dict(art)
+    ident = body.pop("experiment_id")
+    assert ident == hashlib.sha256(json.dumps(body, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
+    # the artifact parses back into the same experiment
+    again = contracts.KernelExperiment.model_validate(body)
+    assert again.experiment_id == ident
+    assert exp.target.accelerator == "MI355X" and exp.target.chip_count == 1
+    # every kernel the profile requires is a kernel of the library
+    for k in exp.profile.required_timed_hlo_markers:
+        assert re.search(rf"__global__[^\n]*\b{k}\(", KERNEL_SRC), k
+    for src in exp.workload.execution.source_manifest:
+        assert src.sha256 == hashlib.sha256((ROOT / src.path).read_bytes()).hexdigest()
+
+
+def test_ids_differ_between_workloads_and_follow_content():
+    ids = {n: contracts.experiment(n).experiment_id for n in contracts.WORKLOADS}
+    assert len(set(ids.values())) == len(ids)
+    exp = contracts.experiment("mi355x-rpa-c2")
+    changed = exp.model_copy(update={"benchmark": exp.benchmark.model_copy(update={"measured_iterations": 51})})
+    assert changed.experiment_id != exp.experiment_id
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c4", "c5"])
+def test_operator_contract_tensors(cfg):
+    exp = contracts.experiment(f"mi355x-rpa-{cfg}")
+    m = config_meta(cfg)
+    t = {x.name: x for x in exp.workload.inputs}
+    assert t["q"].shape == (int(np.sum(m.q_lens)), m.num_q_heads, 128)
+    assert t["kv_pages"].shape == (m.pool_pages, m.page_size, 2 * m.num_kv_heads, 128)
+    assert t["page_indices"].shape == (len(m.kv_lens), m.pages_per_seq)
+    assert t["cu_q_lens"].shape == (len(m.kv_lens) + 1,)
+    assert (t["kv_pages"].dtype == "f8e4m3") == (cfg == "c4") and (("kv_scales" in t) == (cfg == "c4"))
+    assert exp.workload.stage.value == ("mixed" if cfg == "c3" else "steady_decode")
+    assert exp.workload.outputs[0].shape == t["q"].shape
+
+
+def test_config_meta_matches_generated_case():
+    case = make_config("c1", values="host")
+    m = config_meta("c1")
+    assert np.array_equal(case.kv_lens, m.kv_lens)
+    assert case.kv_pages.shape[0] == m.pool_pages and case.page_indices.shape[1] == m.pages_per_seq
+    assert m.kv_read_bytes() == case.kv_read_bytes()
+
+
+def _units_by_rows(kv_len, q_len, group):
+    """Stream-K units recounted from the rows: a 16-row block visits the keys its last row sees."""
+    rows = q_len * group
+    units = 0
+    for r0 in range(0, rows, 16):
+        last_tok = (min(r0 + 15, rows - 1)) // group
+        visible = kv_len - q_len + last_tok + 1
+        units += math.ceil(visible / 32)
+    return units
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c5"])
+def test_plan_unit_counts(cfg):
+    m = config_meta(cfg)
+    group = m.num_q_heads // m.num_kv_heads
+    hg = max(g for g in range(1, min(m.num_kv_heads, 8) + 1) if m.num_kv_heads % g == 0)
+    W = sum(_units_by_rows(int(L), int(q), group) for L, q in zip(m.kv_lens, m.q_lens)) * (m.num_kv_heads // hg)
+    text = contracts.render_workload(f"mi355x-rpa-{cfg}")
+    assert f"stream-K = {W} units" in text
+    grid = 256 * (8 // hg)
+    lo, hi = W // grid, -(-W // grid)
+    assert f"({lo}..{hi} units each)" in text
+
+
+def test_mixed_plan_splits_prefill_and_decode():
+    text = contracts.render_workload("mi355x-rpa-c3")
+    m = config_meta("c3")
+    tiles = sum(math.ceil(int(q) / 64) * 8 for q in m.q_lens if q >= 16)
+    got = re.search(r"prefill tiles = (\d+) tiles of 64 tokens x 1 kv head \((\d+) chunk steps\) on (\d+) workgroups",
+                    text)
+    assert got and int(got.group(1)) == tiles
+    # chunk steps of the causal tiles: tile t of a 512-token chunk sees prior + 64 (t + 1) keys
+    steps = sum(8 * sum((int(L) - int(q) + 64 * (t + 1)) / 32 for t in range(math.ceil(int(q) / 64)))
+                for L, q in zip(m.kv_lens, m.q_lens) if q >= 16)
+    assert int(got.group(2)) == round(steps)
+    assert 0 < int(got.group(3)) < 256
+
+
+def test_cli_writes_artifacts(tmp_path, capsys):
+    out = tmp_path / "exp.json"
+    assert contracts.main(["experiment", "inkling-rpa", "--output", str(out)]) == 0
+    art = json.loads(out.read_text())
+    assert f"id={art['experiment_id']}" in capsys.readouterr().out
+    assert [t["name"] for t in art["workload"]["inputs"]] == [
+        "query", "key_cache", "value_cache", "page_table", "sequence_lengths", "relative_bias"]
+    plan = tmp_path / "plan.txt"
+    assert contracts.main(["render-workload", "inkling-rpa", "--output", str(plan)]) == 0
+    assert hashlib.sha256(plan.read_bytes()).hexdigest() == art["schedule_sha256"]
+    with pytest.raises(SystemExit):
+        contracts.main(["experiment", "no-such-workload"])

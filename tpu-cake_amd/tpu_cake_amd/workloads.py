@@ -186,41 +186,93 @@ def quantize_fp8(case: RpaCase) -> RpaCase:
                                kv_source=case.kv_pages)
 
 
-def make_config(cfg: str, seed: int | None = None, values: str = "auto") -> RpaCase:
-    """Build one of the benchmark configurations ``c1`` .. ``c5``."""
-    cfg = cfg.lower()
-    if seed is None:
-        seed = CONFIG_SEEDS[cfg]
-    rng = np.random.default_rng(seed)
-    vk = dict(values=_resolve_values(values), seed=seed)
+@dataclasses.dataclass(frozen=True)
+class ConfigMeta:
+    """Shapes and metadata of a benchmark configuration (no values): what a contract names."""
+    name: str
+    kv_lens: np.ndarray
+    q_lens: np.ndarray
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int
+    pool_pages: int
+    pages_per_seq: int
+    kv_dtype: str = "bf16"
+
+    @property
+    def num_tokens(self) -> int:
+        return int(np.sum(self.q_lens))
+
+    @property
+    def num_seqs(self) -> int:
+        return len(self.kv_lens)
+
+    def kv_read_bytes(self) -> int:
+        """sum(L) * Hkv * 2 * D * elem (+ the fp8 pool's per-(page, head) K and V scales)."""
+        toks = int(np.sum(self.kv_lens, dtype=np.int64))
+        elem = 1 if self.kv_dtype == "fp8" else 2
+        b = toks * self.num_kv_heads * 2 * self.head_dim * elem
+        if self.kv_dtype == "fp8":
+            b += int(np.sum(-(-self.kv_lens.astype(np.int64) // self.page_size))) * self.num_kv_heads * 2 * 4
+        return b
+
+    def prefill_flops(self) -> int:
+        """Causal QK^T + PV flops of rows with q_len > 1: 4*Hq*D*sum(visible keys)."""
+        total = 0
+        for L, ql in zip(self.kv_lens.tolist(), self.q_lens.tolist()):
+            if ql > 1:
+                total += ql * (L - ql) + ql * (ql + 1) // 2
+        return 4 * self.num_q_heads * self.head_dim * total
+
+
+def _config_meta(cfg: str, rng) -> ConfigMeta:
+    """The lengths and shapes of ``cfg``, drawn from ``rng`` (the first draws of make_config)."""
     if cfg == "c1":
         lens = rng.integers(1, 512, size=4, endpoint=True)
-        return build_case("c1", kv_lens=lens, q_lens=np.ones(4), num_q_heads=8, num_kv_heads=2,
-                          head_dim=128, page_size=16, pool_pages=160, pages_per_seq=32, rng=rng, **vk)
+        return ConfigMeta("c1", lens, np.ones(4, np.int64), 8, 2, 128, 16, 160, 32)
     if cfg in ("c2", "c4"):
         z = rng.standard_normal(64)
         lens = np.clip(np.rint(np.exp(math.log(2048.0) + LOGNORMAL_SIGMA * z)), 128, 8192).astype(np.int64)
         pages = int(np.sum(-(-lens // 64)))
-        case = build_case(cfg, kv_lens=lens, q_lens=np.ones(64), num_q_heads=32, num_kv_heads=8,
-                          head_dim=128, page_size=64, pool_pages=math.ceil(POOL_FACTOR * pages),
-                          pages_per_seq=128, rng=rng, **vk)
-        return quantize_fp8(case) if cfg == "c4" else case
+        return ConfigMeta(cfg, lens, np.ones(64, np.int64), 32, 8, 128, 64, math.ceil(POOL_FACTOR * pages), 128,
+                          "fp8" if cfg == "c4" else "bf16")
     if cfg == "c3":
         dec = rng.integers(512, 8192, size=24, endpoint=True)
         prior = rng.integers(0, 3584, size=4, endpoint=True)
         lens = np.concatenate([dec, prior + 512])
         qls = np.concatenate([np.ones(24, dtype=np.int64), np.full(4, 512)])
         pages = int(np.sum(-(-lens // 64)))
-        return build_case("c3", kv_lens=lens, q_lens=qls, num_q_heads=32, num_kv_heads=8,
-                          head_dim=128, page_size=64, pool_pages=math.ceil(POOL_FACTOR * pages),
-                          pages_per_seq=128, rng=rng, **vk)
+        return ConfigMeta("c3", lens, qls, 32, 8, 128, 64, math.ceil(POOL_FACTOR * pages), 128)
     if cfg == "c5":
         lens = np.clip(np.floor(16.0 * (1.0 + rng.pareto(1.2, size=256))), 16, 131072).astype(np.int64)
         pages = int(np.sum(-(-lens // 64)))
-        return build_case("c5", kv_lens=lens, q_lens=np.ones(256), num_q_heads=64, num_kv_heads=8,
-                          head_dim=128, page_size=64, pool_pages=math.ceil(POOL_FACTOR * pages),
-                          pages_per_seq=2048, rng=rng, **vk)
+        return ConfigMeta("c5", lens, np.ones(256, np.int64), 64, 8, 128, 64, math.ceil(POOL_FACTOR * pages), 2048)
     raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+
+
+def config_meta(cfg: str, seed: int | None = None) -> ConfigMeta:
+    """Shapes and lengths of configuration ``cfg`` (the same draws as make_config), no values."""
+    cfg = cfg.lower()
+    if cfg not in CONFIG_SEEDS:
+        raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+    return _config_meta(cfg, np.random.default_rng(CONFIG_SEEDS[cfg] if seed is None else seed))
+
+
+def make_config(cfg: str, seed: int | None = None, values: str = "auto") -> RpaCase:
+    """Build one of the benchmark configurations ``c1`` .. ``c5``."""
+    cfg = cfg.lower()
+    if cfg not in CONFIG_SEEDS:
+        raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+    if seed is None:
+        seed = CONFIG_SEEDS[cfg]
+    rng = np.random.default_rng(seed)
+    m = _config_meta(cfg, rng)
+    case = build_case(cfg, kv_lens=m.kv_lens, q_lens=m.q_lens, num_q_heads=m.num_q_heads,
+                      num_kv_heads=m.num_kv_heads, head_dim=m.head_dim, page_size=m.page_size,
+                      pool_pages=m.pool_pages, pages_per_seq=m.pages_per_seq, rng=rng,
+                      values=_resolve_values(values), seed=seed)
+    return quantize_fp8(case) if cfg == "c4" else case
 
 
 def make_custom(*, kv_lens, q_lens, num_q_heads, num_kv_heads, head_dim=128, page_size=16,
