@@ -57,6 +57,7 @@ namespace {
 
 constexpr int kD = 128;          // head_dim built
 constexpr int kVTRow = 80;       // bytes per LDS row (one dim) of the transposed V chunk: 64 + 16 pad
+constexpr int kVtBytes_ = 128 * kVTRow;  // one wave's transposed V chunk
 constexpr int kMaxWavesPerCU = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.f;  // lazy softmax rescale threshold (log2 units)
@@ -246,6 +247,13 @@ __device__ __forceinline__ int opaque_zero() {
   int z;
   asm volatile("v_mov_b32 %0, 0" : "=v"(z));
   return z;
+}
+
+// A non-temporal (streaming) load: for lines read once, and only where one load instruction covers
+// whole 128-byte lines (with half-line loads the second half misses a line already dropped).
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T* ptr) {
+  return __builtin_nontemporal_load(ptr);
 }
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -646,6 +654,92 @@ struct RowState {
   bool started_here;
 };
 
+// The unit's scores s0, s1 (keys 16*blk + 4j + rr of row n) -> online-softmax update of st and
+// P^T packed for the PV MFMA.  bias (KV_BF16_BIAS): the relative bias of those scores.
+template <int MODE>
+__device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x, f32x4 s0, f32x4 s1,
+                                               const f32x4* bias, RowState& st, int j) {
+  // scores in log2 units; this lane holds keys 16*blk + 4j + rr of row n.  A chunk every row
+  // of the block sees in full (no window, no soft cap) needs no per-score masking.
+  float xs[2][4];
+  const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
+  bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
+               (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
+  if (plain) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      xs[0][rr] = s0[rr] * p.scale_log2;
+      xs[1][rr] = s1[rr] * p.scale_log2;
+      if constexpr (MODE == KV_BF16_BIAS) {  // the table holds 0 for keys outside the window
+        xs[0][rr] += bias[0][rr] * kLog2e;
+        xs[1][rr] += bias[1][rr] * kLog2e;
+      }
+    }
+  } else {
+    const int key0 = x.c * KV_CHUNK + 4 * j;
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float sv = blk ? s1[rr] : s0[rr];
+        float xv;
+        if (p.soft_cap > 0.f) {
+          float t = sv * p.sm_scale;
+          xv = p.soft_cap * tanhf(t / p.soft_cap) * kLog2e;
+        } else {
+          xv = sv * p.scale_log2;
+        }
+        int kt = key0 + 16 * blk + rr;
+        if constexpr (MODE == KV_BF16_BIAS) xv += bias[blk][rr] * kLog2e;
+        bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
+        if (masked) xv += p.mask_log2;
+        if (kt >= x.kv_len) xv = -INFINITY;
+        xs[blk][rr] = xv;
+      }
+  }
+
+  // Online softmax with a lazily moved reference: st.m only moves when a row's chunk maximum
+  // exceeds it by more than kRescaleLog2 (probabilities then stay <= 2^kRescaleLog2), so most
+  // chunks skip the rescale of l and acc.  Any reference gives the same normalised result.
+  float mc = fmaxf(fmaxf(fmaxf(xs[0][0], xs[0][1]), fmaxf(xs[0][2], xs[0][3])),
+                   fmaxf(fmaxf(xs[1][0], xs[1][1]), fmaxf(xs[1][2], xs[1][3])));
+  mc = rows4_max(mc);
+  const bool grow = mc > st.m + kRescaleLog2;
+  if (__ballot(grow)) {
+    const float mn = grow ? mc : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
+    st.l *= alpha;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+    st.m = mn;
+  }
+  const float mu = st.m == -INFINITY ? 0.f : st.m;
+  float pr[2][4];
+  float lsum = 0.f;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      pr[blk][rr] = __builtin_amdgcn_exp2f(xs[blk][rr] - mu);
+      lsum += pr[blk][rr];
+    }
+  st.l += lsum;
+
+  u32x4 pw;
+  pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
+  pw[1] = pack_bf16x2(pr[0][2], pr[0][3]);
+  pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
+  pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
+  const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+  return pb;
+}
+
+template <int MODE>
+__device__ __forceinline__ const f32x4* bias_of(const HalfRegs<MODE>& r) {
+  if constexpr (MODE == KV_BF16_BIAS) return r.bias;
+  return nullptr;
+}
+
 // One unit.  S = K Q^T; then the next unit's queries are loaded into q (their registers are
 // free once QK^T has issued); V^T goes to LDS, after which the next unit's V is loaded into the
 // registers just released; then softmax and O^T += V^T P^T.
@@ -687,78 +781,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   }
   load_half<MODE>(p, nx_addr, 1, v_next);
 
-  // scores in log2 units; this lane holds keys 16*blk + 4j + rr of row n.  A chunk every row
-  // of the block sees in full (no window, no soft cap) needs no per-score masking.
-  float xs[2][4];
-  const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
-  bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
-               (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
-  if (plain) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      xs[0][rr] = s0[rr] * p.scale_log2;
-      xs[1][rr] = s1[rr] * p.scale_log2;
-      if constexpr (MODE == KV_BF16_BIAS) {  // the table holds 0 for keys outside the window
-        xs[0][rr] += kr.bias[0][rr] * kLog2e;
-        xs[1][rr] += kr.bias[1][rr] * kLog2e;
-      }
-    }
-  } else {
-    const int key0 = x.c * KV_CHUNK + 4 * j;
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        float sv = blk ? s1[rr] : s0[rr];
-        float xv;
-        if (p.soft_cap > 0.f) {
-          float t = sv * p.sm_scale;
-          xv = p.soft_cap * tanhf(t / p.soft_cap) * kLog2e;
-        } else {
-          xv = sv * p.scale_log2;
-        }
-        int kt = key0 + 16 * blk + rr;
-        if constexpr (MODE == KV_BF16_BIAS) xv += kr.bias[blk][rr] * kLog2e;
-        bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
-        if (masked) xv += p.mask_log2;
-        if (kt >= x.kv_len) xv = -INFINITY;
-        xs[blk][rr] = xv;
-      }
-  }
-
-  // Online softmax with a lazily moved reference: st.m only moves when a row's chunk maximum
-  // exceeds it by more than kRescaleLog2 (probabilities then stay <= 2^kRescaleLog2), so most
-  // chunks skip the rescale of l and acc.  Any reference gives the same normalised result.
-  float mc = fmaxf(fmaxf(fmaxf(xs[0][0], xs[0][1]), fmaxf(xs[0][2], xs[0][3])),
-                   fmaxf(fmaxf(xs[1][0], xs[1][1]), fmaxf(xs[1][2], xs[1][3])));
-  mc = rows4_max(mc);
-  const bool grow = mc > st.m + kRescaleLog2;
-  if (__ballot(grow)) {
-    const float mn = grow ? mc : st.m;
-    const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
-    st.l *= alpha;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
-    st.m = mn;
-  }
-  const float mu = st.m == -INFINITY ? 0.f : st.m;
-  float pr[2][4];
-  float lsum = 0.f;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      pr[blk][rr] = __builtin_amdgcn_exp2f(xs[blk][rr] - mu);
-      lsum += pr[blk][rr];
-    }
-  st.l += lsum;
-
-  u32x4 pw;
-  pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
-  pw[1] = pack_bf16x2(pr[0][2], pr[0][3]);
-  pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
-  pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
-  const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+  const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j);
 
   wave_lds_fence();
 #pragma unroll
@@ -859,6 +882,179 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   nxt = ahead;
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// full-line decode path (bf16 KV, page size a multiple of 32)
+// ---------------------------------------------------------------------------------------------
+// The path above loads K and V straight into the MFMA operand layout: 16 keys x 64 bytes per load
+// instruction, half of every 128-byte line.  Here a wave loads its kv head's K (then V) rows of a
+// unit as whole lines -- load i covers keys 4i .. 4i+3, lane L holding key 4i + L/16, dims
+// 8*(L%16) .. +7 -- with non-temporal loads, since every line is read once.  K goes to a
+// wave-private LDS tile (key rows, 272-byte stride: conflict-free A fragments), written at the end
+// of the step that loaded it and read by the next step's QK^T; V^T is written as before (key order
+// tau) with its 16-byte key groups XOR-swizzled by row bits 3-4, so the 16 dim rows one
+// transposing store touches fall in different banks.  Measured on C2's pool (a loads + LDS probe
+// of both patterns): 104 vs 111 us per 638 MB.  One K and one V register set suffice: K of the
+// next unit lands while this unit's K is read from the tile, V of the next unit is loaded once this
+// unit's V^T is stored.
+constexpr int kKtRow = kD * 2 + 16;
+constexpr int kKtBytes = KV_CHUNK * kKtRow;
+constexpr int kWaveLds = kVtBytes_ + kKtBytes;
+
+template <int MODE, bool UPG>
+struct LinePath {
+  static constexpr bool on = UPG && (MODE == KV_BF16 || MODE == KV_BF16_SCALED || MODE == KV_BF16_BIAS);
+};
+
+struct LineRegs {
+  u32x4 w[8];  // load i: key 4i + lane/16, dims 8*(lane%16) .. +7 of the K (or V) row
+};
+
+struct LineAddr {
+  size_t e0;    // element index of this lane's dims of the unit's first key, K row
+  int kmax;     // the unit's last key with data (keys past it read it instead)
+  int bias_at;  // as UnitAddr
+};
+
+__device__ __forceinline__ int vt_swz(int row, int g) { return g ^ ((row >> 3) & 3); }
+
+__device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, const Pages& pages, int lane, int n,
+                                              int j, int wv, int& err) {
+  const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err);  // page checks, head, bias position
+  LineAddr a;
+  const bool live = x.nch > 0;
+  a.e0 = kv_elem(p, u.pg[0], live ? x.c * KV_CHUNK : 0, 2 * u.h) + 8 * (lane & 15);
+  const int k = live ? x.kv_len - 1 - x.c * KV_CHUNK : 0;
+  a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
+  a.bias_at = u.bias_at;
+  return a;
+}
+
+// which = 0: K rows (combined head 2h), 1: V rows (2h+1).
+__device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, int lane, int which, LineRegs& r) {
+  const uint16_t* kv = (const uint16_t*)p.kv + a.e0 + (size_t)which * kD;
+  const size_t row = (size_t)(2 * p.Hkv) * kD;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int key = 4 * i + (lane >> 4);
+    key = key < a.kmax ? key : a.kmax;
+    r.w[i] = ld_stream((const u32x4*)(kv + (size_t)key * row));
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ void load_line_bias(const Params& p, const LineAddr& a, f32x4 bias[2]) {
+  if constexpr (MODE == KV_BF16_BIAS) {
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at + 16 * blk);  // aligned
+  }
+}
+
+template <int MODE>
+__device__ __forceinline__ u32x4 line_word(const LineRegs& r, int i, const Params& p, int which) {
+  if constexpr (MODE == KV_BF16_SCALED) return scale_bf16x8(r.w[i], which ? p.v_scale : p.k_scale);
+  return r.w[i];
+}
+
+// K of a unit into the wave's K tile.
+template <int MODE>
+__device__ __forceinline__ void store_k_tile(const Params& p, const LineRegs& k, uint8_t* kt, int lane) {
+  wave_lds_fence();  // the tile's previous unit has been read
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    *(u32x4*)(kt + (4 * i + (lane >> 4)) * kKtRow + (lane & 15) * 16) = line_word<MODE>(k, i, p, 0);
+}
+
+// compute_unit with K read from the K tile, V^T stored from the line layout (swizzled) and the
+// next unit's V loaded into v (after its V^T store).
+template <int MODE>
+__device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor& x, LineRegs& v, const f32x4* bias,
+                                                  bf16x8 q[4], const Cursor& nx, const LineAddr& nx_addr,
+                                                  RowState& st, uint8_t* vt, const uint8_t* kt, int lane, int n,
+                                                  int j, int wv) {
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const bf16x8 a0 = *(const bf16x8*)(kt + n * kKtRow + (32 * s + 8 * j) * 2);
+    const bf16x8 a1 = *(const bf16x8*)(kt + (16 + n) * kKtRow + (32 * s + 8 * j) * 2);
+    s0 = mfma(a0, q[s], s0);
+    s1 = mfma(a1, q[s], s1);
+  }
+  load_q<MODE>(p, nx, n, j, wv, q);
+
+  // V^T: key t = 4i + lane/16 goes to position tau^-1(t) = 8*((t%16)/4) + 4*(t/16) + t%4 of each
+  // dim row, i.e. 16-byte group i%4 (swizzled), element 4*(i/4) + lane/16
+  wave_lds_fence();
+  const int e = lane >> 4, d0 = 8 * (lane & 15);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 vw = line_word<MODE>(v, i, p, 1);
+    const int g = i & 3, off = 2 * (4 * (i >> 2) + e);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int d = d0 + 2 * t;
+      *(uint16_t*)(vt + d * kVTRow + 16 * vt_swz(d, g) + off) = (uint16_t)(vw[t] & 0xffffu);
+      *(uint16_t*)(vt + (d + 1) * kVTRow + 16 * vt_swz(d + 1, g) + off) = (uint16_t)(vw[t] >> 16);
+    }
+  }
+  load_lines(p, nx_addr, lane, 1, v);
+
+  const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
+
+  wave_lds_fence();
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const int row = 16 * d + n;
+    const bf16x8 a = *(const bf16x8*)(vt + row * kVTRow + 16 * vt_swz(row, j));
+    st.acc[d] = mfma(a, pb, st.acc[d]);
+  }
+}
+
+template <int MODE, bool UPG>
+__device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, int n, int j, int b, long long u,
+                                          long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
+                                          Pages& pg_nxt, LineRegs& k, LineRegs& v, f32x4 bias[2], bf16x8 q[4],
+                                          RowState& st, uint8_t* vt, uint8_t* kt, int& err, const Partition& pt,
+                                          int wv) {
+  Cursor ahead = nxt;
+  if (u + 2 < u1)
+    advance(p, nseq, lane, win, ahead, err);
+  else
+    ahead.nch = 0;
+  const Pages pg_ahead = load_pages<UPG>(p, ahead, n);
+  const LineAddr nx_addr = line_addr(p, nxt, pg_nxt, lane, n, j, wv, err);
+  __syncthreads();
+  load_lines(p, nx_addr, lane, 0, k);  // the next unit's K (this unit's K is in the tile)
+  f32x4 bias_nx[2];
+  load_line_bias<MODE>(p, nx_addr, bias_nx);
+
+  if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
+  compute_unit_line<MODE>(p, cur, v, bias, q, nxt, nx_addr, st, vt, kt, lane, n, j, wv);
+  const bool last_of_rb = cur.c == cur.nch - 1;
+  if (last_of_rb || u == u1 - 1) {
+    const bool complete = st.started_here && last_of_rb;
+    finish_row_block(p, cur, st, b, complete, n, j, wv);
+    if (!complete && !st.started_here && last_of_rb && lane == 0) {
+      SplitDesc* d = p.desc + b;
+      d->nch = cur.nch;
+      d->q_start = cur.q_start;
+      d->q_len = cur.q_len;
+      d->h = cur.h;
+      d->rb = cur.rb;
+      d->b0 = owner_of(u - cur.c, pt);
+      d->valid[wv] = 1;
+    }
+  }
+  store_k_tile<MODE>(p, k, kt, lane);
+  if constexpr (MODE == KV_BF16_BIAS) {
+    bias[0] = bias_nx[0];
+    bias[1] = bias_nx[1];
+  }
+
+  pg_nxt = pg_ahead;
+  cur = nxt;
+  nxt = ahead;
+}
 
 // ---------------------------------------------------------------------------------------------
 // prefill tiles (sequences with many query tokens)
@@ -1257,10 +1453,11 @@ __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], i
 
 template <int MODE, bool UPG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x transposed V chunk
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x (transposed V chunk, K tile)
   const int lane = threadIdx.x & 63;
   const int wv = uni(threadIdx.x >> 6);
-  uint8_t* vt = smem + wv * (kD * kVTRow);
+  uint8_t* vt = smem + wv * kWaveLds;  // this wave's V^T chunk, then its K tile (full-line path)
+  uint8_t* kt = vt + kVtBytes_;
   const int n = lane & 15, j = lane >> 4;
   const int b = blockIdx.x;
   int err = 0;
@@ -1392,22 +1589,45 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         nxt.nch = 0;
       const Pages pg_cur = load_pages<UPG>(p, cur, n);
       Pages pg_nxt = load_pages<UPG>(p, nxt, n);
-      HalfRegs<MODE> ka, va, kb, vb;
-      bf16x8 q[4];
-      {
-        const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err);
-        load_half<MODE>(p, a0, 0, ka);
-        load_half<MODE>(p, a0, 1, va);
-      }
-      load_q<MODE>(p, cur, n, j, wv, q);
-      RowState st;
+      if constexpr (LinePath<MODE, UPG>::on) {
+        LineRegs k, v;
+        f32x4 bias[2];
+        bf16x8 q[4];
+        {
+          const LineAddr a0 = line_addr(p, cur, pg_cur, lane, n, j, wv, err);
+          load_lines(p, a0, lane, 0, k);
+          load_lines(p, a0, lane, 1, v);
+          load_line_bias<MODE>(p, a0, bias);
+        }
+        load_q<MODE>(p, cur, n, j, wv, q);
+        store_k_tile<MODE>(p, k, kt, lane);
+        RowState st;
+        long long u = u0;
+        for (;;) {
+          step_line<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, k, v, bias, q, st, vt, kt,
+                               err, pt, wv);
+          if (++u >= u1) break;
+        }
+      } else {
+        HalfRegs<MODE> ka, va, kb, vb;
+        bf16x8 q[4];
+        {
+          const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err);
+          load_half<MODE>(p, a0, 0, ka);
+          load_half<MODE>(p, a0, 1, va);
+        }
+        load_q<MODE>(p, cur, n, j, wv, q);
+        RowState st;
 
-      long long u = u0;
-      for (;;) {
-        step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt, wv);
-        if (++u >= u1) break;
-        step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt, wv);
-        if (++u >= u1) break;
+        long long u = u0;
+        for (;;) {
+          step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt,
+                          wv);
+          if (++u >= u1) break;
+          step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt,
+                          wv);
+          if (++u >= u1) break;
+        }
       }
     }
   }
@@ -1638,7 +1858,7 @@ int heads_per_group(int hkv) {
   return 1;
 }
 
-constexpr int kVtBytes = kD * kVTRow;
+constexpr int kVtBytes = kWaveLds;  // LDS per wave: V^T chunk + K tile
 
 // Workgroups for the persistent grid: the kernel's occupancy (2 waves per SIMD) in workgroups
 // of hg waves, capped so no CU holds more than kMaxWavesPerCU waves.
