@@ -121,23 +121,31 @@ def test_padding_rows_and_seqs(cuda):
     _check(case)
 
 
-def test_sliding_window_soft_cap_mask(cuda):
-    _say("sliding window + soft cap")
-    case = make_custom(kv_lens=[300, 77], q_lens=[20, 1], num_q_heads=16, num_kv_heads=4, page_size=16, seed=19)
+# page sizes 16 (per-key page ids, 16-byte operand loads) and 32 / 64 (one page per 32-key unit: the
+# full-line path, K through the LDS tile); 8 kv heads fill a workgroup, 2 leave it at two waves
+@pytest.mark.parametrize("page,hkv", [(16, 4), (64, 8), (32, 2)])
+def test_sliding_window_soft_cap_mask(cuda, page, hkv):
+    _say(f"sliding window + soft cap, page {page}")
+    case = make_custom(kv_lens=[300, 77, 1000], q_lens=[12, 1, 1], num_q_heads=4 * hkv, num_kv_heads=hkv,
+                       page_size=page, seed=19 + page)
     kw = dict(sliding_window=50, soft_cap=5.0)
     _check(case, gpu_kw=kw, oracle_kw=kw)
 
 
-def test_custom_mask_value(cuda):
-    _say("finite mask value")
-    case = make_custom(kv_lens=[90], q_lens=[40], num_q_heads=8, num_kv_heads=2, page_size=16, seed=23)
+@pytest.mark.parametrize("page", [16, 64])
+def test_custom_mask_value(cuda, page):
+    _say(f"finite mask value, page {page}")
+    case = make_custom(kv_lens=[90, 333], q_lens=[40, 1], num_q_heads=8, num_kv_heads=2, page_size=page,
+                       seed=23 + page)
     kw = dict(mask_value=-3.0)
     _check(case, gpu_kw=kw, oracle_kw=kw)
 
 
-def test_scalar_kv_scales_bf16(cuda):
-    _say("scalar k_scale / v_scale on bf16 KV")
-    case = make_custom(kv_lens=[129, 64], q_lens=[1, 1], num_q_heads=8, num_kv_heads=2, page_size=16, seed=29)
+@pytest.mark.parametrize("page", [16, 64])
+def test_scalar_kv_scales_bf16(cuda, page):
+    _say(f"scalar k_scale / v_scale on bf16 KV, page {page}")
+    case = make_custom(kv_lens=[129, 64, 700], q_lens=[1, 1, 3], num_q_heads=32, num_kv_heads=8, page_size=page,
+                       seed=29 + page)
     kw = dict(k_scale=0.75, v_scale=1.5)
     _check(case, gpu_kw=kw, oracle_kw=kw)
 
