@@ -98,6 +98,19 @@ def test_plan_unit_counts(cfg):
     assert f"({lo}..{hi} units each)" in text
 
 
+def test_plan_lds_matches_kernel_constants():
+    # the per-wave LDS the host requests, restated from the kernel's own constants
+    const = {k: int(v) for k, v in re.findall(r"constexpr int (kVTRow|kD|KV_CHUNK) = (\d+);",
+                                               KERNEL_SRC + (ROOT / "tpu-cake_amd" / "csrc" / "rpa_schedule.h").read_text())}
+    kt_row = const["kD"] * 2 + 16
+    assert re.search(r"constexpr int kKtRow = kD \* 2 \+ 16;", KERNEL_SRC)
+    per_wave = const["kD"] * const["kVTRow"] + const["KV_CHUNK"] * kt_row
+    assert contracts.WAVE_LDS_BYTES == per_wave
+    assert f"LDS {8 * per_wave} B" in contracts.render_workload("mi355x-rpa-c2")
+    assert "whole 128-byte K/V lines" in contracts.render_workload("mi355x-rpa-c2")
+    assert "16-byte operand loads" in contracts.render_workload("mi355x-rpa-c4")
+
+
 def test_mixed_plan_splits_prefill_and_decode():
     text = contracts.render_workload("mi355x-rpa-c3")
     m = config_meta("c3")

@@ -198,6 +198,9 @@ MI355X_BF16_FLOPS = 2_500_000_000_000_000   # dense bf16 MFMA, AMD's published p
 WAVES_PER_CU = 8                            # the attention kernel: 2 waves per SIMD
 KV_CHUNK = 32                               # keys per stream-K unit (csrc/rpa_schedule.h)
 ROW_BLOCK = 16
+# LDS per wave of the attention kernel: the transposed V chunk (128 dim rows x 80 B) and the K tile
+# of the full-line path (32 key rows x 272 B) (csrc/rpa_kernels.hip, kVTRow / kKtRow)
+WAVE_LDS_BYTES = 128 * 80 + KV_CHUNK * (128 * 2 + 16)
 PF_MIN = 16                                 # query tokens that make a sequence a prefill one
 PF_COST = 0.45                              # prefill chunk-step cost in stream-K units
 
@@ -317,6 +320,8 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
     hg = split["heads_per_workgroup"]
     unit_bytes = hg * KV_CHUNK * 2 * m.head_dim * (1 if m.kv_dtype == "fp8" else 2)
     mode = "KV_FP8" if m.kv_dtype == "fp8" else "KV_BF16"
+    upg = m.page_size % KV_CHUNK == 0
+    line = upg and m.kv_dtype != "fp8"
     floor_hbm = (kv_bytes + qo_bytes) / MI355X_HBM_BYTES_PER_S * 1e6
     floor_mfma = flops / MI355X_BF16_FLOPS * 1e6
     lines = [
@@ -325,9 +330,10 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
         f"sequences = {m.num_seqs}; query tokens = {m.num_tokens}; sum kv_len = {int(sum(m.kv_lens))}",
         f"heads = Hq {m.num_q_heads} / Hkv {m.num_kv_heads} (G {split['group']}); head_dim {m.head_dim}; "
         f"page_size {m.page_size}; pool pages {m.pool_pages}; pages per sequence {m.pages_per_seq}",
-        f"launch 0 = rpa_attn_kernel<{mode}, page ids per {'chunk' if m.page_size % KV_CHUNK == 0 else 'key'}>: "
+        f"launch 0 = rpa_attn_kernel<{mode}, page ids per {'chunk' if upg else 'key'}>: "
         f"grid {split['grid']} x block {64 * hg} ({hg} kv heads per workgroup, one wave each; "
-        f"{WAVES_PER_CU} waves per CU), LDS {hg * 128 * 80} B",
+        f"{WAVES_PER_CU} waves per CU), LDS {hg * WAVE_LDS_BYTES} B",
+        f"  decode loads = {'whole 128-byte K/V lines, K through an LDS tile' if line else '16-byte operand loads'}",
         f"  stream-K = {split['stream_k_units']} units of {KV_CHUNK} keys x (sequence, kv-head group, "
         f"{ROW_BLOCK}-row block) over {split['stream_k_workgroups']} workgroups "
         f"({split['units_per_workgroup'][0]}..{split['units_per_workgroup'][1]} units each); "
