@@ -65,6 +65,7 @@ constexpr float kDefaultMask = -0.7f * 3.4028234663852886e38f;  // ragged_paged_
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -497,7 +498,8 @@ __host__ __device__ __forceinline__ int bias_chunk_lo(int kv_len, int E) { retur
 template <>
 struct HalfRegs<KV_FP8> {
   u32x4 w[2][2];  // 16 codes per load: dims kdim(j, 2i) .. +7 and kdim(j, 2i+1) .. +7 (see kdim)
-  float sc[2];    // per-(page, kv head) scale of each of the lane's two keys (k_scale/v_scale not applied)
+  float sc[2];    // per-(page, kv head) scale of each of the lane's two keys (k_scale/v_scale not
+                  // applied); UPG: the K registers hold the unit's page's (K, V) scales, V's none
 };
 
 // The 8 dims lane group j holds in MFMA k-step s (QK^T; the same for K, Q and V^T rows).  bf16:
@@ -549,7 +551,7 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
 }
 
 // which = 0 loads K (combined head 2h), 1 loads V (2h+1, one row of kD further).
-template <int MODE>
+template <int MODE, bool UPG>
 __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, int which, HalfRegs<MODE>& r) {
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
@@ -562,8 +564,21 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 #pragma unroll
       for (int i = 0; i < 2; ++i) r.w[blk][i] = *(const u32x4*)(kp + 64 * i);
       // the raw per-(page, head) scale; multiplied in where it is used (to_bf16x8), a step later,
-      // so that nothing waits for this load here
-      r.sc[blk] = p.kv_scales ? p.kv_scales[((size_t)a.pg[blk] * p.Hkv + a.h) * 2 + which] : 1.f;
+      // so that nothing waits for this load here.  UPG: one page per unit, whose K and V scales
+      // (adjacent) come with K in one 8-byte load
+      if constexpr (UPG) {
+        if (which == 0 && blk == 0) {
+          if (p.kv_scales) {
+            const f32x2 kvs = *(const f32x2*)(p.kv_scales + ((size_t)a.pg[0] * p.Hkv + a.h) * 2);
+            r.sc[0] = kvs[0];
+            r.sc[1] = kvs[1];
+          } else {
+            r.sc[0] = r.sc[1] = 1.f;
+          }
+        }
+      } else {
+        r.sc[blk] = p.kv_scales ? p.kv_scales[((size_t)a.pg[blk] * p.Hkv + a.h) * 2 + which] : 1.f;
+      }
     } else {
       const uint16_t* kp = (const uint16_t*)p.kv + e;
 #pragma unroll
@@ -624,15 +639,17 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8_exact(u32x2 w) {
   return o;
 }
 
-// UPG fp8 K: a unit's 32 keys share one page, hence one K scale, applied to the unit's fp32
-// scores (compute_unit) instead of to every element.  V keeps the reference's bf16(v * scale).
+// UPG fp8: a unit's 32 keys share one page, hence one K and one V scale per head.  Both codes
+// convert exactly (e4m3 values are bf16 values); the K scale multiplies the unit's fp32 scores and
+// the V scale its fp32 probabilities before they are packed for the PV product (compute_unit),
+// i.e. P·(s·V) = (s·P)·V with the rounding to bf16 taken after the product s·P instead of
+// s·V.  Per-key pages (not UPG) apply bf16(v * scale) to every element.
 template <int MODE, bool UPG>
 __device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which) {
   if constexpr (MODE == KV_FP8) {
     const u32x4 w4 = r.w[blk][s >> 1];
     const u32x2 c8 = (s & 1) ? u32x2{w4[2], w4[3]} : u32x2{w4[0], w4[1]};  // the codes of k-step s
     if constexpr (UPG) {
-      if (which) return fp8x8_to_bf16x8(c8, p.v_scale * r.sc[blk]);
       return fp8x8_to_bf16x8_exact(c8);
     } else {
       return fp8x8_to_bf16x8(c8, (which ? p.v_scale : p.k_scale) * r.sc[blk]);
@@ -655,10 +672,11 @@ struct RowState {
 };
 
 // The unit's scores s0, s1 (keys 16*blk + 4j + rr of row n) -> online-softmax update of st and
-// P^T packed for the PV MFMA.  bias (KV_BF16_BIAS): the relative bias of those scores.
+// P^T packed for the PV MFMA, times p_scale (the unit's V scale, or 1; the denominator l stays
+// unscaled).  bias (KV_BF16_BIAS): the relative bias of those scores.
 template <int MODE>
 __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x, f32x4 s0, f32x4 s1,
-                                               const f32x4* bias, RowState& st, int j) {
+                                               const f32x4* bias, RowState& st, int j, float p_scale = 1.f) {
   // scores in log2 units; this lane holds keys 16*blk + 4j + rr of row n.  A chunk every row
   // of the block sees in full (no window, no soft cap) needs no per-score masking.
   float xs[2][4];
@@ -724,6 +742,10 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
       lsum += pr[blk][rr];
     }
   st.l += lsum;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) pr[blk][rr] *= p_scale;  // a constant 1 folds away
 
   u32x4 pw;
   pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
@@ -761,6 +783,8 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     s1 *= ks;
   }
   load_q<MODE>(p, nx, n, j, wv, q);
+  float vs = 1.f;
+  if constexpr (MODE == KV_FP8 && UPG) vs = p.v_scale * kr.sc[1];  // the unit's V scale (one page)
 
   // V^T into LDS: key t = 16*blk + n goes to slot pos = 8*(n/4) + 4*blk + n%4 of each dim row
   wave_lds_fence();
@@ -779,9 +803,9 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
       }
     }
   }
-  load_half<MODE>(p, nx_addr, 1, v_next);
+  load_half<MODE, UPG>(p, nx_addr, 1, v_next);
 
-  const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j);
+  const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j, vs);
 
   wave_lds_fence();
 #pragma unroll
@@ -855,7 +879,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   // keep the workgroup's waves (the kv heads of one group) in step, so the heads' slices of the
   // same keys reach the memory system together
   __syncthreads();
-  load_half<MODE>(p, nx_addr, 0, k_nxt);
+  load_half<MODE, UPG>(p, nx_addr, 0, k_nxt);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
   compute_unit<MODE, UPG>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j, wv);
@@ -1613,8 +1637,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         bf16x8 q[4];
         {
           const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err);
-          load_half<MODE>(p, a0, 0, ka);
-          load_half<MODE>(p, a0, 1, va);
+          load_half<MODE, UPG>(p, a0, 0, ka);
+          load_half<MODE, UPG>(p, a0, 1, va);
         }
         load_q<MODE>(p, cur, n, j, wv, q);
         RowState st;
