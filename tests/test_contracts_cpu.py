@@ -111,6 +111,15 @@ def test_plan_lds_matches_kernel_constants():
     assert "16-byte operand loads" in contracts.render_workload("mi355x-rpa-c4")
 
 
+def test_combine_grid_matches_kernel_constants():
+    const = dict(re.findall(r"constexpr int (kHeavyContrib|kHeavySlices) = (\d+);", KERNEL_SRC))
+    assert int(const["kHeavyContrib"]) == contracts.HEAVY_CONTRIB
+    assert int(const["kHeavySlices"]) == contracts.HEAVY_SLICES
+    # 256 workgroups of 8 kv heads: 2048 merges + 9 slots x 8 heads x 4 slices
+    assert contracts.combine_grid(256, 8) == 2048 + 288
+    assert f"grid {2048 + 288} x block 256" in contracts.render_workload("mi355x-rpa-c2")
+
+
 def test_mixed_plan_splits_prefill_and_decode():
     text = contracts.render_workload("mi355x-rpa-c3")
     m = config_meta("c3")

@@ -101,6 +101,16 @@ def test_long_sequence_split_k(cuda):
     _check(case)
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 8), (8, 2)])
+def test_heavy_merges(cuda, hq, hkv):
+    # several long sequences, each spread over dozens of workgroups (merged by the dim-sliced
+    # helper workgroups), with 4-, 8- and 16-row blocks, among short ones merged the ordinary way
+    _say(f"heavy merges hq={hq} hkv={hkv}")
+    case = make_custom(kv_lens=[6000, 40, 5000, 7, 7000, 300], q_lens=[1, 1, 4, 1, 2, 3], num_q_heads=hq,
+                       num_kv_heads=hkv, page_size=64, seed=41 + hq)
+    _check(case)
+
+
 def test_prefill_causal_self_attention(cuda):
     _say("prefill q_len == kv_len")
     case = make_custom(kv_lens=[64, 100], q_lens=[64, 100], num_q_heads=8, num_kv_heads=2, page_size=16, seed=11)

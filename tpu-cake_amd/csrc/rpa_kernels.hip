@@ -82,6 +82,16 @@ struct SplitDesc {
   long long b0;
 };
 
+// Heavy merges: a split row block with at least kHeavyContrib contributors (a long sequence spread
+// over many workgroups) is merged by kHeavySlices helper workgroups per head, each over 32 of the
+// 128 dims, instead of one.  Its contributors b0..b span at least kHeavyContrib - 1 workgroup
+// boundaries and the next heavy descriptor's first contributor is >= b, so b / (kHeavyContrib - 1)
+// differs between any two heavy descriptors of a call: that is its helper slot.
+constexpr int kHeavyContrib = 32;
+constexpr int kHeavySlices = 4;
+__host__ __device__ constexpr int heavy_slot(long long b) { return (int)(b / (kHeavyContrib - 1)); }
+__host__ __device__ constexpr int heavy_slots(int grid) { return (grid - 1) / (kHeavyContrib - 1) + 1; }
+
 struct Params {
   const uint16_t* q;
   const uint8_t* kv;
@@ -94,6 +104,7 @@ struct Params {
   float* part_acc;  // [2*grid][16][kD]
   float* part_ml;   // [2*grid][16][2]  (m in log2 units, l)
   struct SplitDesc* desc;  // [grid] split row block ending in workgroup b (valid = 0 otherwise)
+  int32_t* heavy;          // [heavy_slots(grid)][8 heads][kHeavySlices] b + 1 of a heavy descriptor (0 = none)
   int32_t* err;
   int T, Hq, Hkv, G, P, S, log2S, Nmax, PPS;
   int HG, NG;  // kv heads per workgroup (one wave each) and kv-head groups (Hkv / HG)
@@ -860,6 +871,26 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
   }
 }
 
+// Workgroup b owns the split row block's last unit u: describe the block for the combine (every
+// wave writes the same fields, its own valid flag and, for a heavy block, its head's helper flags).
+__device__ __forceinline__ void write_split_desc(const Params& p, const Cursor& cur, long long u, const Partition& pt,
+                                                 int b, int wv) {
+  SplitDesc* d = p.desc + b;
+  const long long b0 = owner_of(u - cur.c, pt);
+  d->nch = cur.nch;
+  d->q_start = cur.q_start;
+  d->q_len = cur.q_len;
+  d->h = cur.h;
+  d->rb = cur.rb;
+  d->b0 = b0;
+  d->valid[wv] = 1;
+  if (b - b0 + 1 >= kHeavyContrib) {
+    int32_t* f = p.heavy + ((size_t)heavy_slot(b) * 8 + wv) * kHeavySlices;
+#pragma unroll
+    for (int sl = 0; sl < kHeavySlices; ++sl) f[sl] = b + 1;
+  }
+}
+
 template <int MODE, bool UPG>
 __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n, int j, int b, long long u,
                                      long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
@@ -887,18 +918,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
     finish_row_block(p, cur, st, b, complete, n, j, wv);
-    if (!complete && !st.started_here && last_of_rb && lane == 0) {
-      // this workgroup owns the split row block's last unit: describe it for the combine (every
-      // wave writes the same fields and its own valid flag)
-      SplitDesc* d = p.desc + b;
-      d->nch = cur.nch;
-      d->q_start = cur.q_start;
-      d->q_len = cur.q_len;
-      d->h = cur.h;
-      d->rb = cur.rb;
-      d->b0 = owner_of(u - cur.c, pt);
-      d->valid[wv] = 1;
-    }
+    if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
 
   pg_nxt = pg_ahead;
@@ -1058,16 +1078,7 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
     finish_row_block(p, cur, st, b, complete, n, j, wv);
-    if (!complete && !st.started_here && last_of_rb && lane == 0) {
-      SplitDesc* d = p.desc + b;
-      d->nch = cur.nch;
-      d->q_start = cur.q_start;
-      d->q_len = cur.q_len;
-      d->h = cur.h;
-      d->rb = cur.rb;
-      d->b0 = owner_of(u - cur.c, pt);
-      d->valid[wv] = 1;
-    }
+    if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
   store_k_tile<MODE>(p, k, kt, lane);
   if constexpr (MODE == KV_BF16_BIAS) {
@@ -1722,25 +1733,10 @@ __device__ __forceinline__ void combine_rows(const Params& p, const SplitDesc& d
 // L = sum l * exp2(m - M), merged through LDS.  Pass 2 (combine_rows): the weighted sum of the
 // contributors' acc rows, the four waves' sums added through LDS in a fixed order (deterministic),
 // divided by L and written as bf16.
-__global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
-  __shared__ float red[3][64][33];   // waves 1..3's sums (33: conflict-free row stride)
-  __shared__ float mlred[16][16][2];  // pass 1: (m, l) per (thread group, row)
-  __shared__ float rowm[16], rowl[16];
-  if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
-  // descriptor (last first: long splits end in late workgroups), wave (head) of its group
-  const int bi = blockIdx.x / p.HG, hw = blockIdx.x - bi * p.HG, b = gridDim.x / p.HG - 1 - bi;
-  // the flag and the fields in one round trip (the empty asm keeps the compiler from moving the
-  // field loads behind the flag test)
-  int valid = p.desc[b].valid[hw];
-  SplitDesc d = p.desc[b];
-  asm volatile("" : "+v"(valid), "+v"(d.nch), "+v"(d.q_start), "+v"(d.q_len), "+v"(d.h), "+v"(d.rb), "+v"(d.b0));
-  if (!__builtin_amdgcn_readfirstlane(valid)) return;
-  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
-  const int ncontrib = (int)(b - d.b0 + 1);
-  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
-  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
-
-  // pass 1: per-row (M, L) over all contributors
+// Pass 1 of a merge: each row's global maximum M and denominator L over the descriptor's
+// contributors (all 256 threads: thread = (row t%16, contributors t/16, t/16 + 16, ...)).
+__device__ __forceinline__ void combine_row_stats(const Params& p, const SplitDesc& d, int hw, int ncontrib, int t,
+                                                  float (*mlred)[16][2], float* rowm, float* rowl) {
   {
     const int r = t & 15, g = t >> 4;
     float m = -INFINITY, l = 0.f;
@@ -1776,6 +1772,129 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
     }
     __syncthreads();
   }
+}
+
+// Pass 2 of a heavy merge for dims 32*slice .. +31: lane = (rows 8i + lane/8 for i < NP, dims
+// 32*slice + 4*(lane%8) .. +3); wave wv takes contributors wv, wv+4, ..., U at a time, as
+// combine_rows does over all dims.
+template <int NP, int U>
+__device__ __forceinline__ void combine_slice(const Params& p, const SplitDesc& d, int hw, int ncontrib, int wv,
+                                              int lane, int slice, const float* mrow_lds, f32x4 (&o)[2]) {
+  const int r8 = lane >> 3, c4 = 32 * slice + 4 * (lane & 7);
+  float mref[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const float m = mrow_lds[8 * i + r8];
+    mref[i] = m == -INFINITY ? 0.f : m;
+  }
+#pragma unroll 1
+  for (int k = wv; k < ncontrib; k += 4 * U) {
+    f32x4 x[U][NP];
+    float mc[U][NP];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = k + 4 * u < ncontrib ? k + 4 * u : k;  // past the end: a valid slot, weight 0
+      const size_t sc = combine_slot(p, d, hw, kk);
+      const float* ml = p.part_ml + sc * ROW_BLOCK * 2;
+      const float* a = p.part_acc + sc * ROW_BLOCK * kD + c4;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        mc[u][i] = ml[2 * (8 * i + r8)];
+        x[u][i] = *(const f32x4*)(a + (8 * i + r8) * kD);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the U contributors issued before any use
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        const float w = k + 4 * u < ncontrib ? __builtin_amdgcn_exp2f(mc[u][i] - mref[i]) : 0.f;
+        o[i] += w * x[u][i];
+      }
+  }
+}
+
+// Helper workgroup hb (after the grid*HG merge workgroups): heavy slot hb / (8 * kHeavySlices),
+// head and dim slice from the rest.  Its flag (written by the attention kernel) names the
+// descriptor; the workgroup merges those 32 dims of its rows and clears the flag.
+__device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*red)[64][33], float (*mlred)[16][2],
+                                              float* rowm, float* rowl) {
+  const int slot = hb / (p.HG * kHeavySlices), rem = hb - slot * (p.HG * kHeavySlices);
+  const int hw = rem / kHeavySlices, slice = rem - hw * kHeavySlices;
+  int32_t* flag = p.heavy + ((size_t)slot * 8 + hw) * kHeavySlices + slice;
+  const int f = __builtin_amdgcn_readfirstlane(*flag);
+  if (f <= 0 || f > p.grid) return;
+  const int b = f - 1;
+  const SplitDesc d = p.desc[b];
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const int ncontrib = (int)(b - d.b0 + 1);
+  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
+  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
+  combine_row_stats(p, d, hw, ncontrib, t, mlred, rowm, rowl);
+  f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  if (nrows <= 8)
+    combine_slice<1, 12>(p, d, hw, ncontrib, wv, lane, slice, rowm, o);
+  else
+    combine_slice<2, 6>(p, d, hw, ncontrib, wv, lane, slice, rowm, o);
+  const int np = nrows <= 8 ? 1 : 2;
+  if (wv > 0)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (i < np)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[wv - 1][lane][4 * i + e] = o[i][e];
+  __syncthreads();
+  if (wv == 0) {
+    const int r8 = lane >> 3, c4 = 32 * slice + 4 * (lane & 7);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = 8 * i + r8;
+      if (i < np && row < nrows) {
+        f32x4 v = o[i];
+        for (int w = 0; w < 3; ++w)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] += red[w][lane][4 * i + e];
+        const float inv = 1.f / rowl[row];
+        const int grow = d.rb * ROW_BLOCK + row;
+        const int tok = grow / p.G;
+        const int head = (d.h * p.HG + hw) * p.G + (grow - tok * p.G);
+        u32x2 w2;
+        w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
+        w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
+        *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + c4) = w2;
+      }
+    }
+    if (lane == 0) *flag = 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
+  __shared__ float red[3][64][33];   // waves 1..3's sums (33: conflict-free row stride)
+  __shared__ float mlred[16][16][2];  // pass 1: (m, l) per (thread group, row)
+  __shared__ float rowm[16], rowl[16];
+  if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
+  if ((int)blockIdx.x >= p.grid * p.HG) {
+    combine_heavy(p, blockIdx.x - p.grid * p.HG, red, mlred, rowm, rowl);
+    return;
+  }
+  // descriptor (last first: long splits end in late workgroups), wave (head) of its group
+  const int bi = blockIdx.x / p.HG, hw = blockIdx.x - bi * p.HG, b = p.grid - 1 - bi;
+  // the flag and the fields in one round trip (the empty asm keeps the compiler from moving the
+  // field loads behind the flag test)
+  int valid = p.desc[b].valid[hw];
+  SplitDesc d = p.desc[b];
+  asm volatile("" : "+v"(valid), "+v"(d.nch), "+v"(d.q_start), "+v"(d.q_len), "+v"(d.h), "+v"(d.rb), "+v"(d.b0));
+  if (!__builtin_amdgcn_readfirstlane(valid)) return;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const int ncontrib = (int)(b - d.b0 + 1);
+  if (ncontrib >= kHeavyContrib) {  // merged by the helper workgroups of its slot
+    if (t == 0) p.desc[b].valid[hw] = 0;
+    return;
+  }
+  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
+  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
+
+  combine_row_stats(p, d, hw, ncontrib, t, mlred, rowm, rowl);
 
   // pass 2: weighted sums of the acc rows
   f32x4 o[8];
@@ -1934,11 +2053,12 @@ int device_info(DeviceInfo& out) {
   return RPA_OK;
 }
 
-// Workspace: [error word | pad to 256] [split descriptors, one per workgroup] [partial m,l]
-// [partial acc].  Header and descriptors are zeroed once (rpa_workspace_init); every call
-// leaves each descriptor invalid again when its combine has run.
+// Workspace: [error word | pad to 256] [split descriptors, one per workgroup] [heavy-merge helper
+// flags] [partial m,l] [partial acc].  Header, descriptors and flags are zeroed once
+// (rpa_workspace_init); every call leaves each descriptor invalid and each flag clear again when
+// its combine has run.
 struct WsLayout {
-  size_t desc, ml, acc, total;
+  size_t desc, heavy, ml, acc, total;
 };
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
@@ -1947,7 +2067,8 @@ WsLayout ws_layout(const DeviceInfo& d) {
   const size_t gmax = (size_t)d.cus * kMaxWavesPerCU;
   WsLayout w;
   w.desc = kHeaderBytes;
-  w.ml = w.desc + round256(gmax * sizeof(SplitDesc));
+  w.heavy = w.desc + round256(gmax * sizeof(SplitDesc));
+  w.ml = w.heavy + round256((size_t)heavy_slots((int)gmax) * 8 * kHeavySlices * sizeof(int32_t));
   w.acc = w.ml + round256(2 * gmax * ROW_BLOCK * 2 * sizeof(float));
   w.total = w.acc + 2 * gmax * ROW_BLOCK * kD * sizeof(float);
   return w;
@@ -2357,6 +2478,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   p.err = (int32_t*)workspace;
   const WsLayout w = ws_layout(d);
   p.desc = (SplitDesc*)((uint8_t*)workspace + w.desc);
+  p.heavy = (int32_t*)((uint8_t*)workspace + w.heavy);
   p.part_ml = (float*)((uint8_t*)workspace + w.ml);
   p.part_acc = (float*)((uint8_t*)workspace + w.acc);
   p.sm_scale = opt->sm_scale;
@@ -2415,7 +2537,9 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("attention launch failed: ") + hipGetErrorString(e));
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(end) failed");
-  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid * p.HG), dim3(256), 0, st, p);
+  // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot
+  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices), dim3(256), 0,
+                     st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
   return RPA_OK;

@@ -201,6 +201,15 @@ ROW_BLOCK = 16
 # LDS per wave of the attention kernel: the transposed V chunk (128 dim rows x 80 B) and the K tile
 # of the full-line path (32 key rows x 272 B) (csrc/rpa_kernels.hip, kVTRow / kKtRow)
 WAVE_LDS_BYTES = 128 * 80 + KV_CHUNK * (128 * 2 + 16)
+# split row blocks with this many contributors are merged by HEAVY_SLICES dim-slice workgroups per
+# kv head, one helper slot per (HEAVY_CONTRIB - 1) workgroups (csrc/rpa_kernels.hip, kHeavyContrib)
+HEAVY_CONTRIB = 32
+HEAVY_SLICES = 4
+
+
+def combine_grid(grid: int, hg: int) -> int:
+    """Workgroups of one combine launch: (descriptor, kv head) merges, then the heavy-merge helpers."""
+    return grid * hg + ((grid - 1) // (HEAVY_CONTRIB - 1) + 1) * hg * HEAVY_SLICES
 PF_MIN = 16                                 # query tokens that make a sequence a prefill one
 PF_COST = 0.45                              # prefill chunk-step cost in stream-K units
 
@@ -340,8 +349,9 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
         f"{unit_bytes} KV bytes per unit per workgroup",
         f"  prefill tiles = {split['prefill_tiles']} tiles of {split['prefill_tile_tokens']} tokens x 1 kv head "
         f"({split['prefill_chunk_steps']} chunk steps) on {split['prefill_workgroups']} workgroups",
-        f"launch 1 = rpa_combine_kernel: grid {split['grid'] * hg} x block 256 (one workgroup per "
-        f"(split descriptor, kv head))",
+        f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg)} x block 256 (one workgroup per "
+        f"(split descriptor, kv head), then {HEAVY_SLICES} per (heavy slot, kv head) for splits of "
+        f">= {HEAVY_CONTRIB} workgroups)",
         f"algorithmic = KV {kv_bytes} B + Q/O {qo_bytes} B; prefill {flops} FLOP",
         f"roofline floor = HBM {floor_hbm:.2f} us; MFMA {floor_mfma:.2f} us; "
         f"bound = {'mfma' if floor_mfma > floor_hbm else 'hbm'}",
@@ -379,7 +389,7 @@ def _inkling_v1_workload() -> tuple[str, WorkloadContract, dict]:
         "[P, S, 2H, 128] layout, writes the bias table by key position, cu_q = 0..B, num_seqs, padded queries",
         f"launch 1 = rpa_attn_kernel<KV_BF16_BIAS>: grid {split['grid']} x block {64 * split['heads_per_workgroup']}; "
         f"at most {split['stream_k_units']} stream-K units (sequences up to {L} keys)",
-        f"launch 2 = rpa_combine_kernel: grid {split['grid'] * split['heads_per_workgroup']} x block 256",
+        f"launch 2 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'])} x block 256",
         "launch 3 = rpa_fused_unpad_kernel: output rows 128 -> D",
     ]
     kernels = ("rpa_inkling_v1_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_unpad_kernel")
@@ -425,7 +435,7 @@ def _inkling_fused_workload() -> tuple[str, WorkloadContract, dict]:
         "launch 0 = rpa_fused_prep_kernel: block s writes sequence s's new K/V rows (16-byte stores); bias blocks "
         "(4 q heads x 256 keys); grid-stride blocks expand the flat page list to a [N, pages per sequence] table",
         f"launch 1 = rpa_attn_kernel<KV_BF16_BIAS>: grid {split['grid']} x block {64 * split['heads_per_workgroup']}",
-        f"launch 2 = rpa_combine_kernel: grid {split['grid'] * split['heads_per_workgroup']} x block 256",
+        f"launch 2 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'])} x block 256",
         "launch 3 = rpa_fused_unpad_kernel: output rows 128 -> D",
     ]
     kernels = ("rpa_fused_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_unpad_kernel")
