@@ -177,6 +177,19 @@ def test_fp8_kv_per_page_scales(cuda):
     assert err["max_abs"] <= TOL_FP8_VS_SOURCE
 
 
+@pytest.mark.parametrize("page", [16, 64])
+def test_fp8_kv_scalar_scales(cuda, page):
+    # fp8 codes with the reference's scalar k_scale / v_scale instead of per-page scales
+    _say(f"fp8 KV with scalar k_scale / v_scale, page {page}")
+    case = make_custom(kv_lens=[3, 70, 333, 1200], q_lens=[1, 1, 2, 1], num_q_heads=32, num_kv_heads=8,
+                       page_size=page, seed=35 + page, kv_dtype="fp8")
+    # the codes span +-448 (quantised with per-page scales max|x| / 448); scalars of that size
+    # bring K and V back to unit scale, where the 2e-2 bound is meaningful
+    case.kv_scales = None
+    kw = dict(k_scale=1.0 / 128, v_scale=1.0 / 112)
+    _check(case, gpu_kw=kw, oracle_kw=kw)
+
+
 @pytest.mark.parametrize("page", [16, 24])
 def test_fp8_kv_unaligned_pages(cuda, page):
     # page sizes that are not a multiple of 32: each key of a 32-key unit carries its own page id

@@ -21,11 +21,12 @@
 //                         directly; a row block split across workgroups leaves one partial
 //                         (m, l, acc) per workgroup, and the workgroup owning its last unit leaves
 //                         a descriptor of it.
-//   rpa_combine_kernel  one 4-wave workgroup per (descriptor, head): the rows' global max and
-//                       denominator from the partials' (m, l), then the weighted sum of their
-//                       acc rows with coalesced loads (waves take every 4th contributor, sums
-//                       added through LDS); writes the rows, clears the descriptor; resets the
-//                       prefill tile queue for the next call.
+//   rpa_combine_kernel  one 4-wave workgroup per (descriptor, head): the partials' (m, l, acc)
+//                       folded in one pass with coalesced loads (waves take every 4th
+//                       contributor, running states merged through LDS); writes the rows,
+//                       clears the descriptor; blocks split over 32+ workgroups go to helper
+//                       workgroups, four per head, each over 32 dims; resets the prefill tile
+//                       queue for the next call.
 //
 // MFMA operand layouts (16x16x32 bf16, wave64): A[i][k] and B[k][j] place row i / column j
 // at lane%16 and the 32 k-slots at (lane/16, element 0..7); D[i][j] sits at lane
@@ -105,6 +106,7 @@ struct Params {
   float* part_ml;   // [2*grid][16][2]  (m in log2 units, l)
   struct SplitDesc* desc;  // [grid] split row block ending in workgroup b (valid = 0 otherwise)
   int32_t* heavy;          // [heavy_slots(grid)][8 heads][kHeavySlices] b + 1 of a heavy descriptor (0 = none)
+  struct SplitDesc* heavy_desc;  // [heavy_slots(grid)] copy of the slot's heavy descriptor (read with the flag)
   int32_t* err;
   int T, Hq, Hkv, G, P, S, log2S, Nmax, PPS;
   int HG, NG;  // kv heads per workgroup (one wave each) and kv-head groups (Hkv / HG)
@@ -885,6 +887,12 @@ __device__ __forceinline__ void write_split_desc(const Params& p, const Cursor& 
   d->b0 = b0;
   d->valid[wv] = 1;
   if (b - b0 + 1 >= kHeavyContrib) {
+    SplitDesc* hd = p.heavy_desc + heavy_slot(b);
+    hd->q_start = cur.q_start;
+    hd->q_len = cur.q_len;
+    hd->h = cur.h;
+    hd->rb = cur.rb;
+    hd->b0 = b0;
     int32_t* f = p.heavy + ((size_t)heavy_slot(b) * 8 + wv) * kHeavySlices;
 #pragma unroll
     for (int sl = 0; sl < kHeavySlices; ++sl) f[sl] = b + 1;
@@ -1686,195 +1694,153 @@ __device__ __forceinline__ size_t combine_slot(const Params& p, const SplitDesc&
   return (size_t)partial_slot(d.b0 + k, k == 0) * p.HG + hw;
 }
 
-// Pass 2 of the combine for row blocks of up to 2*NP rows: lane = (rows 2i + half for i < NP,
-// dims 4*(lane%32) .. +3), so one load instruction reads two whole 512-byte rows (coalesced).
-// Wave wv takes contributors wv, wv+4, ..., U at a time with all their loads issued first; each
-// is weighted by exp2(m - M[row]) with the row's global maximum M from pass 1 (no rescaling).
-template <int NP, int U>
-__device__ __forceinline__ void combine_rows(const Params& p, const SplitDesc& d, int hw, int ncontrib, int wv,
-                                             int lane, const float* mrow_lds, f32x4 (&o)[8]) {
-  const int half = lane >> 5, c4 = 4 * (lane & 31);
-  float mref[NP];
+// One-pass merge of a split row block's partials.  A lane holds NP row slots: row RS*i + lane/(64/RS)
+// of the block, dims dim0 + 4*(lane % (64/RS)) .. +3 (RS = 2: two whole 512-byte rows per load
+// instruction; RS = 8: a 32-dim slice of eight rows).  Wave wv takes contributors wv, wv+4, ...,
+// U at a time with all their (m, l, acc) loads issued before any is used (sched_barrier), and
+// folds each into a running (m, l, o) with the online log-sum-exp update -- in contributor order,
+// so the result is deterministic.
+template <int NP>
+struct MergeAcc {
+  f32x4 o[NP];
+  float m[NP], l[NP];
+};
+
+template <int NP, int U, int RS>
+__device__ __forceinline__ void merge_rows(const Params& p, const SplitDesc& d, int hw, int ncontrib, int wv, int lane,
+                                           int row0, int dim0, MergeAcc<NP>& a) {
+  constexpr int kLanesPerRow = 64 / RS;
+  const int r0 = row0 + lane / kLanesPerRow, c4 = dim0 + 4 * (lane % kLanesPerRow);
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
-    const float m = mrow_lds[2 * i + half];
-    mref[i] = m == -INFINITY ? 0.f : m;
+    a.o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    a.m[i] = -INFINITY;
+    a.l[i] = 0.f;
   }
 #pragma unroll 1
   for (int k = wv; k < ncontrib; k += 4 * U) {
     f32x4 x[U][NP];
-    float mc[U][NP];
+    float mc[U][NP], lc[U][NP];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kk = k + 4 * u < ncontrib ? k + 4 * u : k;  // past the end: a valid slot, weight 0
+      const int kk = k + 4 * u < ncontrib ? k + 4 * u : k;  // past the end: a valid slot, skipped below
       const size_t sc = combine_slot(p, d, hw, kk);
       const float* ml = p.part_ml + sc * ROW_BLOCK * 2;
-      const float* a = p.part_acc + sc * ROW_BLOCK * kD + c4;
+      const float* acc = p.part_acc + sc * ROW_BLOCK * kD + c4;
 #pragma unroll
       for (int i = 0; i < NP; ++i) {
-        mc[u][i] = ml[2 * (2 * i + half)];
-        x[u][i] = *(const f32x4*)(a + (2 * i + half) * kD);
+        const int row = RS * i + r0;
+        mc[u][i] = ml[2 * row];
+        lc[u][i] = ml[2 * row + 1];
+        x[u][i] = *(const f32x4*)(acc + row * kD);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the U contributors issued before any use
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u)
+      if (k + 4 * u < ncontrib)
 #pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        const float w = k + 4 * u < ncontrib ? __builtin_amdgcn_exp2f(mc[u][i] - mref[i]) : 0.f;
-        o[i] += w * x[u][i];
-      }
+        for (int i = 0; i < NP; ++i) {
+          const float mn = fmaxf(a.m[i], mc[u][i]), mu = mn == -INFINITY ? 0.f : mn;
+          const float sa = __builtin_amdgcn_exp2f(a.m[i] - mu), sb = __builtin_amdgcn_exp2f(mc[u][i] - mu);
+          a.o[i] = a.o[i] * sa + x[u][i] * sb;
+          a.l[i] = a.l[i] * sa + lc[u][i] * sb;
+          a.m[i] = mn;
+        }
   }
 }
 
-// Workgroup b merges the row block described by desc[b] for head hw: contributors b0..b, b0's
-// share in slot 2*b0+1 and every later one's in slot 2*bb.  Pass 1 (all 256 threads; thread =
-// (row t%16, contributors t/16, t/16 + 16, ...)): each row's global maximum M and denominator
-// L = sum l * exp2(m - M), merged through LDS.  Pass 2 (combine_rows): the weighted sum of the
-// contributors' acc rows, the four waves' sums added through LDS in a fixed order (deterministic),
-// divided by L and written as bf16.
-// Pass 1 of a merge: each row's global maximum M and denominator L over the descriptor's
-// contributors (all 256 threads: thread = (row t%16, contributors t/16, t/16 + 16, ...)).
-__device__ __forceinline__ void combine_row_stats(const Params& p, const SplitDesc& d, int hw, int ncontrib, int t,
-                                                  float (*mlred)[16][2], float* rowm, float* rowl) {
-  {
-    const int r = t & 15, g = t >> 4;
-    float m = -INFINITY, l = 0.f;
-#pragma unroll 1
-    for (int k = g; k < ncontrib; k += 64) {
-      float mc[4], lc[4];
+// The four waves' running states merged through LDS (waves 1..3 into wave 0, in that order),
+// divided by the denominator and written as bf16: rows below nrows of descriptor d, head hw.
+template <int NP, int RS>
+__device__ __forceinline__ void merge_waves_store(const Params& p, const SplitDesc& d, int hw, int nrows, int wv,
+                                                  int lane, int row0, int dim0, const MergeAcc<NP>& a,
+                                                  float (*red)[64][33], float (*redml)[64][16]) {
+  constexpr int kLanesPerRow = 64 / RS;
+  if (wv > 0) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int kk = k + 16 * u < ncontrib ? k + 16 * u : k;
-        const float* ml = p.part_ml + (combine_slot(p, d, hw, kk) * ROW_BLOCK + r) * 2;
-        mc[u] = ml[0];
-        lc[u] = ml[1];
-      }
+    for (int i = 0; i < NP; ++i) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float mcu = k + 16 * u < ncontrib ? mc[u] : -INFINITY;
-        const float mn = fmaxf(m, mcu), mu = mn == -INFINITY ? 0.f : mn;
-        l = l * __builtin_amdgcn_exp2f(m - mu) + lc[u] * __builtin_amdgcn_exp2f(mcu - mu);
-        m = mn;
-      }
+      for (int e = 0; e < 4; ++e) red[wv - 1][lane][4 * i + e] = a.o[i][e];
+      redml[wv - 1][lane][2 * i] = a.m[i];
+      redml[wv - 1][lane][2 * i + 1] = a.l[i];
     }
-    mlred[g][r][0] = m;
-    mlred[g][r][1] = l;
-    __syncthreads();
-    if (t < 16) {
-      float M = -INFINITY;
-      for (int gg = 0; gg < 16; ++gg) M = fmaxf(M, mlred[gg][t][0]);
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const int r0 = row0 + lane / kLanesPerRow, c4 = dim0 + 4 * (lane % kLanesPerRow);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int row = RS * i + r0;
+      if (row >= nrows) continue;
+      float M = a.m[i];
+      for (int w = 0; w < 3; ++w) M = fmaxf(M, redml[w][lane][2 * i]);
       const float mu = M == -INFINITY ? 0.f : M;
-      float L = 0.f;
-      for (int gg = 0; gg < 16; ++gg) L += mlred[gg][t][1] * __builtin_amdgcn_exp2f(mlred[gg][t][0] - mu);
-      rowm[t] = M;
-      rowl[t] = L;
+      float sw = __builtin_amdgcn_exp2f(a.m[i] - mu);
+      f32x4 v = a.o[i] * sw;
+      float L = a.l[i] * sw;
+      for (int w = 0; w < 3; ++w) {
+        sw = __builtin_amdgcn_exp2f(redml[w][lane][2 * i] - mu);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += red[w][lane][4 * i + e] * sw;
+        L += redml[w][lane][2 * i + 1] * sw;
+      }
+      const float inv = 1.f / L;
+      const int grow = d.rb * ROW_BLOCK + row;  // row of the sequence's (token, head) rows
+      const int tok = grow / p.G;
+      const int head = (d.h * p.HG + hw) * p.G + (grow - tok * p.G);
+      // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
+      u32x2 w2;
+      w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
+      w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
+      *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + c4) = w2;
     }
-    __syncthreads();
   }
+  __syncthreads();  // red / redml free for a next merge
 }
 
-// Pass 2 of a heavy merge for dims 32*slice .. +31: lane = (rows 8i + lane/8 for i < NP, dims
-// 32*slice + 4*(lane%8) .. +3); wave wv takes contributors wv, wv+4, ..., U at a time, as
-// combine_rows does over all dims.
-template <int NP, int U>
-__device__ __forceinline__ void combine_slice(const Params& p, const SplitDesc& d, int hw, int ncontrib, int wv,
-                                              int lane, int slice, const float* mrow_lds, f32x4 (&o)[2]) {
-  const int r8 = lane >> 3, c4 = 32 * slice + 4 * (lane & 7);
-  float mref[NP];
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const float m = mrow_lds[8 * i + r8];
-    mref[i] = m == -INFINITY ? 0.f : m;
-  }
-#pragma unroll 1
-  for (int k = wv; k < ncontrib; k += 4 * U) {
-    f32x4 x[U][NP];
-    float mc[U][NP];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kk = k + 4 * u < ncontrib ? k + 4 * u : k;  // past the end: a valid slot, weight 0
-      const size_t sc = combine_slot(p, d, hw, kk);
-      const float* ml = p.part_ml + sc * ROW_BLOCK * 2;
-      const float* a = p.part_acc + sc * ROW_BLOCK * kD + c4;
-#pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        mc[u][i] = ml[2 * (8 * i + r8)];
-        x[u][i] = *(const f32x4*)(a + (8 * i + r8) * kD);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);  // every load of the U contributors issued before any use
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        const float w = k + 4 * u < ncontrib ? __builtin_amdgcn_exp2f(mc[u][i] - mref[i]) : 0.f;
-        o[i] += w * x[u][i];
-      }
-  }
+__device__ __forceinline__ int rows_of(const Params& p, const SplitDesc& d) {
+  const int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
+  return nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
 }
 
-// Helper workgroup hb (after the grid*HG merge workgroups): heavy slot hb / (8 * kHeavySlices),
-// head and dim slice from the rest.  Its flag (written by the attention kernel) names the
-// descriptor; the workgroup merges those 32 dims of its rows and clears the flag.
-__device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*red)[64][33], float (*mlred)[16][2],
-                                              float* rowm, float* rowl) {
+// Helper workgroup hb (after the grid*HG merge workgroups): heavy slot hb / (HG * kHeavySlices),
+// head and dim slice from the rest.  Its flag (set by the attention kernel) says whether the slot
+// holds a heavy descriptor this call; the flag and the slot's copy of the descriptor come in one
+// round trip.  The workgroup merges those 32 dims of the block's rows and clears its flag.
+__device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*red)[64][33], float (*redml)[64][16]) {
   const int slot = hb / (p.HG * kHeavySlices), rem = hb - slot * (p.HG * kHeavySlices);
   const int hw = rem / kHeavySlices, slice = rem - hw * kHeavySlices;
   int32_t* flag = p.heavy + ((size_t)slot * 8 + hw) * kHeavySlices + slice;
-  const int f = __builtin_amdgcn_readfirstlane(*flag);
+  int f = *flag;
+  SplitDesc d = p.heavy_desc[slot];
+  asm volatile("" : "+v"(f), "+v"(d.q_start), "+v"(d.q_len), "+v"(d.h), "+v"(d.rb), "+v"(d.b0));
+  f = __builtin_amdgcn_readfirstlane(f);
   if (f <= 0 || f > p.grid) return;
   const int b = f - 1;
-  const SplitDesc d = p.desc[b];
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
-  const int ncontrib = (int)(b - d.b0 + 1);
-  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
-  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
-  combine_row_stats(p, d, hw, ncontrib, t, mlred, rowm, rowl);
-  f32x4 o[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  if (nrows <= 8)
-    combine_slice<1, 12>(p, d, hw, ncontrib, wv, lane, slice, rowm, o);
-  else
-    combine_slice<2, 6>(p, d, hw, ncontrib, wv, lane, slice, rowm, o);
-  const int np = nrows <= 8 ? 1 : 2;
-  if (wv > 0)
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      if (i < np)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[wv - 1][lane][4 * i + e] = o[i][e];
-  __syncthreads();
-  if (wv == 0) {
-    const int r8 = lane >> 3, c4 = 32 * slice + 4 * (lane & 7);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = 8 * i + r8;
-      if (i < np && row < nrows) {
-        f32x4 v = o[i];
-        for (int w = 0; w < 3; ++w)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += red[w][lane][4 * i + e];
-        const float inv = 1.f / rowl[row];
-        const int grow = d.rb * ROW_BLOCK + row;
-        const int tok = grow / p.G;
-        const int head = (d.h * p.HG + hw) * p.G + (grow - tok * p.G);
-        u32x2 w2;
-        w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
-        w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
-        *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + c4) = w2;
-      }
-    }
-    if (lane == 0) *flag = 0;
+  const int ncontrib = (int)(b - d.b0 + 1), nrows = rows_of(p, d);
+  if (nrows <= 8) {
+    MergeAcc<1> a;
+    merge_rows<1, 8, 8>(p, d, hw, ncontrib, wv, lane, 0, 32 * slice, a);
+    merge_waves_store<1, 8>(p, d, hw, nrows, wv, lane, 0, 32 * slice, a, red, redml);
+  } else {
+    MergeAcc<2> a;
+    merge_rows<2, 4, 8>(p, d, hw, ncontrib, wv, lane, 0, 32 * slice, a);
+    merge_waves_store<2, 8>(p, d, hw, nrows, wv, lane, 0, 32 * slice, a, red, redml);
   }
+  if (t == 0) *flag = 0;
 }
 
-__global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
-  __shared__ float red[3][64][33];   // waves 1..3's sums (33: conflict-free row stride)
-  __shared__ float mlred[16][16][2];  // pass 1: (m, l) per (thread group, row)
-  __shared__ float rowm[16], rowl[16];
+// Workgroup b merges the row block described by desc[b] for head hw: contributors b0..b, b0's
+// share in slot 2*b0+1 and every later one's in slot 2*bb (merge_rows, merge_waves_store), unless
+// the block is heavy (its slot's helper workgroups merge it).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
+  __shared__ float red[3][64][33];    // waves 1..3's o (33: conflict-free row stride)
+  __shared__ float redml[3][64][16];  // waves 1..3's (m, l) per row slot
   if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
   if ((int)blockIdx.x >= p.grid * p.HG) {
-    combine_heavy(p, blockIdx.x - p.grid * p.HG, red, mlred, rowm, rowl);
+    combine_heavy(p, blockIdx.x - p.grid * p.HG, red, redml);
     return;
   }
   // descriptor (last first: long splits end in late workgroups), wave (head) of its group
@@ -1887,56 +1853,23 @@ __global__ __launch_bounds__(256) void rpa_combine_kernel(Params p) {
   if (!__builtin_amdgcn_readfirstlane(valid)) return;
   const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
   const int ncontrib = (int)(b - d.b0 + 1);
-  if (ncontrib >= kHeavyContrib) {  // merged by the helper workgroups of its slot
-    if (t == 0) p.desc[b].valid[hw] = 0;
-    return;
-  }
-  int nrows = d.q_len * p.G - d.rb * ROW_BLOCK;
-  nrows = nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
-
-  combine_row_stats(p, d, hw, ncontrib, t, mlred, rowm, rowl);
-
-  // pass 2: weighted sums of the acc rows
-  f32x4 o[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (nrows <= 4)
-    combine_rows<2, 4>(p, d, hw, ncontrib, wv, lane, rowm, o);
-  else if (nrows <= 8)
-    combine_rows<4, 3>(p, d, hw, ncontrib, wv, lane, rowm, o);
-  else
-    combine_rows<8, 1>(p, d, hw, ncontrib, wv, lane, rowm, o);
-  const int np = nrows <= 4 ? 2 : nrows <= 8 ? 4 : 8;
-  if (wv > 0)
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (i < np)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[wv - 1][lane][4 * i + e] = o[i][e];
-  __syncthreads();
-  if (wv == 0) {
-    const int half = lane >> 5, c4 = 4 * (lane & 31);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 2 * i + half;
-      if (i < np && row < nrows) {
-        f32x4 v = o[i];
-        for (int w = 0; w < 3; ++w)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] += red[w][lane][4 * i + e];
-        const float inv = 1.f / rowl[row];
-        const int grow = d.rb * ROW_BLOCK + row;  // row of the sequence's (token, head) rows
-        const int tok = grow / p.G;
-        const int head = (d.h * p.HG + hw) * p.G + (grow - tok * p.G);
-        // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
-        u32x2 w2;
-        w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
-        w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
-        *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + c4) = w2;
+  if (ncontrib < kHeavyContrib) {
+    const int nrows = rows_of(p, d);
+    if (nrows <= 4) {
+      MergeAcc<2> a;
+      merge_rows<2, 4, 2>(p, d, hw, ncontrib, wv, lane, 0, 0, a);
+      merge_waves_store<2, 2>(p, d, hw, nrows, wv, lane, 0, 0, a, red, redml);
+    } else {
+      // rows 0..7, then (16-row blocks) rows 8..15
+#pragma unroll 1
+      for (int row0 = 0; row0 < nrows; row0 += 8) {
+        MergeAcc<4> a;
+        merge_rows<4, 1, 2>(p, d, hw, ncontrib, wv, lane, row0, 0, a);
+        merge_waves_store<4, 2>(p, d, hw, nrows, wv, lane, row0, 0, a, red, redml);
       }
     }
-    if (lane == 0) p.desc[b].valid[hw] = 0;
   }
+  if (t == 0) p.desc[b].valid[hw] = 0;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2058,7 +1991,7 @@ int device_info(DeviceInfo& out) {
 // (rpa_workspace_init); every call leaves each descriptor invalid and each flag clear again when
 // its combine has run.
 struct WsLayout {
-  size_t desc, heavy, ml, acc, total;
+  size_t desc, heavy, heavy_desc, ml, acc, total;
 };
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
@@ -2068,7 +2001,8 @@ WsLayout ws_layout(const DeviceInfo& d) {
   WsLayout w;
   w.desc = kHeaderBytes;
   w.heavy = w.desc + round256(gmax * sizeof(SplitDesc));
-  w.ml = w.heavy + round256((size_t)heavy_slots((int)gmax) * 8 * kHeavySlices * sizeof(int32_t));
+  w.heavy_desc = w.heavy + round256((size_t)heavy_slots((int)gmax) * 8 * kHeavySlices * sizeof(int32_t));
+  w.ml = w.heavy_desc + round256((size_t)heavy_slots((int)gmax) * sizeof(SplitDesc));
   w.acc = w.ml + round256(2 * gmax * ROW_BLOCK * 2 * sizeof(float));
   w.total = w.acc + 2 * gmax * ROW_BLOCK * kD * sizeof(float);
   return w;
@@ -2479,6 +2413,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   const WsLayout w = ws_layout(d);
   p.desc = (SplitDesc*)((uint8_t*)workspace + w.desc);
   p.heavy = (int32_t*)((uint8_t*)workspace + w.heavy);
+  p.heavy_desc = (SplitDesc*)((uint8_t*)workspace + w.heavy_desc);
   p.part_ml = (float*)((uint8_t*)workspace + w.ml);
   p.part_acc = (float*)((uint8_t*)workspace + w.acc);
   p.sm_scale = opt->sm_scale;
