@@ -1537,15 +1537,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // prefill tiles need the whole metadata in the four windows
     pf_min = (MODE == KV_BF16 && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
 #pragma unroll
-    for (int w = 0; w < kWin; ++w)
-      wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, pf_min, err);
+    for (int w = 0; w < kWin; ++w) {
+      wsi[w] = SeqInfo{0, 0, 0, 0};
+      if (nseq > 64 * w)  // windows past num_seqs hold no sequence (a uniform branch)
+        wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, pf_min, err);
+    }
   }
   win.pf_min = pf_min;
   long long W = 0, tile[kWin];
   if (nseq <= 64 * kWin) {
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
-      tile[w] = wave_sum_units((long long)wsi[w].units * p.NG);
+      tile[w] = nseq > 64 * w ? wave_sum_units((long long)wsi[w].units * p.NG) : 0;
       W += tile[w];
     }
   } else {
@@ -1555,7 +1558,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Work split: the first gpre workgroups take prefill tiles, the rest run stream-K over the
   // other sequences.  Every workgroup computes the same split from the same metadata.
   int gpre = 0, pf_total = 0;
-  if (MODE == KV_BF16 && pf_min > 0) {
+  bool any_pf = false;
+#pragma unroll
+  for (int w = 0; w < kWin; ++w) any_pf = any_pf || wsi[w].q_len >= pf_min;
+  if (MODE == KV_BF16 && pf_min > 0 && __ballot(any_pf) != 0) {
     // per lane over the four windows, then one wave sum each (skipped when no sequence is a
     // prefill sequence)
     float st = 0.f;
