@@ -775,8 +775,8 @@ __device__ __forceinline__ const f32x4* bias_of(const HalfRegs<MODE>& r) {
   return nullptr;
 }
 
-// One unit.  S = K Q^T; then, if the next unit starts a new row block, its queries are loaded
-// into q (their registers are free once QK^T has issued); V^T goes to LDS, after which the next unit's V is loaded into the
+// One unit.  S = K Q^T; V^T goes to LDS; then, if the next unit starts a new row block, its
+// queries are loaded into q (their registers are free once QK^T has issued), after which the next unit's V is loaded into the
 // registers just released; then softmax and O^T += V^T P^T.
 template <int MODE, bool UPG>
 __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const HalfRegs<MODE>& kr,
@@ -795,7 +795,6 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     s0 *= ks;
     s1 *= ks;
   }
-  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);  // a new row block (else q already holds its rows)
   float vs = 1.f;
   if constexpr (MODE == KV_FP8 && UPG) vs = p.v_scale * kr.sc[1];  // the unit's V scale (one page)
 
@@ -816,6 +815,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
       }
     }
   }
+  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);  // a new row block's queries (as in compute_unit_line)
   load_half<MODE, UPG>(p, nx_addr, 1, v_next);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j, vs);
@@ -1032,7 +1032,6 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
     s0 = mfma(a0, q[s], s0);
     s1 = mfma(a1, q[s], s1);
   }
-  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);  // a new row block (else q already holds its rows)
 
   // V^T: key t = 4i + lane/16 goes to position tau^-1(t) = 8*((t%16)/4) + 4*(t/16) + t%4 of each
   // dim row, i.e. 16-byte group i%4 (swizzled), element 4*(i/4) + lane/16
@@ -1049,6 +1048,10 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
       *(uint16_t*)(vt + (d + 1) * kVTRow + 16 * vt_swz(d + 1, g) + off) = (uint16_t)(vw[t] >> 16);
     }
   }
+  // a new row block's queries (else q already holds its rows), issued after the wait for this
+  // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
+  // issued before it they would make that wait also retire the next unit's K
+  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);
   load_lines(p, nx_addr, lane, 1, v);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
