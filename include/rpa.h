@@ -82,7 +82,8 @@ const char* rpa_last_error(void);
 size_t rpa_workspace_size(const rpa_shape_t* shape);
 
 /* One-time initialisation of a freshly allocated workspace (zeroes the error
- * word and the split-K descriptors, which every call leaves cleared again),
+ * word, the split-K descriptors and the heavy-merge flags, which every call
+ * leaves cleared again),
  * stream-ordered.  Call once per workspace buffer.  Calls sharing one
  * workspace must not overlap in time (same stream, or ordered by events). */
 int rpa_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
