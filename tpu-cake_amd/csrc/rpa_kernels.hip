@@ -1645,13 +1645,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         LineRegs k, v;
         f32x4 bias[2];
         bf16x8 q[4];
+        // K, bias, queries, V: the loop's order (vmcnt retires in order, and the compiler
+        // counts each wait for the least favourable path into it, this prologue included)
         {
           const LineAddr a0 = line_addr(p, cur, pg_cur, lane, n, j, wv, err);
           load_lines(p, a0, lane, 0, k);
-          load_lines(p, a0, lane, 1, v);
           load_line_bias<MODE>(p, a0, bias);
+          load_q<MODE>(p, cur, n, j, wv, q);
+          load_lines(p, a0, lane, 1, v);
         }
-        load_q<MODE>(p, cur, n, j, wv, q);
         store_k_tile<MODE>(p, k, kt, lane);
         RowState st;
         long long u = u0;
@@ -1663,12 +1665,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       } else {
         HalfRegs<MODE> ka, va, kb, vb;
         bf16x8 q[4];
-        {
+        {  // K, queries, V: the loop's order (as above)
           const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err);
           load_half<MODE, UPG>(p, a0, 0, ka);
+          load_q<MODE>(p, cur, n, j, wv, q);
           load_half<MODE, UPG>(p, a0, 1, va);
         }
-        load_q<MODE>(p, cur, n, j, wv, q);
         RowState st;
 
         long long u = u0;
