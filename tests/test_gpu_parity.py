@@ -101,7 +101,7 @@ def test_long_sequence_split_k(cuda):
     _check(case)
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 8), (8, 2)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (64, 8), (8, 2), (8, 1)])
 def test_heavy_merges(cuda, hq, hkv):
     # several long sequences, each spread over dozens of workgroups (merged by the dim-sliced
     # helper workgroups), with 4-, 8- and 16-row blocks, among short ones merged the ordinary way
