@@ -8,7 +8,9 @@
 //     workgroups owner(first)..owner(last), each workgroup contributes to at most one split row
 //     block that began before its range and one that runs past its end, and the partial slots
 //     they write (2*b0+1, then 2*b) are distinct across the whole call;
-//   * a row block's units visit keys up to the causal limit of its last row and no further.
+//   * a row block's units visit keys up to the causal limit of its last row and no further;
+//   * the heavy split row blocks of a call (kHeavyContrib or more contributors) have distinct
+//     helper slots heavy_slot(describer), all below heavy_slots(grid).
 // Prints "OK <cases>" or the first violation.
 #include <cstdio>
 #include <cstdlib>
@@ -30,6 +32,7 @@ static int fail(const char* what, long long a, long long b) {
 int main() {
   std::mt19937_64 rng(1234);
   int cases = 0;
+  long long heavy_blocks = 0;
   for (int it = 0; it < 400; ++it) {
     const int Hkv = 1 + (int)(rng() % 8);
     const int G = 1 + (int)(rng() % 16);
@@ -84,7 +87,7 @@ int main() {
         if (owner_of(u, pt) != owner[u]) return fail("owner_of", owner_of(u, pt), owner[u]);
       }
       // split row blocks: describer, contributors, slots
-      std::set<long long> slots, counters;  // counters: descriptor indices
+      std::set<long long> slots, counters, heavy;  // counters: descriptor indices
       std::vector<int> heads(grid, 0), tails(grid, 0);
       long long start = 0;
       while (start < W) {
@@ -98,6 +101,12 @@ int main() {
           // the kernel's view: b0 processes c == 0 (started_here) and runs past its range end;
           // every later contributor starts inside the block; b1 ends it and describes it.
           if (!counters.insert(b1).second) return fail("descriptor reused", b1, b0);
+          if (b1 - b0 + 1 >= kHeavyContrib) {
+            const int hs = heavy_slot(b1);
+            if (hs < 0 || hs >= heavy_slots((int)grid)) return fail("heavy slot out of range", hs, grid);
+            if (!heavy.insert(hs).second) return fail("heavy slot shared", hs, b1);
+            ++heavy_blocks;
+          }
           for (long long b = b0; b <= b1; ++b) {
             if (++(b == b0 ? tails : heads)[b] > 1) return fail("two pieces of one kind", b, b0);
             const long long u0 = range_start(b, pt), u1 = range_start(b + 1, pt);
@@ -114,6 +123,7 @@ int main() {
     }
     ++cases;
   }
-  std::printf("OK %d\n", cases);
+  if (heavy_blocks == 0) return fail("no heavy split row block exercised", 0, 0);
+  std::printf("OK %d (%lld heavy split row blocks)\n", cases, heavy_blocks);
   return 0;
 }

@@ -112,7 +112,8 @@ def test_plan_lds_matches_kernel_constants():
 
 
 def test_combine_grid_matches_kernel_constants():
-    const = dict(re.findall(r"constexpr int (kHeavyContrib|kHeavySlices) = (\d+);", KERNEL_SRC))
+    sched = (ROOT / "tpu-cake_amd" / "csrc" / "rpa_schedule.h").read_text()
+    const = dict(re.findall(r"constexpr int (kHeavyContrib|kHeavySlices) = (\d+);", sched))
     assert int(const["kHeavyContrib"]) == contracts.HEAVY_CONTRIB
     assert int(const["kHeavySlices"]) == contracts.HEAVY_SLICES
     # 256 workgroups of 8 kv heads: 2048 merges + 9 slots x 8 heads x 4 slices

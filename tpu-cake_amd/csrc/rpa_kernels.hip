@@ -83,15 +83,6 @@ struct SplitDesc {
   long long b0;
 };
 
-// Heavy merges: a split row block with at least kHeavyContrib contributors (a long sequence spread
-// over many workgroups) is merged by kHeavySlices helper workgroups per head, each over 32 of the
-// 128 dims, instead of one.  Its contributors b0..b span at least kHeavyContrib - 1 workgroup
-// boundaries and the next heavy descriptor's first contributor is >= b, so b / (kHeavyContrib - 1)
-// differs between any two heavy descriptors of a call: that is its helper slot.
-constexpr int kHeavyContrib = 32;
-constexpr int kHeavySlices = 4;
-__host__ __device__ constexpr int heavy_slot(long long b) { return (int)(b / (kHeavyContrib - 1)); }
-__host__ __device__ constexpr int heavy_slots(int grid) { return (grid - 1) / (kHeavyContrib - 1) + 1; }
 
 struct Params {
   const uint16_t* q;
