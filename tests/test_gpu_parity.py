@@ -178,6 +178,17 @@ def test_fp8_kv_per_page_scales(cuda):
 
 
 @pytest.mark.parametrize("page", [16, 64])
+def test_fp8_kv_window_soft_cap(cuda, page):
+    # the knobs on the fp8 path (per-key pages at 16, one page per unit at 64), decode and a
+    # short chunk of query rows
+    _say(f"fp8 KV with sliding window + soft cap, page {page}")
+    case = make_custom(kv_lens=[300, 77, 1000], q_lens=[6, 1, 1], num_q_heads=32, num_kv_heads=8,
+                       page_size=page, seed=47 + page, kv_dtype="fp8")
+    kw = dict(sliding_window=50, soft_cap=5.0)
+    _check(case, gpu_kw=kw, oracle_kw=kw)
+
+
+@pytest.mark.parametrize("page", [16, 64])
 def test_fp8_kv_scalar_scales(cuda, page):
     # fp8 codes with the reference's scalar k_scale / v_scale instead of per-page scales
     _say(f"fp8 KV with scalar k_scale / v_scale, page {page}")
