@@ -124,6 +124,17 @@ def test_chunked_prefill_and_decode_mixed(cuda):
     _check(case)
 
 
+@pytest.mark.parametrize("mode", ["fp8", "scaled"])
+def test_chunked_prefill_without_tiles(cuda, mode):
+    # fp8 KV and scalar K/V scales take no prefill tiles: their long query chunks run as causal
+    # 16-row blocks through the stream-K role
+    _say(f"chunked prefill through stream-K, {mode}")
+    case = make_custom(kv_lens=[700, 45, 1030, 9], q_lens=[1, 45, 130, 1], num_q_heads=32, num_kv_heads=8,
+                       page_size=64, seed=53, kv_dtype="fp8" if mode == "fp8" else "bf16")
+    kw = dict(k_scale=0.75, v_scale=1.25) if mode == "scaled" else {}
+    _check(case, gpu_kw=kw, oracle_kw=kw)
+
+
 def test_padding_rows_and_seqs(cuda):
     _say("padded max_num_seqs and num_tokens")
     case = make_custom(kv_lens=[40, 300], q_lens=[1, 3], num_q_heads=8, num_kv_heads=2, page_size=16, seed=17,
