@@ -643,17 +643,19 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8_exact(u32x2 w) {
   return o;
 }
 
-// UPG fp8: a unit's 32 keys share one page, hence one K and one V scale per head.  Both codes
-// convert exactly (e4m3 values are bf16 values); the K scale multiplies the unit's fp32 scores and
-// the V scale its fp32 probabilities before they are packed for the PV product (compute_unit),
-// i.e. P·(s·V) = (s·P)·V with the rounding to bf16 taken after the product s·P instead of
-// s·V.  Per-key pages (not UPG) apply bf16(v * scale) to every element.
+// UPG fp8: a unit's 32 keys share one page, hence one K and one V scale per head, both loaded with
+// K (HalfRegs::sc).  K codes convert exactly (e4m3 values are bf16 values) and the K scale
+// multiplies the unit's fp32 scores (compute_unit); V keeps the reference's bf16(v * scale) per
+// element, with the V scale passed in (vs).  Per-key pages (not UPG) apply bf16(x * scale) to K
+// and V elements with each key's own scale.
 template <int MODE, bool UPG>
-__device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which) {
+__device__ __forceinline__ u32x4 to_bf16x8(const HalfRegs<MODE>& r, const Params& p, int blk, int s, int which,
+                                           float vs = 1.f) {
   if constexpr (MODE == KV_FP8) {
     const u32x4 w4 = r.w[blk][s >> 1];
     const u32x2 c8 = (s & 1) ? u32x2{w4[2], w4[3]} : u32x2{w4[0], w4[1]};  // the codes of k-step s
     if constexpr (UPG) {
+      if (which) return fp8x8_to_bf16x8(c8, vs);
       return fp8x8_to_bf16x8_exact(c8);
     } else {
       return fp8x8_to_bf16x8(c8, (which ? p.v_scale : p.k_scale) * r.sc[blk]);
@@ -676,11 +678,10 @@ struct RowState {
 };
 
 // The unit's scores s0, s1 (keys 16*blk + 4j + rr of row n) -> online-softmax update of st and
-// P^T packed for the PV MFMA, times p_scale (the unit's V scale, or 1; the denominator l stays
-// unscaled).  bias (KV_BF16_BIAS): the relative bias of those scores.
+// P^T packed for the PV MFMA.  bias (KV_BF16_BIAS): the relative bias of those scores.
 template <int MODE>
 __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x, f32x4 s0, f32x4 s1,
-                                               const f32x4* bias, RowState& st, int j, float p_scale = 1.f) {
+                                               const f32x4* bias, RowState& st, int j) {
   // scores in log2 units; this lane holds keys 16*blk + 4j + rr of row n.  A chunk every row
   // of the block sees in full (no window, no soft cap) needs no per-score masking.
   float xs[2][4];
@@ -746,10 +747,6 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
       lsum += pr[blk][rr];
     }
   st.l += lsum;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) pr[blk][rr] *= p_scale;  // a constant 1 folds away
 
   u32x4 pw;
   pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
@@ -796,7 +793,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     const int slot_b = 2 * (8 * (n >> 2) + 4 * blk + (n & 3));
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 vw = to_bf16x8<MODE, UPG>(vr, p, blk, s, 1);
+      const u32x4 vw = to_bf16x8<MODE, UPG>(vr, p, blk, s, 1, vs);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         uint32_t w = vw[t];
@@ -809,7 +806,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);  // a new row block's queries (as in compute_unit_line)
   load_half<MODE, UPG>(p, nx_addr, 1, v_next);
 
-  const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j, vs);
+  const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j);
 
   wave_lds_fence();
 #pragma unroll
