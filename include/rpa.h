@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RPA_ABI_VERSION 1
+#define RPA_ABI_VERSION 2
 
 enum {
   RPA_OK = 0,
@@ -54,9 +54,24 @@ typedef struct rpa_shape {
 } rpa_shape_t;
 
 /* Scalar knobs of the reference signature (:718-731).  Zero-initialise and
- * set what is used: sliding_window 0 = none, soft_cap 0 = none,
- * has_mask_value 0 = DEFAULT_MASK_VALUE (-0.7 * FLT_MAX, :32),
- * has_k_scale / has_v_scale 0 = no scalar K/V scale. */
+ * set what is used: sliding_window 0 = none, soft_cap 0 = none (any nonzero
+ * value caps as the reference's soft_cap * tanh(s / soft_cap), which equals
+ * |soft_cap| * tanh(s / |soft_cap|)), has_mask_value 0 = DEFAULT_MASK_VALUE
+ * (-0.7 * FLT_MAX, :32), has_k_scale / has_v_scale 0 = no scalar K/V scale.
+ *
+ * Tuning knobs (ABI 2), per call, zero = the library default; they change the
+ * schedule, never the result beyond fp32 summation order.  They take the place
+ * of the reference's per-call block sizes num_kv_pages_per_block /
+ * num_queries_per_block (ragged_paged_attention.py:726-728, :801-816):
+ *   waves_per_cu   1..7 caps the persistent attention grid at that many waves
+ *                  per compute unit (0 or 8: the kernel's occupancy, 8);
+ *   prefill_tiles  -1 = sequences with long query chunks run as causal row
+ *                  blocks of the stream-K role, 0 or 1 = they take the
+ *                  MFMA prefill tiles where those are built (bf16 KV without
+ *                  scales, the default mask value, 8 kv heads per workgroup);
+ *   prefill_cost   > 0: the cost of one prefill-tile chunk step in stream-K
+ *                  units, which sets the work split between the two roles
+ *                  (0 = 0.45). */
 typedef struct rpa_options {
   float sm_scale;
   int32_t sliding_window;
@@ -67,6 +82,9 @@ typedef struct rpa_options {
   float k_scale;
   int32_t has_v_scale;
   float v_scale;
+  int32_t waves_per_cu;
+  int32_t prefill_tiles;
+  float prefill_cost;
 } rpa_options_t;
 
 /* ABI version of the loaded library (RPA_ABI_VERSION). */
@@ -101,9 +119,16 @@ int rpa_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
  *   k_scale / v_scale, :124-129); dequantised K = bf16(float(k) * scale).
  * Rows of `out` at or past cu_q_lens[num_seqs] are written as zeros.
  * Stream-ordered and asynchronous; no host synchronisation inside.
- * Metadata is range-checked on the device: an out-of-range page id or query
- * row is never dereferenced, the affected rows are left unwritten, and a
- * nonzero error word is recorded (rpa_read_error_word). */
+ * Metadata is range-checked on the device, and an out-of-range value is never
+ * dereferenced: a page id outside [0, total_pages) is replaced by page 0 (the
+ * rows that read it hold values computed from page 0's keys, i.e. garbage), a
+ * query range outside [0, num_tokens) makes its sequence contribute no rows
+ * (left unwritten), kv_len is clamped to pages_per_seq * page_size, and a bit
+ * of the error word is set (rpa_read_error_word).  A caller that cannot rule
+ * out bad metadata must read the error word and discard the output when it is
+ * nonzero; the reference instead rejects such metadata on the host before any
+ * launch (ragged_paged_attention.py:152-212, rpa_lowering.py:71-128), which is
+ * what the Python wrapper does. */
 int rpa_ragged_paged_attention(const rpa_shape_t* shape, const rpa_options_t* options,
                                const void* q, const void* kv_pages, const float* kv_scales,
                                const int32_t* kv_lens, const int32_t* page_indices,

@@ -271,9 +271,16 @@ def ref_ragged_paged_attention(
         head_map = np.arange(num_q_heads) // group
         if _mutation == "wrong_gqa_map":
             head_map = np.arange(num_q_heads) % num_kv_heads
-        kk = k[:, head_map, :].astype(np.float64)    # [L, Hq, D]
-        vv = v[:, head_map, :].astype(np.float64)
-        attn = np.einsum("qhd,khd->hqk", q, kk).astype(np.float32)
+        # repeat(k, G, axis=1) then einsum("qhd,khd->hqk") (:130-133), computed per kv head as one
+        # float64 matrix product over the q heads that map to it (the same sums, BLAS speed)
+        kk = k.astype(np.float64)                    # [L, Hkv, D]
+        vv = v.astype(np.float64)
+        groups = [(hk, np.nonzero(head_map == hk)[0]) for hk in range(num_kv_heads)]
+        attn = np.empty((num_q_heads, q_len, kv_len), dtype=np.float32)
+        for hk, heads in groups:
+            if heads.size:
+                qh = q[:, heads, :].transpose(1, 0, 2).reshape(-1, head_dim)   # [g * q_len, D]
+                attn[heads] = (qh @ kk[:, hk, :].T).reshape(heads.size, q_len, kv_len)
         scale = sm_scale if _mutation != "wrong_scale" else 1.0 / head_dim
         attn = (attn * np.float32(scale)).astype(np.float32)
         q_span = (kv_len - q_len) + np.arange(q_len)[None, :, None]
@@ -291,7 +298,11 @@ def ref_ragged_paged_attention(
         probs = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
         if probs_bf16:
             probs = bf16_round(probs)
-        out = np.einsum("hqk,khd->qhd", probs.astype(np.float64), vv).astype(np.float32)
+        out = np.empty((q_len, num_q_heads, head_dim), dtype=np.float32)
+        for hk, heads in groups:   # einsum("hqk,khd->qhd") (:144-145), per kv head
+            if heads.size:
+                pv = probs[heads].astype(np.float64).reshape(-1, kv_len) @ vv[:, hk, :]
+                out[:, heads, :] = pv.reshape(heads.size, q_len, head_dim).transpose(1, 0, 2)
         outs.append(out)
     if not outs:
         return np.zeros((0, num_q_heads, head_dim), dtype=np.float32)

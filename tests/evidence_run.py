@@ -10,6 +10,8 @@ import json
 import pathlib
 import sys
 
+import numpy as np
+
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 sys.path[:0] = [str(ROOT), str(ROOT / "tpu-cake_amd")]
 
@@ -24,7 +26,7 @@ def oracle_checker(case, out):
     ref = orc.ref_ragged_paged_attention(case.q, case.kv_pages, case.kv_lens, case.page_indices, case.cu_q_lens,
                                          case.num_seqs, sm_scale=case.sm_scale, kv_scales=case.kv_scales,
                                          kv_dtype=case.kv_dtype)
-    got = out.float().cpu().numpy()[: ref.shape[0]]
+    got = (out.float().cpu().numpy() if hasattr(out, "float") else np.asarray(out, np.float32))[: ref.shape[0]]
     err = orc.errors(got, orc.bf16_round(ref))
     return {"oracle": "oracle/rpa_oracle.py::ref_ragged_paged_attention", "tolerance": TOL,
             "max_abs": err["max_abs"], "max_rel": err["max_rel"], "rel_l2": err["rel_l2"], "finite": err["finite"],

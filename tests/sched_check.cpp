@@ -8,7 +8,9 @@
 //     workgroups owner(first)..owner(last), each workgroup contributes to at most one split row
 //     block that began before its range and one that runs past its end, and the partial slots
 //     they write (2*b0+1, then 2*b) are distinct across the whole call;
-//   * a row block's units visit keys up to the causal limit of its last row and no further;
+//   * a row block's units visit keys up to the causal limit of its last row and no further, and
+//     with a sliding window start at the chunk of the lowest key its first row sees (every key
+//     below is masked for every row of the block) and no later;
 //   * the heavy split row blocks of a call (kHeavyContrib or more contributors) have distinct
 //     helper slots heavy_slot(describer), all below heavy_slots(grid).
 // Prints "OK <cases>" or the first violation.
@@ -38,6 +40,7 @@ int main() {
     const int G = 1 + (int)(rng() % 16);
     const int N = 1 + (int)(rng() % 40);
     const bool skip = rng() % 4 != 0;
+    const int window = rng() % 3 == 0 ? 1 + (int)(rng() % 700) : 0;
     std::vector<int> kv(N), ql(N);
     for (int i = 0; i < N; ++i) {
       const int mode = (int)(rng() % 4);
@@ -47,13 +50,26 @@ int main() {
     }
     std::vector<Unit> units;
     for (int i = 0; i < N; ++i) {
-      const int per_head = seq_units_per_head(kv[i], ql[i], G, skip);
+      const int per_head = seq_units_per_head(kv[i], ql[i], G, skip, window);
       int sum = 0;
       for (int h = 0; h < Hkv; ++h)
         for (int rb = 0; rb < num_row_blocks(ql[i], G); ++rb) {
-          const int n = rb_units(kv[i], ql[i], G, rb, skip);
+          const int n = rb_units(kv[i], ql[i], G, rb, skip, window);
+          const int c0 = rb_first_chunk(kv[i], ql[i], G, rb, skip, window);
           const int vis = rb_visible_keys(kv[i], ql[i], G, rb, skip);
-          if (n * KV_CHUNK < vis || (n - 1) * KV_CHUNK >= vis) return fail("chunks vs visible keys", n, vis);
+          if (vis > 0 && ((c0 + n) * KV_CHUNK < vis || (c0 + n - 1) * KV_CHUNK >= vis))
+            return fail("chunks vs visible keys", c0 + n, vis);
+          if (vis <= 0 && n != 0) return fail("units of an invisible block", n, vis);
+          // the window: no visible key of any row lies below chunk c0, and (a tight start) the
+          // first row sees a key of chunk c0
+          const int first_row_pos = kv[i] - ql[i] + rb * ROW_BLOCK / G;
+          if (window > 0 && skip) {
+            const int lowest = first_row_pos - window + 1;  // keys <= pos - window are masked
+            if (c0 * KV_CHUNK > (lowest > 0 ? lowest : 0)) return fail("window start past a visible key", c0, lowest);
+            if (lowest > 0 && (c0 + 1) * KV_CHUNK <= lowest) return fail("window start not tight", c0, lowest);
+          } else if (c0 != 0) {
+            return fail("chunk start without a window", c0, window);
+          }
           if (skip) {  // causal limit of the block's last existing row
             const int last_row = std::min(ql[i] * G - 1, rb * ROW_BLOCK + ROW_BLOCK - 1);
             const int limit = kv[i] - ql[i] + last_row / G + 1;

@@ -43,7 +43,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rpa_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.rpa_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_struct_layout_matches_c(tmp_path):
@@ -51,9 +51,12 @@ def test_struct_layout_matches_c(tmp_path):
     src.write_text(
         '#include <stdio.h>\n#include <stddef.h>\n#include "rpa.h"\n'
         "int main(void){\n"
-        '  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t), offsetof(rpa_shape_t, kv_dtype),\n'
+        '  printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n", sizeof(rpa_shape_t),\n'
+        "         offsetof(rpa_shape_t, kv_dtype),\n"
         "         sizeof(rpa_options_t), offsetof(rpa_options_t, mask_value), offsetof(rpa_options_t, v_scale),\n"
-        "         offsetof(rpa_options_t, has_k_scale), sizeof(rpa_fused_shape_t),\n"
+        "         offsetof(rpa_options_t, has_k_scale), offsetof(rpa_options_t, waves_per_cu),\n"
+        "         offsetof(rpa_options_t, prefill_tiles), offsetof(rpa_options_t, prefill_cost),\n"
+        "         sizeof(rpa_fused_shape_t),\n"
         "         offsetof(rpa_fused_shape_t, relative_extent), sizeof(rpa_inkling_shape_t),\n"
         "         offsetof(rpa_inkling_shape_t, bias_len));\n  return 0; }\n")
     exe = tmp_path / "layout"
@@ -61,7 +64,8 @@ def test_struct_layout_matches_c(tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [ctypes.sizeof(_lib.RpaShape), _lib.RpaShape.kv_dtype.offset, ctypes.sizeof(_lib.RpaOptions),
             _lib.RpaOptions.mask_value.offset, _lib.RpaOptions.v_scale.offset, _lib.RpaOptions.has_k_scale.offset,
-            ctypes.sizeof(_lib.RpaFusedShape), _lib.RpaFusedShape.relative_extent.offset,
+            _lib.RpaOptions.waves_per_cu.offset, _lib.RpaOptions.prefill_tiles.offset,
+            _lib.RpaOptions.prefill_cost.offset, ctypes.sizeof(_lib.RpaFusedShape), _lib.RpaFusedShape.relative_extent.offset,
             ctypes.sizeof(_lib.RpaInklingShape), _lib.RpaInklingShape.bias_len.offset]
     assert got == want
 
@@ -87,6 +91,17 @@ def test_unsupported_head_dim_rejected_before_launch(lib):
 def test_invalid_shapes_rejected(lib, bad, msg):
     opts = _lib.RpaOptions(sm_scale=1.0)
     rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape(**bad)), ctypes.byref(opts), *([None] * 9), 0, None)
+    assert rc == -1 and msg in lib.rpa_last_error()
+
+
+@pytest.mark.parametrize("knob,msg", [(dict(waves_per_cu=9), b"waves_per_cu"), (dict(waves_per_cu=-1), b"waves_per_cu"),
+                                      (dict(prefill_tiles=2), b"prefill_tiles"),
+                                      (dict(prefill_cost=-0.5), b"prefill_cost")])
+def test_invalid_tuning_knobs_rejected(lib, knob, msg):
+    opts = _lib.RpaOptions(sm_scale=1.0, **knob)
+    # distinct fake pointers, never dereferenced: the options are checked before any launch
+    ptrs = [ctypes.c_void_p(256 * (i + 1)) for i in range(9)]
+    rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape()), ctypes.byref(opts), *ptrs, 0, None)
     assert rc == -1 and msg in lib.rpa_last_error()
 
 

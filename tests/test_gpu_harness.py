@@ -2,8 +2,8 @@
 the oracle as checker (tpu_cake_amd.evidence); the rocprofv3 phases run from tests/evidence_run.py."""
 
 import json
-import sys
 import pathlib
+import sys
 
 import pytest
 import torch
@@ -22,16 +22,26 @@ def cuda():
         pytest.skip("no GPU")
 
 
-def test_search_runs_every_candidate_in_latin_order(cuda, tmp_path):
-    print("[case] knob search c1", flush=True)
-    cands = {"base": {}, "w4": {"RPA_WAVES_PER_CU": "4"}}
-    res = search.run_search(tmp_path, "c1", cands, baseline="base", rounds=4, steps=3, warmup=1)
-    log = json.loads((tmp_path / "runs.json").read_text())
-    assert [e["candidate"] for e in log[:4]] == ["base", "w4", "w4", "base"]
-    for name in cands:
+def test_search_with_trace_runs_and_the_oracle_gate(cuda, tmp_path):
+    """A small real search on C1: every run a rocprofv3-traced child process, the objective from the
+    trace, every candidate gated by the oracle; then a resume re-validates every run."""
+    print("[case] knob search c1 (rocprofv3 runs)", flush=True)
+    c = search.SearchContract(config="c1", baseline="base", candidates=(("base", {}), ("w4", {"waves_per_cu": 4})),
+                              rounds=4, confirmation_rounds=0, steps=3, warmup=1, bootstrap_samples=1000)
+    res = search.run_search(tmp_path, c, runner=search.TraceRunner(timeout_s=240), checker=evidence_run.oracle_checker)
+    assert res["rejected_candidates"] == []
+    assert all(v["passed"] and v["max_abs"] <= 2e-2 for v in res["correctness"].values())
+    for name in ("base", "w4"):
         st = res["statistics"][name]
-        assert st["runs"] >= 2 and st["median_ns"] > 0
-    assert res["winner"] in (None, "w4")
+        assert st["runs"] == 4 and st["samples"] == 12 and st["median_ns"] > 0
+    assert res["winner"] is None  # no confirmation rounds were asked for
+
+    class NoRuns:
+        def run(self, *a):
+            raise AssertionError("a completed run was run again")
+
+    again = search.run_search(tmp_path, c, runner=NoRuns(), checker=evidence_run.oracle_checker)
+    assert again["statistics"]["w4"]["median_ns"] == res["statistics"]["w4"]["median_ns"]
 
 
 def test_timing_phase_with_the_oracle_checker(cuda, tmp_path):

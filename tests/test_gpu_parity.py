@@ -363,13 +363,12 @@ def test_prefill_tiles_window_and_soft_cap(cuda):
     _check(case, gpu_kw=dict(sliding_window=100, soft_cap=30.0), oracle_kw=dict(sliding_window=100, soft_cap=30.0))
 
 
-def test_prefill_tiles_match_stream_k(cuda, monkeypatch):
-    """The same batch with prefill tiles switched off (RPA_NO_PREFILL_TILES, read per call)
-    agrees with the tiled result to the bf16 output tolerance."""
+def test_prefill_tiles_match_stream_k(cuda):
+    """The same batch with prefill tiles switched off (the per-call prefill_tiles knob) agrees with
+    the tiled result to the bf16 output tolerance."""
     _say("prefill tiles vs stream-K only")
     case = make_custom(kv_lens=[1200, 700, 64], q_lens=[256, 1, 64], num_q_heads=32, num_kv_heads=8, page_size=64,
                        seed=73)
-    tiled = _gpu_out(case)
-    monkeypatch.setenv("RPA_NO_PREFILL_TILES", "1")
-    plain = _gpu_out(case)
+    tiled = _gpu_out(case, prefill_tiles=True)
+    plain = _gpu_out(case, prefill_tiles=False)
     assert orc.errors(tiled, plain)["max_abs"] <= TOL_BF16

@@ -1,5 +1,5 @@
 """GPU parity over random valid batches: KV modes (bf16, fp8, scalar K/V scales), page sizes
-1..128, GQA groups 1..16, 1..8 kv heads, decode rows and query chunks up to 80 tokens, sliding
+1..128, GQA groups 1..16 (including 3, 5, 6, 7), 1..12 kv heads (kv-head groups of 1..8 waves), decode rows and query chunks up to 80 tokens, sliding
 window and soft cap, each against the oracle on the same inputs.
 
 Bar per case: the reference's own gate, allclose(atol=rtol=0.02) (``src/tpu_cake/rpa_runner.py:105-122``),
@@ -19,8 +19,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _random_case(rng):
-    hkv = int(rng.choice([1, 2, 4, 8]))
-    g = int(rng.choice([1, 2, 4, 8, 16])) if hkv < 8 else int(rng.choice([1, 4, 8]))
+    hkv = int(rng.choice([1, 2, 3, 4, 6, 8, 12]))
+    g = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16])) if hkv < 8 else int(rng.choice([1, 3, 4, 5, 8]))
     page = int(rng.choice([1, 8, 16, 24, 32, 64, 128]))
     kvl, ql = [], []
     for _ in range(int(rng.integers(1, 12))):

@@ -2,11 +2,13 @@
 (tpu_cake_amd.search, after rpa_search.py:201-210), rocprofv3 profile inspection and the receipt
 over three phases (tpu_cake_amd.evidence, after rpa_bundle.py:664-800), on synthetic files."""
 
+import hashlib
 import json
 
+import numpy as np
 import pytest
 
-from tpu_cake_amd import evidence, search
+from tpu_cake_amd import evidence, search, tuned
 
 
 def test_orders_are_forward_then_reversed_latin_squares():
@@ -19,35 +21,208 @@ def test_orders_are_forward_then_reversed_latin_squares():
         search.execution_orders(["a", "b"], 3)
 
 
-def test_statistics_promote_only_a_clear_improvement():
-    base = [[100 + (i % 3)] * 5 for i in range(8)]
-    fast = [[80 + (i % 3)] * 5 for i in range(8)]
-    same = [[100 + ((i + 1) % 3)] * 5 for i in range(8)]
-    st = search.statistics({"base": base, "fast": fast, "same": same}, "base", resamples=400)
-    assert st["fast"]["promotable"] and st["fast"]["improvement"] > 0.2
-    assert not st["same"]["promotable"] and not st["base"]["promotable"]
-    assert st["base"]["runs"] == 8 and st["base"]["samples"] == 40
+def _contract(**kw):
+    base = dict(config="c3", baseline="incumbent", rounds=6, confirmation_rounds=6, bootstrap_samples=1000,
+                candidates=(("incumbent", {}), ("pf25", {"prefill_cost": 0.25}), ("pf50", {"prefill_cost": 0.5})))
+    base.update(kw)
+    return search.SearchContract(**base)
+
+
+def _timing(median):
+    return search.DeviceTiming.of([float(median)] * 50)
+
+
+def test_statistics_promote_from_paired_run_level_measurements():
+    # the reference's own case (tests/test_rpa_search.py:100-115): 20% faster in every round is
+    # promotable with an interval above the 1% practical threshold, +-2% noise is not
+    c = _contract()
+    res = {"incumbent": [_timing(v) for v in (100, 102, 98, 101, 99, 100)],
+           "pf25": [_timing(v) for v in (80, 82, 78, 81, 79, 80)],
+           "pf50": [_timing(v) for v in (101, 100, 100, 102, 99, 101)]}
+    st = search.statistics(c, res)
+    assert st["pf25"]["promotable"] and st["pf25"]["runs"] == 6 and st["pf25"]["samples"] == 300
+    assert st["pf25"]["improvement_ci95"][0] > 0.01
+    assert not st["pf50"]["promotable"] and not st["incumbent"]["promotable"]
+
+
+def test_statistics_are_paired_per_round():
+    # a session-wide drift that hits both candidates alike: unpaired medians overlap, the paired
+    # per-round improvement (always +3%) is promotable
+    c = _contract(candidates=(("incumbent", {}), ("pf25", {"prefill_cost": 0.25})), rounds=8)
+    drift = [100, 130, 90, 120, 95, 140, 105, 110]
+    res = {"incumbent": [_timing(d) for d in drift], "pf25": [_timing(d * 0.97) for d in drift]}
+    st = search.statistics(c, res)
+    assert st["pf25"]["promotable"] and abs(st["pf25"]["improvement"] - 0.03) < 1e-9
+    # below the practical threshold: +0.5% every round is real but not worth promoting
+    res = {"incumbent": [_timing(d) for d in drift], "pf25": [_timing(d * 0.995) for d in drift]}
+    assert not search.statistics(c, res)["pf25"]["promotable"]
+
+
+def test_confirmation_requires_fresh_paired_improvement():
+    c = _contract()
+    orders = [("incumbent", "pf25") if i % 2 == 0 else ("pf25", "incumbent") for i in range(6)]
+    conf = search.confirmation_statistics(c, "pf25", orders, [_timing(v) for v in (100, 102, 98, 101, 99, 100)],
+                                          [_timing(v) for v in (80, 82, 78, 81, 79, 80)])
+    assert conf["confirmed"] and conf["runs"] == 6 and conf["orders"][1] == ["pf25", "incumbent"]
+    conf = search.confirmation_statistics(c, "pf25", orders, [_timing(100)] * 6, [_timing(99.5)] * 6)
+    assert not conf["confirmed"]
+
+
+@pytest.mark.parametrize("kw,msg", [(dict(rounds=4), "Latin squares"), (dict(confirmation_rounds=3), "both run orders"),
+                                    (dict(baseline="nope"), "baseline"),
+                                    (dict(candidates=(("a", {}), ("b", {"prefill_cost": 0.0}))), "unique"),
+                                    (dict(candidates=(("a", {}), ("b", {"bogus": 1}))), "unknown knobs"),
+                                    (dict(bootstrap_samples=10), "bootstrap")])
+def test_contract_rejections(kw, msg):
+    if "candidates" in kw:
+        kw.setdefault("baseline", "a")
+        kw.setdefault("rounds", 4)
+    with pytest.raises(ValueError, match=msg):
+        _contract(**kw)
+
+
+def _trace_csv(path, durations_by_call):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    rows = ['"Kind","Dispatch_Id","Kernel_Name","Start_Timestamp","End_Timestamp"']
+    t = 1000
+    for i, (a, c) in enumerate(durations_by_call):
+        rows.append(f'"KERNEL_DISPATCH",{2 * i},"void rpa::(anonymous namespace)::rpa_attn_kernel<0, true>(Params)",'
+                    f'{t},{t + a}')
+        t += a + 7
+        rows.append(f'"KERNEL_DISPATCH",{2 * i + 1},"rpa::(anonymous namespace)::rpa_combine_kernel(Params)",{t},{t + c}')
+        t += c + 50
+        rows.append(f'"KERNEL_DISPATCH",{900 + i},"__amd_rocclr_copyBuffer",{t},{t + 3}')
+        t += 10
+    path.write_text("\n".join(rows) + "\n")
+
+
+def test_device_timing_from_the_kernel_trace(tmp_path):
+    _trace_csv(tmp_path / "trace" / "x" / "run_kernel_trace.csv", [(500, 50)] * 2 + [(100 + i, 10) for i in range(4)])
+    t = search.device_timing(tmp_path, 4)  # the last 4 calls, attention + combine each
+    assert t.durations_ns == (110.0, 111.0, 112.0, 113.0) and t.median_ns == 111.5
+    with pytest.raises(ValueError, match="DISPATCH_PROTOCOL"):
+        search.device_timing(tmp_path, 7)
+
+
+def test_incomplete_run_is_archived_with_a_manifest(tmp_path):
+    run = tmp_path / "round-00" / "00-incumbent"
+    run.mkdir(parents=True)
+    (run / "failure.log").write_text("launch failed\n")
+    arch = search.archive_incomplete_run(tmp_path, run, "launch failed")
+    assert not run.exists() and arch == tmp_path / "incomplete/round-00/00-incumbent-attempt-00"
+    assert "launch failed" in (arch / "failure.json").read_text()
+    att = search.incomplete_attempts(tmp_path)
+    assert len(att) == 1 and att[0]["path"] == "incomplete/round-00/00-incumbent-attempt-00"
+    before = att[0]["manifest_sha256"]
+    (arch / "failure.log").write_text("changed\n")
+    assert search.incomplete_attempts(tmp_path)[0]["manifest_sha256"] != before
+    run.mkdir(parents=True)
+    assert search.archive_incomplete_run(tmp_path, run, "again").name == "00-incumbent-attempt-01"
+
+
+class _Case:
+    def __init__(self):
+        self.q = np.arange(8, dtype=np.uint16)
+        self.kv_pages = np.arange(16, dtype=np.uint16)
+        self.kv_lens = np.array([3], np.int32)
+        self.page_indices = np.array([[0]], np.int32)
+
+    def sha(self):
+        return hashlib.sha256(self.q.tobytes() + self.kv_pages.tobytes() + self.kv_lens.tobytes()
+                              + self.page_indices.tobytes()).hexdigest()
 
 
 class _FakeRunner:
-    def __init__(self, times):
-        self.times = times
-        self.calls = []
+    """Writes what a TraceRunner run leaves: steps.json, output.npy and a kernel trace; the device
+    time per call depends on the candidate's prefill_cost, its output bits on whether it is 'bad'."""
 
-    def run(self, env, steps, warmup):
-        self.calls.append(dict(env))
-        return [self.times[env.get("RPA_PF_COST", "base")]] * steps
+    def __init__(self, case, times):
+        self.case, self.times, self.calls = case, times, []
+
+    def run(self, run_root, contract, knobs):
+        self.calls.append(str(run_root))
+        run_root.mkdir(parents=True, exist_ok=True)
+        cost = knobs["prefill_cost"]
+        (run_root / "steps.json").write_text(json.dumps({
+            "identity": {"kernel_source_digest": "k", "library_sha256": "l"}, "input_sha256": self.case.sha(),
+            "config": contract.config, "knobs": knobs}))
+        np.save(run_root / "output.npy", np.full(4, 7 if cost != 0.7 else 9, np.uint16))
+        n = len(self.calls)
+        _trace_csv(run_root / "trace" / "h" / "run_kernel_trace.csv",
+                   [(self.times[cost] + (n % 3), 10)] * (contract.warmup + contract.steps))
 
 
-def test_search_confirms_a_winner(tmp_path):
-    fake = _FakeRunner({"base": 100, "0.25": 90, "0.5": 120})
-    cands = {"base": {}, "pf25": {"RPA_PF_COST": "0.25"}, "pf50": {"RPA_PF_COST": "0.5"}}
-    res = search.run_search(tmp_path, "c3", cands, baseline="base", rounds=6, steps=3, warmup=0, runner=fake)
-    assert res["winner"] == "pf25" and res["provisional_winner"] == "pf25"
-    assert len(fake.calls) == 6 * 3 + 2 * 2  # the rounds, then two confirmation pairs
+def _checker(case, out):
+    return {"passed": bool(np.all(out == out[0]) and out[0] != 0 and
+                           np.all(out.view(np.uint32) >> 16 == 7)), "max_abs": 0.0}
+
+
+def test_search_gates_times_confirms_and_resumes(tmp_path):
+    case = _Case()
+    c = _contract(candidates=(("incumbent", {}), ("pf25", {"prefill_cost": 0.25}), ("pf50", {"prefill_cost": 0.5}),
+                              ("bad", {"prefill_cost": 0.7})), rounds=8, confirmation_rounds=2, steps=5, warmup=2)
+    fake = _FakeRunner(case, {0.0: 1000, 0.25: 900, 0.5: 1200, 0.7: 500})
+    res = search.run_search(tmp_path, c, runner=fake, checker=_checker, case=case)
+    # 'bad' (fastest, wrong output) fails the gate and is never timed
+    assert res["rejected_candidates"] == ["bad"] and not res["correctness"]["bad"]["passed"]
+    assert not any("round-" in p and p.endswith("-bad") for p in fake.calls)
+    assert res["provisional_winner"] == "pf25" and res["winner"] == "pf25"
+    assert res["winner_knobs"]["prefill_cost"] == 0.25 and res["confirmation"]["confirmed"]
+    assert len(fake.calls) == 4 + 8 * 3 + 2 * 2
     assert json.loads((tmp_path / "result.json").read_text())["winner"] == "pf25"
-    with pytest.raises(ValueError, match="unknown knobs"):
-        search.run_search(tmp_path, "c3", {"x": {"BOGUS": "1"}}, baseline="x", rounds=2, runner=fake)
+    # resume: every run re-validated from its files, nothing re-run
+    fake.calls.clear()
+    assert search.run_search(tmp_path, c, runner=fake, checker=_checker, case=case)["winner"] == "pf25"
+    assert fake.calls == []
+    # an unfinished run is archived and run again
+    (tmp_path / "round-00" / "02-pf50" / "result.json").unlink()
+    search.run_search(tmp_path, c, runner=fake, checker=_checker, case=case)
+    assert fake.calls == [str(tmp_path / "round-00" / "02-pf50")]
+    assert search.incomplete_attempts(tmp_path)[0]["path"] == "incomplete/round-00/02-pf50-attempt-00"
+    # a tampered timing no longer replays; a changed contract is refused
+    tpath = tmp_path / "round-00" / "00-incumbent" / "device_timing.json"
+    tpath.write_text(tpath.read_text().replace('"median_ns": 1', '"median_ns": 2'))
+    with pytest.raises(ValueError, match="REPLAY_MISMATCH"):
+        search.run_search(tmp_path, c, runner=fake, checker=_checker, case=case)
+    with pytest.raises(ValueError, match="CONTRACT_CHANGED"):
+        search.run_search(tmp_path, _contract(rounds=12), runner=fake, checker=_checker, case=case)
+
+
+def test_search_refuses_a_candidate_whose_output_changes(tmp_path):
+    case = _Case()
+    c = _contract(candidates=(("incumbent", {}), ("pf25", {"prefill_cost": 0.25})), rounds=4, confirmation_rounds=0,
+                  steps=3, warmup=0)
+
+    class Flaky(_FakeRunner):
+        def run(self, run_root, contract, knobs):
+            super().run(run_root, contract, knobs)
+            if "round-01" in str(run_root) and knobs["prefill_cost"] == 0.25:
+                np.save(run_root / "output.npy", np.full(4, 8, np.uint16))
+
+    with pytest.raises(ValueError, match="CANDIDATE_OUTPUT_MISMATCH"):
+        search.run_search(tmp_path, c, runner=Flaky(case, {0.0: 100, 0.25: 90}), checker=_checker, case=case)
+    assert search.incomplete_attempts(tmp_path)  # the offending run was archived
+
+
+def test_promote_writes_the_tuned_table(tmp_path):
+    res = {"winner": "pf25", "winner_knobs": {"waves_per_cu": 0, "prefill_tiles": True, "prefill_cost": 0.25},
+           "search_id": "ab" * 32, "contract": {"config": "c3", "seed": None, "baseline": "incumbent"},
+           "confirmation": {"improvement": 0.05, "improvement_ci95": [0.02, 0.08]}}
+    path = tmp_path / "tuned.json"
+    key = search.promote(res, path=path)
+    assert key == "bf16/g4/p64/t4096"
+    assert tuned.get_tuned_knobs("bf16", 4, 64, 2072, path=path)["prefill_cost"] == 0.25
+    assert tuned.get_tuned_knobs("bf16", 4, 64, 64, path=path) == tuned.DEFAULTS
+    assert search.promote(dict(res, winner=None), path=path) is None
+
+
+def test_tuned_table_keys_and_checked_in_entries():
+    assert tuned.simplify_key("bf16", 4, 64, 2072) == "bf16/g4/p64/t4096"
+    assert tuned.simplify_key("fp8", 3, 24, 1) == "fp8/g4/p32/t1"
+    with pytest.raises(ValueError):
+        tuned.validate_entry({"waves_per_cu": 9})
+    for key, entry in tuned.table().items():  # the checked-in table is valid
+        assert entry == tuned.validate_entry(entry) and key.count("/") == 3
 
 
 def _write_profile(d, attn_calls=10, counters=None):

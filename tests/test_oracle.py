@@ -104,6 +104,82 @@ def test_reference_known_answer_inkling():
     np.testing.assert_allclose(out[0], np.broadcast_to(np.arange(6) + 12, (4, 6)))
 
 
+def _inkling_case(seed, hq=8, hk=2, d=32, lens=(1, 17, 40), page=8, pool=24):
+    """bf16-representable inputs for the Inkling oracle and the same data in the operator layout
+    (K of kv head h at combined head 2h, V at 2h+1; one query token per sequence)."""
+    g = np.random.default_rng(seed)
+    rnd = lambda *shape: orc.bf16_round(g.normal(size=shape).astype(np.float32))
+    query, kc, vc = rnd(len(lens), hq, d), rnd(pool, page, hk, d), rnd(pool, page, hk, d)
+    mp = max(-(-L // page) for L in lens)
+    perm = g.permutation(pool).astype(np.int32)
+    table = np.zeros((len(lens), mp), np.int32)
+    off = 0
+    for i, L in enumerate(lens):
+        n = -(-L // page)
+        table[i, :n] = perm[off:off + n]
+        off += n
+    lengths = np.asarray(lens, np.int32)
+    kv = np.empty((pool, page, 2 * hk, d), np.float32)
+    kv[:, :, 0::2], kv[:, :, 1::2] = kc, vc
+    op = dict(q_bits=orc.bf16_from_f32(query), kv_pages=orc.bf16_from_f32(kv), kv_lens=lengths,
+              page_indices=table, cu_q_lens=np.arange(len(lens) + 1, dtype=np.int32),
+              num_seqs=np.array([len(lens)], np.int32))
+    return (query, kc, vc, table, lengths), op
+
+
+def test_inkling_reference_zero_bias_is_rpa_at_scale_one_over_d():
+    """With a zero bias the Inkling oracle (scale 1/D, inkling_rpa.py:68) is the upstream operator's
+    oracle at sm_scale = 1/D with fp32 probabilities, over distinct K and V heads, shuffled pages
+    and ragged lengths; at 1/sqrt(D) it is not (the slip this pins)."""
+    (query, kc, vc, table, lengths), op = _inkling_case(3)
+    d = query.shape[-1]
+    zero = np.zeros((query.shape[1], int(lengths.max())), np.float32)
+    got = orc.inkling_rpa_reference(query, kc, vc, table, lengths, zero)
+    ref = orc.ref_ragged_paged_attention(**op, sm_scale=1.0 / d, probs_bf16=False)
+    assert np.allclose(got, ref, atol=2e-5, rtol=2e-5)
+    # and the brute-force dense attention, GQA-expanded, per sequence
+    kmap = np.arange(query.shape[1]) // (query.shape[1] // kc.shape[2])
+    for b, L in enumerate(lengths.tolist()):
+        keys = kc[table[b, : -(-L // kc.shape[1])]].reshape(-1, kc.shape[2], d)[:L][:, kmap]
+        vals = vc[table[b, : -(-L // vc.shape[1])]].reshape(-1, vc.shape[2], d)[:L][:, kmap]
+        dense = orc.dense_attention_f64(query[b][None].astype(np.float64), keys.astype(np.float64),
+                                        vals.astype(np.float64), 1.0 / d, None)[0]
+        assert np.allclose(got[b], dense, atol=2e-5, rtol=2e-5)
+    wrong = orc.ref_ragged_paged_attention(**op, sm_scale=1.0 / np.sqrt(d), probs_bf16=False)
+    assert np.abs(got - wrong).max() > 0.05
+
+
+def test_inkling_reference_bias_selects_and_adds_by_key_position():
+    """A one-hot bias (+60 at key l_h of head h) makes head h return V row l_h of its kv head: the
+    bias is indexed [head, key position] and added to the scaled scores.  A small random bias
+    shifts the result exactly as adding it to the upstream oracle's scores would (mask_value
+    path: bias b -> softmax over s/D + b)."""
+    (query, kc, vc, table, lengths), op = _inkling_case(5)
+    hq, d = query.shape[1], query.shape[2]
+    hk = kc.shape[2]
+    L = int(lengths.max())
+    bias = np.zeros((hq, L), np.float32)
+    pick = [(7 * h + 3) % int(lengths.min()) for h in range(hq)]
+    for h in range(hq):
+        bias[h, pick[h]] = 60.0
+    got = orc.inkling_rpa_reference(query, kc, vc, table, lengths, bias)
+    for b, Lb in enumerate(lengths.tolist()):
+        vals = vc[table[b, : -(-Lb // vc.shape[1])]].reshape(-1, hk, d)[:Lb]
+        for h in range(hq):
+            assert np.allclose(got[b, h], vals[pick[h], h // (hq // hk)], atol=1e-5)
+    # transposing the bias (indexing it [key, head]) would pick other rows
+    small = np.random.default_rng(9).normal(scale=0.3, size=(hq, L)).astype(np.float32)
+    got = orc.inkling_rpa_reference(query, kc, vc, table, lengths, small)
+    kmap = np.arange(hq) // (hq // hk)
+    for b, Lb in enumerate(lengths.tolist()):
+        keys = kc[table[b, : -(-Lb // kc.shape[1])]].reshape(-1, hk, d)[:Lb][:, kmap].astype(np.float64)
+        vals = vc[table[b, : -(-Lb // vc.shape[1])]].reshape(-1, hk, d)[:Lb][:, kmap].astype(np.float64)
+        s = np.einsum("hd,lhd->hl", query[b].astype(np.float64), keys) / d + small[:, :Lb]
+        w = np.exp(s - s.max(axis=1, keepdims=True))
+        w /= w.sum(axis=1, keepdims=True)
+        assert np.allclose(got[b], np.einsum("hl,lhd->hd", w, vals), atol=2e-5)
+
+
 def test_inkling_reference_deterministic_and_finite():
     inputs = orc.inkling_rpa_inputs()
     a = orc.inkling_rpa_reference(*inputs)

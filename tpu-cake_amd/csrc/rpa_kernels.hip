@@ -307,7 +307,7 @@ __device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int
     s.kv_len = kv;
     s.q_start = c0;
     s.q_len = ql;
-    s.units = (pf_min > 0 && ql >= pf_min) ? 0 : seq_units_per_head(kv, ql, p.G, p.skip_masked);
+    s.units = (pf_min > 0 && ql >= pf_min) ? 0 : seq_units_per_head(kv, ql, p.G, p.skip_masked, p.sliding_window);
   }
   return s;
 }
@@ -369,11 +369,20 @@ __device__ __forceinline__ void load_window(const Params& p, int nseq, int base,
 }
 
 struct Cursor {
-  int i, h, rb, c;  // sequence, kv-head group, row block, chunk
+  int i, h, rb, c;  // sequence, kv-head group, row block, chunk (0 .. nch-1 from the block's first)
   int nch;          // chunks of (i, h, rb); 0 = past the end
+  int c0;           // first chunk of the row block (rb_first_chunk: > 0 only with a sliding window)
   int nrb;
   int kv_len, q_len, q_start;
+  // first key of the cursor's chunk
+  __device__ __forceinline__ int key0() const { return (c0 + c) * KV_CHUNK; }
 };
+
+// Chunk range of row block x.rb.
+__device__ __forceinline__ void set_row_block(const Params& p, Cursor& x) {
+  x.nch = rb_units(x.kv_len, x.q_len, p.G, x.rb, p.skip_masked, p.sliding_window);
+  x.c0 = rb_first_chunk(x.kv_len, x.q_len, p.G, x.rb, p.skip_masked, p.sliding_window);
+}
 
 __device__ __forceinline__ void cursor_load_seq(const Params& p, const Window& w, int i, Cursor& x) {
   int k = i - w.base;
@@ -392,13 +401,12 @@ __device__ __forceinline__ Cursor cursor_at(const Params& p, const Window& w, in
   int rem = (int)(ul - (long long)x.h * per_head);
   x.rb = 0;
   for (;;) {
-    int n = rb_units(x.kv_len, x.q_len, p.G, x.rb, p.skip_masked);
-    if (rem < n) {
+    set_row_block(p, x);
+    if (rem < x.nch) {
       x.c = rem;
-      x.nch = n;
       break;
     }
-    rem -= n;
+    rem -= x.nch;
     x.rb++;
   }
   return x;
@@ -431,7 +439,7 @@ __device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Win
       x.h = 0;
       x.rb = 0;
     }
-    x.nch = rb_units(x.kv_len, x.q_len, p.G, x.rb, p.skip_masked);
+    set_row_block(p, x);
     if (x.nch > 0) return;
   }
 }
@@ -455,7 +463,7 @@ __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, in
   Pages r;
   if constexpr (UPG) {
     // one load at a wave-uniform address, kept per lane until it is used (a step later)
-    const size_t idx = x.nch > 0 ? (size_t)x.i * p.PPS + page_of(x.c * KV_CHUNK, p) : 0;
+    const size_t idx = x.nch > 0 ? (size_t)x.i * p.PPS + page_of(x.key0(), p) : 0;
     const int pg = p.page_indices[idx + opaque_zero()];
     r.pg[0] = r.pg[1] = pg;
     return r;
@@ -465,7 +473,7 @@ __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, in
   const size_t row = live ? (size_t)x.i * p.PPS : 0;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    int kt = x.c * KV_CHUNK + 16 * blk + n;
+    int kt = x.key0() + 16 * blk + n;
     kt = live ? (kt < last ? kt : last) : 0;
     r.pg[blk] = p.page_indices[row + page_of(kt, p)];
   }
@@ -534,7 +542,7 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
   a.j8 = 8 * j;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    int kt = x.c * KV_CHUNK + 16 * blk + n;
+    int kt = x.key0() + 16 * blk + n;
     const bool in_seq = live && kt < x.kv_len;
     kt = live ? (kt < last ? kt : last) : 0;
     int pg = pages.pg[blk];
@@ -549,8 +557,8 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
   const int row = x.rb * ROW_BLOCK + n;
   const int lo = bias_chunk_lo(x.kv_len, p.rel_extent);
   const int at = kBiasHead + (x.i * p.Hq + (x.h * p.HG + wv) * p.G + row % p.G) * bias_row_len(p.rel_extent) +
-                 (x.c - lo) * KV_CHUNK + 4 * j;
-  a.bias_at = live && x.c >= lo ? at : 0;
+                 (x.c0 + x.c - lo) * KV_CHUNK + 4 * j;
+  a.bias_at = live && x.c0 + x.c >= lo ? at : 0;
   return a;
 }
 
@@ -687,7 +695,7 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
   float xs[2][4];
   const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
   bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
-               (x.c + 1) * KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
+               x.key0() + KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
   if (plain) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -699,7 +707,7 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
       }
     }
   } else {
-    const int key0 = x.c * KV_CHUNK + 4 * j;
+    const int key0 = x.key0() + 4 * j;
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
@@ -963,8 +971,8 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
   const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err);  // page checks, head, bias position
   LineAddr a;
   const bool live = x.nch > 0;
-  a.e0 = kv_elem(p, u.pg[0], live ? x.c * KV_CHUNK : 0, 2 * u.h) + 8 * (lane & 15);
-  const int k = live ? x.kv_len - 1 - x.c * KV_CHUNK : 0;
+  a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h) + 8 * (lane & 15);
+  const int k = live ? x.kv_len - 1 - x.key0() : 0;
   a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
   a.bias_at = u.bias_at;
   return a;
@@ -1950,16 +1958,13 @@ int occupancy_grid(int cus, int hg) {
   return cus * per_cu;
 }
 
-// RPA_WAVES_PER_CU (1..kMaxWavesPerCU, read per call) lowers the waves per CU of the grid -- a
-// tuning knob, like the reference's block-size parameters.
-int grid_for_call(const DeviceInfo& d, int mode, int hg) {
+// waves_per_cu (rpa_options_t, 1..kMaxWavesPerCU - 1) lowers the waves per CU of the grid -- a
+// per-call tuning knob, like the reference's block-size parameters.
+int grid_for_call(const DeviceInfo& d, int mode, int hg, int waves_per_cu) {
   int grid = d.grid[mode][hg];
-  if (const char* env = getenv("RPA_WAVES_PER_CU")) {
-    const int v = atoi(env);
-    if (v >= 1 && v < kMaxWavesPerCU) {
-      const int per_cu = v / hg > 0 ? v / hg : 1;
-      if (grid > d.cus * per_cu) grid = d.cus * per_cu;
-    }
+  if (waves_per_cu >= 1 && waves_per_cu < kMaxWavesPerCU) {
+    const int per_cu = waves_per_cu / hg > 0 ? waves_per_cu / hg : 1;
+    if (grid > d.cus * per_cu) grid = d.cus * per_cu;
   }
   return grid;
 }
@@ -2390,6 +2395,11 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (shape->num_tokens > 0 && (!q || !out)) return fail(RPA_E_INVALID, "NULL q or out pointer");
   if (q == out && q) return fail(RPA_E_INVALID, "out must not alias q");
   if (opt->sliding_window < 0) return fail(RPA_E_INVALID, "sliding_window must be positive");
+  if (opt->waves_per_cu < 0 || opt->waves_per_cu > kMaxWavesPerCU)
+    return fail(RPA_E_INVALID, "waves_per_cu must be in [0, 8]");
+  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 1) return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0 or 1");
+  if (!(opt->prefill_cost >= 0.f && opt->prefill_cost <= 64.f))
+    return fail(RPA_E_INVALID, "prefill_cost must be in [0, 64]");
   if (shape->num_tokens == 0 || shape->max_num_seqs == 0) return RPA_OK;
   DeviceInfo d;
   rc = device_info(d);
@@ -2420,7 +2430,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   const float mask = opt->has_mask_value ? opt->mask_value : kDefaultMask;
   p.mask_log2 = mask * kLog2e;
   p.skip_masked = mask <= -1e30f;
-  p.soft_cap = opt->soft_cap;
+  p.soft_cap = fabsf(opt->soft_cap);  // c * tanh(s / c) == |c| * tanh(s / |c|)
   p.sliding_window = opt->sliding_window;
   p.k_scale = opt->has_k_scale ? opt->k_scale : 1.f;
   p.v_scale = opt->has_v_scale ? opt->v_scale : 1.f;
@@ -2439,14 +2449,13 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (kv_scales) return fail(RPA_E_INVALID, "kv_scales is only used with fp8 kv_pages");
     if (opt->has_k_scale || opt->has_v_scale) mode = KV_BF16_SCALED;
   }
-  p.grid = grid_for_call(d, mode, p.HG);
+  p.grid = grid_for_call(d, mode, p.HG, opt->waves_per_cu);
   // prefill tiles: bf16 KV without scales, masked keys at weight 0, eight waves (kv heads) per
   // workgroup
-  if (mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG && !getenv("RPA_NO_PREFILL_TILES")) {
+  if (mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG && opt->prefill_tiles >= 0) {
     p.pf_tq = 32 * p.HG / p.G;
     p.pf_min = 16;
-    p.pf_cost = kPfCost;
-    if (const char* e = getenv("RPA_PF_COST")) p.pf_cost = (float)atof(e);
+    p.pf_cost = opt->prefill_cost > 0.f ? opt->prefill_cost : kPfCost;
   }
   hipStream_t st = (hipStream_t)stream;
   if (ev_begin && hipEventRecord((hipEvent_t)ev_begin, st) != hipSuccess)

@@ -10,7 +10,14 @@
 //     fully masked chunks are never loaded -- exact when the mask value makes
 //     masked weights vanish in fp32 (skip_masked); with a finite mask value
 //     the reference gives masked keys weight exp(s + mask - m), so every key
-//     below kv_len is visited instead.
+//     below kv_len is visited instead;
+//   * with a sliding window w (and masked weights that vanish), a row block also
+//     starts at the first chunk that holds a key inside the window of its FIRST
+//     row (rb_first_chunk): keys at or below pos_first - w are masked for every
+//     row of the block (ragged_paged_attention.py:532-534), so their chunks are
+//     never loaded either (the reference starts each sequence's KV walk at
+//     max(kv_q_gap - window, 0) // bkv, src/tpu_cake/rpa_owned_kernel.py:185-193,
+//     :705-712, :748-749).
 // Units are ordered sequence-major, then kv head, then row block, then chunk.
 // Workgroup b of a grid of `grid` owns units [start(b), start(b+1)): with q = W / grid and
 // r = W % grid, the first r workgroups own q + 1 units and the rest q, so every workgroup gets
@@ -45,9 +52,22 @@ RPA_HD int rb_visible_keys(int kv_len, int q_len, int group, int rb, bool skip_m
   return vis < kv_len ? vis : kv_len;
 }
 
-RPA_HD int rb_units(int kv_len, int q_len, int group, int rb, bool skip_masked) {
+// First chunk visited by row block rb: 0 without a window (or when masked keys keep a nonzero
+// weight), else the chunk of key pos_first - window + 1, the lowest key any row of the block sees.
+RPA_HD int rb_first_chunk(int kv_len, int q_len, int group, int rb, bool skip_masked, int window) {
+  if (!skip_masked || window <= 0) return 0;
+  const int first_tok = rb * ROW_BLOCK / group;
+  const long long lo = (long long)kv_len - q_len + first_tok - window + 1;
+  return lo > 0 ? (int)(lo / KV_CHUNK) : 0;
+}
+
+// Units (chunks) of row block rb: from rb_first_chunk to the chunk of its last visible key.
+RPA_HD int rb_units(int kv_len, int q_len, int group, int rb, bool skip_masked, int window) {
   int vis = rb_visible_keys(kv_len, q_len, group, rb, skip_masked);
-  return vis > 0 ? (vis + KV_CHUNK - 1) / KV_CHUNK : 0;
+  if (vis <= 0) return 0;
+  const int hi = (vis + KV_CHUNK - 1) / KV_CHUNK;
+  const int lo = rb_first_chunk(kv_len, q_len, group, rb, skip_masked, window);
+  return hi > lo ? hi - lo : 0;
 }
 
 RPA_HD int num_row_blocks(int q_len, int group) {
@@ -55,11 +75,11 @@ RPA_HD int num_row_blocks(int q_len, int group) {
 }
 
 // Units of one kv head of a sequence (sum over its row blocks).
-RPA_HD int seq_units_per_head(int kv_len, int q_len, int group, bool skip_masked) {
+RPA_HD int seq_units_per_head(int kv_len, int q_len, int group, bool skip_masked, int window) {
   if (q_len <= 0 || kv_len <= 0) return 0;
   int nrb = num_row_blocks(q_len, group);
   int u = 0;
-  for (int rb = 0; rb < nrb; ++rb) u += rb_units(kv_len, q_len, group, rb, skip_masked);
+  for (int rb = 0; rb < nrb; ++rb) u += rb_units(kv_len, q_len, group, rb, skip_masked, window);
   return u;
 }
 

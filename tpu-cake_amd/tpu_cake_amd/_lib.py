@@ -13,7 +13,7 @@ import pathlib
 import threading
 
 LIB_PATH = pathlib.Path(__file__).with_name("librpa.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 RPA_OK = 0
 RPA_KV_BF16 = 0
@@ -61,6 +61,10 @@ class RpaOptions(ctypes.Structure):
         ("k_scale", ctypes.c_float),
         ("has_v_scale", ctypes.c_int32),
         ("v_scale", ctypes.c_float),
+        # tuning knobs (ABI 2; 0 = library default)
+        ("waves_per_cu", ctypes.c_int32),
+        ("prefill_tiles", ctypes.c_int32),
+        ("prefill_cost", ctypes.c_float),
     ]
 
 

@@ -141,9 +141,12 @@ def assess_profile(profile: dict, *, dispatches: int, counters: tuple = ()) -> d
 
 
 # --------------------------------------------------------------------------- phases
-def _steps(config: str, steps: int, warmup: int, events: bool, seed: int | None = None) -> dict:
+def _steps(config: str, steps: int, warmup: int, events: bool, seed: int | None = None,
+           knobs: dict | None = None) -> dict:
     """Run ``steps`` timed calls of a benchmark configuration (inputs resident, pools rotated);
-    with ``events``, time the attention kernel and each whole call with HIP events."""
+    with ``events``, time the attention kernel and each whole call with HIP events.  ``knobs``:
+    explicit schedule knobs (``waves_per_cu``, ``prefill_tiles``, ``prefill_cost``) for every
+    call, else the tuned table's."""
     import torch
 
     from . import ops
@@ -157,7 +160,7 @@ def _steps(config: str, steps: int, warmup: int, events: bool, seed: int | None 
     copies = max(2, math.ceil(2e9 / (pool.numel() * pool.element_size())))
     pools = [pool] + [pool.clone() for _ in range(copies - 1)]
     out = torch.empty_like(d["q"])
-    kw = dict(sm_scale=case.sm_scale, out=out)
+    kw = dict(sm_scale=case.sm_scale, out=out, **(knobs or {}))
     if "kv_scales" in d:
         kw["kv_scales"] = d["kv_scales"]
     kev = [(KernelEvent(), KernelEvent()) for _ in range(steps)] if events else None
@@ -178,7 +181,7 @@ def _steps(config: str, steps: int, warmup: int, events: bool, seed: int | None 
     for i in range(steps):
         call(i, True)
     torch.cuda.synchronize()
-    res = {"config": config, "steps": steps, "warmup": warmup}
+    res = {"config": config, "steps": steps, "warmup": warmup, "seed": seed, "knobs": knobs or {}}
     if events:
         res["attention_ns"] = [round(a.elapsed_time(b) * 1e6) for a, b in kev]
         res["call_ns"] = [round(a.elapsed_time(b) * 1e6) for a, b in cev]

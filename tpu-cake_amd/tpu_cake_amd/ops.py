@@ -19,7 +19,7 @@ import math
 
 import torch
 
-from . import _lib
+from . import _lib, tuned
 
 DEFAULT_MASK_VALUE = -0.7 * float(torch.finfo(torch.float32).max)  # ragged_paged_attention.py:32
 
@@ -27,6 +27,7 @@ _KV_DTYPES = {torch.bfloat16: _lib.RPA_KV_BF16, torch.float8_e4m3fn: _lib.RPA_KV
               torch.uint8: _lib.RPA_KV_FP8_E4M3}
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_ws_need: dict[int, int] = {}  # device index -> workspace bytes (depends only on the device)
 
 
 def _require_cuda(name: str, t: torch.Tensor) -> None:
@@ -122,18 +123,76 @@ def make_shape(q, kv_pages, page_indices) -> _lib.RpaShape:
 
 
 def workspace_for(shape: _lib.RpaShape, device: torch.device, stream: int) -> torch.Tensor:
-    """Cached per-(device, stream) workspace; calls that share one must not overlap."""
+    """Cached per-(device, stream) workspace; calls that share one must not overlap.  Its size
+    depends only on the device (the persistent grid), so it is asked for once per device."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get((index, stream))
+    if ws is not None and ws.numel() >= _ws_need[index]:
+        return ws
     lib = _lib.load()
     need = lib.rpa_workspace_size(ctypes.byref(shape))
     if need == 0:
         _lib.check(-1)
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
-    ws = _workspaces.get(key)
+    _ws_need[index] = need
     if ws is None or ws.numel() < need:
         ws = torch.empty(need, dtype=torch.uint8, device=device)
         _lib.check(lib.rpa_workspace_init(ws.data_ptr(), ws.numel(), stream))
-        _workspaces[key] = ws
+        _workspaces[(index, stream)] = ws
     return ws
+
+
+def _static_plan(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_scales, knobs: dict) -> tuple:
+    """Validate everything that depends only on shapes, dtypes, devices and the scalar knobs (the
+    reference's static checks, :216-287, plus this build's), and build the ctypes structs.
+    Returns (shape, options)."""
+    static_validate_inputs(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, **{
+        k: knobs[k] for k in ("sm_scale", "sliding_window", "soft_cap", "mask_value", "k_scale", "v_scale",
+                              "num_kv_pages_per_block", "num_queries_per_block", "vmem_limit_bytes")})
+    for name, t in (("q", q), ("kv_pages", kv_pages), ("kv_lens", kv_lens), ("page_indices", page_indices),
+                    ("cu_q_lens", cu_q_lens), ("num_seqs", num_seqs)):
+        _require_cuda(name, t)
+        if t.device != q.device:
+            raise ValueError(f"{name} is on {t.device}, q on {q.device}")
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"q dtype {q.dtype} must be bfloat16")
+    if num_seqs.dtype != torch.int32:
+        raise ValueError(f"num_seqs dtype {num_seqs.dtype} must be int32")
+    shape = make_shape(q, kv_pages, page_indices)
+    if kv_scales is not None:
+        if shape.kv_dtype != _lib.RPA_KV_FP8_E4M3:
+            raise ValueError("kv_scales requires fp8 kv_pages")
+        _require_cuda("kv_scales", kv_scales)
+        if kv_scales.dtype != torch.float32 or tuple(kv_scales.shape) != (shape.total_pages, shape.num_kv_heads, 2):
+            raise ValueError(f"kv_scales must be float32 [{shape.total_pages}, {shape.num_kv_heads}, 2]")
+        if knobs["k_scale"] is not None or knobs["v_scale"] is not None:
+            raise ValueError("pass either per-page kv_scales or scalar k_scale/v_scale, not both")
+    # tuning knobs: the caller's, else the tuned table's entry for this shape, else the defaults
+    tuned_knobs = tuned.get_tuned_knobs("fp8" if shape.kv_dtype == _lib.RPA_KV_FP8_E4M3 else "bf16",
+                                        shape.num_q_heads // shape.num_kv_heads, shape.page_size, shape.num_tokens)
+    wpc = knobs["waves_per_cu"] if knobs["waves_per_cu"] is not None else tuned_knobs["waves_per_cu"]
+    tiles = knobs["prefill_tiles"] if knobs["prefill_tiles"] is not None else tuned_knobs["prefill_tiles"]
+    cost = knobs["prefill_cost"] if knobs["prefill_cost"] is not None else tuned_knobs["prefill_cost"]
+    if not (isinstance(wpc, int) and 0 <= wpc <= 8):
+        raise ValueError(f"waves_per_cu={wpc!r} must be an int in [0, 8]")
+    if not (0.0 <= float(cost) <= 64.0):
+        raise ValueError(f"prefill_cost={cost!r} must be in [0, 64]")
+    mask_value = knobs["mask_value"]
+    if mask_value is None:
+        mask_value = DEFAULT_MASK_VALUE
+    k_scale, v_scale = knobs["k_scale"], knobs["v_scale"]
+    opts = _lib.RpaOptions(
+        float(knobs["sm_scale"]), int(knobs["sliding_window"] or 0), float(knobs["soft_cap"] or 0.0),
+        1, float(mask_value),
+        int(k_scale is not None), float(k_scale if k_scale is not None else 1.0),
+        int(v_scale is not None), float(v_scale if v_scale is not None else 1.0),
+        int(wpc), 1 if tiles else -1, float(cost),
+    )
+    return shape, opts
+
+
+# Validated (shape, options) per call signature: shapes, dtypes, devices and knobs.  A serving loop
+# calls with the same signature every step, so the checks and struct building above run once.
+_plans: dict[tuple, tuple] = {}
 
 
 def ragged_paged_attention(
@@ -157,62 +216,73 @@ def ragged_paged_attention(
     out: torch.Tensor | None = None,
     kernel_events: tuple | None = None,      # (begin, end) events around the attention kernel: torch.cuda.Event
                                              # or timing.KernelEvent (anything with a .cuda_event handle)
+    waves_per_cu: int | None = None,         # tuning knobs (rpa_options_t); None = the tuned table's entry
+    prefill_tiles: bool | None = None,
+    prefill_cost: float | None = None,
 ) -> torch.Tensor:
     """Ragged paged attention (mixed prefill and decode) on MI355X.
 
     Semantics of ``ref_ragged_paged_attention`` (ragged_paged_attention.py:73-148).
     Returns a new ``[T, Hq, D]`` bf16 tensor (or fills ``out``); rows at or past
-    ``cu_q_lens[num_seqs]`` are zero.
+    ``cu_q_lens[num_seqs]`` are zero.  The Pallas block sizes are validated like upstream
+    and have no effect; the schedule knobs ``waves_per_cu`` / ``prefill_tiles`` /
+    ``prefill_cost`` take their place (``tpu_cake_amd.tuned`` holds per-shape values).
     """
-    static_validate_inputs(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, sm_scale=sm_scale,
-                           sliding_window=sliding_window, soft_cap=soft_cap, mask_value=mask_value,
-                           k_scale=k_scale, v_scale=v_scale, num_kv_pages_per_block=num_kv_pages_per_block,
-                           num_queries_per_block=num_queries_per_block, vmem_limit_bytes=vmem_limit_bytes)
-    for name, t in (("q", q), ("kv_pages", kv_pages), ("kv_lens", kv_lens), ("page_indices", page_indices),
-                    ("cu_q_lens", cu_q_lens), ("num_seqs", num_seqs)):
-        _require_cuda(name, t)
-    if q.dtype != torch.bfloat16:
-        raise ValueError(f"q dtype {q.dtype} must be bfloat16")
-    if num_seqs.dtype != torch.int32:
-        raise ValueError(f"num_seqs dtype {num_seqs.dtype} must be int32")
-    shape = make_shape(q, kv_pages, page_indices)
-    if kv_scales is not None:
-        if shape.kv_dtype != _lib.RPA_KV_FP8_E4M3:
-            raise ValueError("kv_scales requires fp8 kv_pages")
-        _require_cuda("kv_scales", kv_scales)
-        if kv_scales.dtype != torch.float32 or tuple(kv_scales.shape) != (shape.total_pages, shape.num_kv_heads, 2):
-            raise ValueError(f"kv_scales must be float32 [{shape.total_pages}, {shape.num_kv_heads}, 2]")
-        if k_scale is not None or v_scale is not None:
-            raise ValueError("pass either per-page kv_scales or scalar k_scale/v_scale, not both")
+    sig = (q.shape, q.dtype, q.device, kv_pages.shape, kv_pages.dtype, kv_pages.device, kv_lens.shape, kv_lens.dtype,
+           page_indices.shape, page_indices.dtype, cu_q_lens.shape, cu_q_lens.dtype, num_seqs.shape, num_seqs.dtype,
+           None if kv_scales is None else (kv_scales.shape, kv_scales.dtype, kv_scales.device),
+           sm_scale, sliding_window, soft_cap, mask_value, k_scale, v_scale, num_kv_pages_per_block,
+           num_queries_per_block, vmem_limit_bytes, waves_per_cu, prefill_tiles, prefill_cost)
+    plan = _plans.get(sig)
+    if plan is None:
+        plan = _static_plan(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_scales, dict(
+            sm_scale=sm_scale, sliding_window=sliding_window, soft_cap=soft_cap, mask_value=mask_value,
+            k_scale=k_scale, v_scale=v_scale, num_kv_pages_per_block=num_kv_pages_per_block,
+            num_queries_per_block=num_queries_per_block, vmem_limit_bytes=vmem_limit_bytes,
+            waves_per_cu=waves_per_cu, prefill_tiles=prefill_tiles, prefill_cost=prefill_cost))
+        if len(_plans) > 256:
+            _plans.clear()
+        _plans[sig] = plan
+    shape, opts = plan
+    # per call: what the signature does not fix
+    if not (q.is_contiguous() and kv_pages.is_contiguous() and kv_lens.is_contiguous()
+            and page_indices.is_contiguous() and cu_q_lens.is_contiguous() and num_seqs.is_contiguous()
+            and (kv_scales is None or kv_scales.is_contiguous())):
+        for name, t in (("q", q), ("kv_pages", kv_pages), ("kv_lens", kv_lens), ("page_indices", page_indices),
+                        ("cu_q_lens", cu_q_lens), ("num_seqs", num_seqs), ("kv_scales", kv_scales)):
+            if t is not None:
+                _require_cuda(name, t)
     if out is None:
         out = torch.empty_like(q)
+    elif (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or not out.is_contiguous()
+          or out.data_ptr() == q.data_ptr()):
+        raise ValueError("out must be a separate contiguous tensor shaped like q on q's device")
+    device = q.device
+    if device.index != torch.cuda.current_device():
+        with torch.cuda.device(device):
+            return ragged_paged_attention(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, sm_scale=sm_scale,
+                                          sliding_window=sliding_window, soft_cap=soft_cap, mask_value=mask_value,
+                                          k_scale=k_scale, v_scale=v_scale,
+                                          num_kv_pages_per_block=num_kv_pages_per_block,
+                                          num_queries_per_block=num_queries_per_block,
+                                          vmem_limit_bytes=vmem_limit_bytes, kv_scales=kv_scales, out=out,
+                                          kernel_events=kernel_events, waves_per_cu=waves_per_cu,
+                                          prefill_tiles=prefill_tiles, prefill_cost=prefill_cost)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    ws = workspace_for(shape, device, stream)
+    lib = _lib.load()
+    args = (shape, opts, q.data_ptr(), kv_pages.data_ptr(),
+            kv_scales.data_ptr() if kv_scales is not None else None,
+            kv_lens.data_ptr(), page_indices.data_ptr(), cu_q_lens.data_ptr(), num_seqs.data_ptr(),
+            out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    if kernel_events is None:
+        rc = lib.rpa_ragged_paged_attention(*args)
     else:
-        _require_cuda("out", out)
-        if out.shape != q.shape or out.dtype != q.dtype or out.data_ptr() == q.data_ptr():
-            raise ValueError("out must be a separate tensor shaped like q")
-    if mask_value is None:
-        mask_value = DEFAULT_MASK_VALUE
-    opts = _lib.RpaOptions(
-        float(sm_scale), int(sliding_window or 0), float(soft_cap or 0.0),
-        1, float(mask_value),
-        int(k_scale is not None), float(k_scale if k_scale is not None else 1.0),
-        int(v_scale is not None), float(v_scale if v_scale is not None else 1.0),
-    )
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        ws = workspace_for(shape, q.device, stream)
-        lib = _lib.load()
-        args = (ctypes.byref(shape), ctypes.byref(opts), q.data_ptr(), kv_pages.data_ptr(),
-                kv_scales.data_ptr() if kv_scales is not None else None,
-                kv_lens.data_ptr(), page_indices.data_ptr(), cu_q_lens.data_ptr(), num_seqs.data_ptr(),
-                out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
-        if kernel_events is None:
-            rc = lib.rpa_ragged_paged_attention(*args)
-        else:
-            begin, end = kernel_events
-            if not begin.cuda_event or not end.cuda_event:
-                raise ValueError("kernel_events must be recorded once before use (HIP events are created lazily)")
-            rc = lib.rpa_ragged_paged_attention_timed(*args, begin.cuda_event, end.cuda_event)
+        begin, end = kernel_events
+        if not begin.cuda_event or not end.cuda_event:
+            raise ValueError("kernel_events must be recorded once before use (HIP events are created lazily)")
+        rc = lib.rpa_ragged_paged_attention_timed(*args, begin.cuda_event, end.cuda_event)
+    if rc:
         _lib.check(rc)
     return out
 
