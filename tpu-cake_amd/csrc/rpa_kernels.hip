@@ -2344,10 +2344,71 @@ V1Layout v1_layout(const DeviceInfo& d, const rpa_inkling_shape_t* f) {
   return l;
 }
 
+// ---------------------------------------------------------------------------------------------
+// allocation-free entry (rpa_ragged_paged_attention_noalloc): the operator's workspace lives in a
+// file-scope device array, one copy per GPU, found with hipGetSymbolAddress once per device
+// ---------------------------------------------------------------------------------------------
+// Bytes of the array: the workspace of a device with up to 352 CUs (about 140 KiB per CU: split
+// descriptors, heavy-merge flags and split-K partials for a persistent grid of 8 waves per CU).
+constexpr size_t kScratchBytes = 48ull << 20;
+
+__global__ __launch_bounds__(256) void rpa_scratch_clear_kernel(u32x4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+struct ScratchState {
+  void* ptr = nullptr;   // the device address of `scratch` on this device (never its host name)
+  bool cleared = false;  // its header, descriptors and flags zeroed (every call leaves them so)
+};
+std::mutex g_scratch_mu;
+ScratchState g_scratch[64];
+
 }  // namespace
 }  // namespace rpa
 
+// The allocation-free entry point's workspace.  Host code never passes this name to a kernel or a
+// copy: it is a host-side stand-in; the device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[rpa::kScratchBytes];
+
 using namespace rpa;
+
+namespace rpa {
+namespace {
+// This device's scratch address; on first use on a device, its zero-initialised region (header,
+// descriptors, heavy-merge flags) is cleared with a fill kernel on `stream` (a kernel, not a
+// memset node, so the call stays capturable).
+int scratch_for_device(const WsLayout& w, hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(RPA_E_HIP, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchState& s = g_scratch[dev];
+  if (!s.ptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(RPA_E_HIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    s.ptr = ptr;
+  }
+  if (!s.cleared) {
+    // the clear must run before any call uses the array, so it cannot be left to a captured graph
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess)
+      return fail(RPA_E_HIP, "hipStreamIsCapturing failed");
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(RPA_E_INVALID, "the first allocation-free call on a device must run outside graph capture "
+                                 "(it clears the device's scratch)");
+    const size_t n16 = w.ml / 16;  // header .. heavy descriptors: a multiple of 256 bytes
+    hipLaunchKernelGGL(rpa_scratch_clear_kernel, dim3(64), dim3(256), 0, stream, (u32x4*)s.ptr, n16);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(RPA_E_HIP, std::string("scratch clear launch failed: ") + hipGetErrorString(e));
+    s.cleared = true;
+  }
+  *out = s.ptr;
+  return RPA_OK;
+}
+}  // namespace
+}  // namespace rpa
 
 extern "C" {
 
@@ -2503,6 +2564,28 @@ int rpa_ragged_paged_attention_timed(const rpa_shape_t* shape, const rpa_options
                                      void* stream, void* event_begin, void* event_end) {
   return launch_rpa(shape, opt, q, kv_pages, kv_scales, kv_lens, page_indices, cu_q_lens, num_seqs, out, workspace,
                     workspace_bytes, stream, event_begin, event_end);
+}
+
+int rpa_ragged_paged_attention_noalloc(const rpa_shape_t* shape, const rpa_options_t* opt, const void* q,
+                                       const void* kv_pages, const float* kv_scales, const int32_t* kv_lens,
+                                       const int32_t* page_indices, const int32_t* cu_q_lens,
+                                       const int32_t* num_seqs, void* out, void* stream) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  if (!opt) return fail(RPA_E_INVALID, "options is NULL");
+  DeviceInfo d;
+  rc = device_info(d);
+  if (rc) return rc;
+  const WsLayout w = ws_layout(d);
+  if (w.total > kScratchBytes)
+    return fail(RPA_E_WORKSPACE, "this device needs " + std::to_string(w.total) +
+                                     " bytes of workspace; the allocation-free entry's scratch holds " +
+                                     std::to_string(kScratchBytes) + " (use rpa_ragged_paged_attention)");
+  void* ws = nullptr;
+  rc = scratch_for_device(w, (hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return launch_rpa(shape, opt, q, kv_pages, kv_scales, kv_lens, page_indices, cu_q_lens, num_seqs, out, ws,
+                    kScratchBytes, stream, nullptr, nullptr);
 }
 
 int rpa_gather_kv(const rpa_shape_t* shape, const void* kv_pages, const int32_t* kv_lens,

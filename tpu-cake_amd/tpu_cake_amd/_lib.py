@@ -27,6 +27,7 @@ EXPORTED_SYMBOLS = (
     "rpa_workspace_init",
     "rpa_ragged_paged_attention",
     "rpa_ragged_paged_attention_timed",
+    "rpa_ragged_paged_attention_noalloc",
     "rpa_gather_kv",
     "rpa_read_error_word",
     "rpa_fused_workspace_size",
@@ -145,6 +146,10 @@ def load() -> ctypes.CDLL:
         lib.rpa_ragged_paged_attention_timed.restype = ctypes.c_int
         lib.rpa_ragged_paged_attention_timed.argtypes = [
             ctypes.POINTER(RpaShape), ctypes.POINTER(RpaOptions), vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp, vp, vp,
+        ]
+        lib.rpa_ragged_paged_attention_noalloc.restype = ctypes.c_int
+        lib.rpa_ragged_paged_attention_noalloc.argtypes = [
+            ctypes.POINTER(RpaShape), ctypes.POINTER(RpaOptions), vp, vp, vp, vp, vp, vp, vp, vp, vp,
         ]
         lib.rpa_gather_kv.restype = ctypes.c_int
         lib.rpa_gather_kv.argtypes = [ctypes.POINTER(RpaShape), vp, vp, vp, vp, vp, ctypes.c_int64, vp, sz, vp]
