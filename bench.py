@@ -13,7 +13,8 @@ roofline   = (KV + Q + O bytes) / average duration of the attention kernel,
              timed step (timing-only events: no system-scope fence), against
              MI355X's 8 TB/s HBM peak (or the bf16 MFMA peak for prefill rows)
 cpu_baseline = the numpy oracle (oracle/rpa_oracle.py) on a bounded sample of
-             the same configuration, 1 thread, on this host.
+             the same configuration, on every core of this process's affinity set (BLAS
+             threads matched), median of 3 runs.
 """
 
 from __future__ import annotations
@@ -29,53 +30,100 @@ import time
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path[:0] = [str(ROOT), str(ROOT / "tpu-cake_amd")]
 
-HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, AMD published
-BF16_PEAK_TFLOPS = 2500.0       # MI355X dense bf16 MFMA, AMD published
 METRIC = "RPA decode KV-read GB/s (% of HBM peak) + tokens/s, 64-seq bf16 GQA, 1 GPU"
+# configurations beyond BASELINE's five: C2 with the 512-key sliding window of Inkling's largest
+# decode family (RPAd-...-sw_512), whose algorithmic bytes are the windows' keys only
+# (tpu_cake_amd.workloads.WINDOWED_CONFIGS)
+
+
+def _rates():
+    from tpu_cake_amd.cost_model import mi355x_rates
+
+    return mi355x_rates()
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(case, budget_s: float = 20.0) -> dict:
-    """Time the oracle on the first sequences of the workload (about budget_s of work)."""
+def _cores() -> int:
+    """Threads for the CPU baseline: the cores of this process's affinity set, capped by
+    OMP_NUM_THREADS when the host sets a smaller CPU share that way."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(omp)) if omp.isdigit() and int(omp) > 0 else n
+
+
+def cpu_baseline(case, budget_s: float = 18.0, runs: int = 3, sliding_window=None) -> dict:
+    """The oracle (oracle/rpa_oracle.py, a numpy restatement of ref_ragged_paged_attention) timed on
+    this host: every core of the affinity set, BLAS threads set to match, on the first sequences of
+    the same workload sized to about budget_s over ``runs`` runs; the median run is reported."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import rpa_oracle as orc
 
     n = int(case.num_seqs[0])
-    lens = case.kv_lens[:n].astype(np.int64)
-    with threadpool_limits(limits=1):
-        # probe speed on one sequence, then size the sample
+    cores = _cores()
+    kw = dict(sm_scale=case.sm_scale, kv_scales=case.kv_scales, kv_dtype=case.kv_dtype, sliding_window=sliding_window)
+
+    def run(k):
         t0 = time.perf_counter()
         orc.ref_ragged_paged_attention(case.q, case.kv_pages, case.kv_lens, case.page_indices, case.cu_q_lens,
-                                       np.array([1], np.int32), sm_scale=case.sm_scale,
-                                       kv_scales=case.kv_scales, kv_dtype=case.kv_dtype)
-        probe = max(time.perf_counter() - t0, 1e-3)
-        per_tok = probe / max(int(lens[0]), 1)
-        k = 1
-        while k < n and per_tok * int(lens[: k + 1].sum()) < budget_s:
-            k += 1
-        t0 = time.perf_counter()
-        orc.ref_ragged_paged_attention(case.q, case.kv_pages, case.kv_lens, case.page_indices, case.cu_q_lens,
-                                       np.array([k], np.int32), sm_scale=case.sm_scale,
-                                       kv_scales=case.kv_scales, kv_dtype=case.kv_dtype)
-        dt = time.perf_counter() - t0
-    toks = int(lens[:k].sum())
-    elem = 1 if case.kv_dtype == "fp8" else 2
-    kv_bytes = toks * case.num_kv_heads * 2 * case.head_dim * elem
+                                       np.array([k], np.int32), **kw)
+        return time.perf_counter() - t0
+
+    with threadpool_limits(limits=cores):
+        per_seq = run(1)  # also warms the BLAS pool
+        # size the sample: grow k while the estimate stays within one run's share of the budget
+        k, t_k = 1, per_seq
+        while k < n and t_k < budget_s / runs / 2:
+            k = min(n, 2 * k)
+            t_k = run(k)
+        times = sorted(run(k) for _ in range(runs))
+    dt = times[len(times) // 2]
+    from tpu_cake_amd.cost_model import rpa_work
+
+    w = case.work(sliding_window)
+    part = rpa_work(case.kv_lens[:k], np.diff(case.cu_q_lens[: k + 1]), num_q_heads=case.num_q_heads,
+                    num_kv_heads=case.num_kv_heads, head_dim=case.head_dim, page_size=case.page_size,
+                    kv_dtype=case.kv_dtype, sliding_window=sliding_window)
+    kv_bytes = part.kv_read_bytes + part.scale_bytes
     q_toks = int(case.cu_q_lens[k] - case.cu_q_lens[0])
     return {
         "value": round(kv_bytes / dt / 1e9, 4),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": cores,
         "kind": "port",
         "tokens_per_s": round(q_toks / dt, 2),
         "seconds": round(dt, 3),
-        "sample": f"first {k} of {n} sequences ({toks} KV tokens, {q_toks} query tokens) of the same workload",
+        "runs_s": [round(t, 3) for t in times],
+        "blas_threads": cores,
+        "affinity_cores": len(os.sched_getaffinity(0)),
+        "sample": (f"first {k} of {n} sequences ({part.keys_read} KV tokens read, {q_toks} query tokens; "
+                   f"{kv_bytes / max(w.kv_read_bytes + w.scale_bytes, 1):.1%} of the step's KV bytes), "
+                   f"median of {runs} runs on {cores} cores"),
     }
+
+
+def copy_probe_gbps(dev, nbytes: int = 1 << 30, reps: int = 5) -> float:
+    """Achieved bandwidth of torch's device-to-device copy (bytes read + written / time) on this box,
+    reported beside the 8 TB/s published peak (a copy kernel, not a bound on a read stream)."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    sec = a.elapsed_time(b) / 1e3 / reps
+    del src, dst
+    return 2 * nbytes / sec / 1e9
 
 
 def kernel_source_digest() -> str:
@@ -100,8 +148,9 @@ def measured_traffic(cfg: str):
     return data["configs"][cfg]["traffic_bytes"]
 
 
-def fused_cpu_baseline(case, budget_s: float = 20.0) -> dict:
-    """The fused-decode oracle (oracle/rpa_fused_oracle.py) on the first sequences of the step."""
+def fused_cpu_baseline(case, budget_s: float = 18.0, runs: int = 3) -> dict:
+    """The fused-decode oracle (oracle/rpa_fused_oracle.py) on the first sequences of the step, on
+    every core of the affinity set (BLAS threads matched), median of ``runs`` runs."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -110,6 +159,7 @@ def fused_cpu_baseline(case, budget_s: float = 20.0) -> dict:
     a = case.arrays
     n = len(a["kv_lengths"])
     S = a["cache"].shape[1]
+    cores = _cores()
 
     def subset(k):
         pages = int(a["cu_kv_lens"][k]) // S
@@ -123,21 +173,26 @@ def fused_cpu_baseline(case, budget_s: float = 20.0) -> dict:
         sub["cache"] = a["cache"].reshape(a["cache"].shape[0], S, -1, 2, a["cache"].shape[-1])
         return sub
 
-    with threadpool_limits(limits=1):
+    def run(k):
+        sub = subset(k)
         t0 = time.perf_counter()
-        fo.inkling_fused_rpa_reference(subset(1))
-        per_seq = max(time.perf_counter() - t0, 1e-3) / max(int(a["kv_lengths"][0]), 1)
-        k = 1
-        while k < n and per_seq * int(a["kv_lengths"][: k + 1].sum()) < budget_s:
-            k += 1
-        t0 = time.perf_counter()
-        fo.inkling_fused_rpa_reference(subset(k))
-        dt = time.perf_counter() - t0
+        fo.inkling_fused_rpa_reference(sub)
+        return time.perf_counter() - t0
+
+    with threadpool_limits(limits=cores):
+        k, t_k = 1, run(1)
+        while k < n and t_k < budget_s / runs / 2:
+            k = min(n, 2 * k)
+            t_k = run(k)
+        times = sorted(run(k) for _ in range(runs))
+    dt = times[len(times) // 2]
     toks = int(a["kv_lengths"][:k].sum())
     kv_bytes = toks * a["keys"].shape[1] * 2 * 128 * 2
-    return {"value": round(kv_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "tokens_per_s": round(k / dt, 2), "seconds": round(dt, 3),
-            "sample": f"first {k} of {n} sequences ({toks} KV tokens, {k} decode steps) of the same step"}
+    return {"value": round(kv_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "tokens_per_s": round(k / dt, 2), "seconds": round(dt, 3), "runs_s": [round(t, 3) for t in times],
+            "blas_threads": cores,
+            "sample": f"first {k} of {n} sequences ({toks} KV tokens, {k} decode steps) of the same step, "
+                      f"median of {runs} runs on {cores} cores"}
 
 
 def fused_bench(args, dev) -> int:
@@ -186,6 +241,7 @@ def fused_bench(args, dev) -> int:
     nseq, hq = a["queries"].shape[:2]
     kv_bytes = case.kv_read_bytes()
     moved = kv_bytes + 2 * nseq * hq * 128 * 2 + 2 * a["keys"].size * 2 * 2
+    peak = _rates().hbm_bytes_per_second / 1e9
     value = kv_bytes / (ms_step * 1e-3) / 1e9
     achieved = moved / (ms_step * 1e-3) / 1e9
     result = {
@@ -197,10 +253,10 @@ def fused_bench(args, dev) -> int:
                    "sum_kv_len": int(a["kv_lengths"].sum()), "kv_bytes_per_step": kv_bytes,
                    "cache_copies_rotated": copies},
         "tokens_per_s": round(nseq / (ms_step * 1e-3), 1),
-        "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
+        "hbm_fraction": round(value / peak, 4),
         "wall_s_timed_region": round(wall, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": measured_traffic("inkling"),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": peak, "unit": "GB/s",
+                     "frac": round(achieved / peak, 4), "traffic": measured_traffic("inkling"),
                      "basis": "whole step (cache write, metadata and bias-table kernels, attention, combine)"},
     }
     if not args.no_cpu_baseline:
@@ -215,9 +271,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "inkling"],
-                    help="c1..c5: the RPA operator configurations; inkling: the fused decode step "
-                         "(KV-cache write + relative-bias attention)")
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2w", "inkling"],
+                    help="c1..c5: the RPA operator configurations; c2w: C2 with a 512-key sliding window; "
+                         "inkling: the fused decode step (KV-cache write + relative-bias attention)")
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--rotate-bytes", type=float, default=2.0e9,
                     help="KV pool copies rotated so that at least this many bytes separate reuses")
@@ -247,19 +303,18 @@ def main() -> int:
 
     if args.copy_probe:
         n = int(args.copy_probe) // 16 * 16
-        src = torch.empty(n // 4, dtype=torch.int32, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": n, "copies": 5}))
+        gbps = copy_probe_gbps(dev, n)
+        print(json.dumps({"copy_probe_bytes": n, "copies": 6, "achieved_gbps": round(gbps, 1)}))
         return 0
 
     if args.config == "inkling":
         return fused_bench(args, dev)
 
+    from tpu_cake_amd.workloads import WINDOWED_CONFIGS
+
+    base_cfg, window = WINDOWED_CONFIGS.get(args.config, (args.config, None))
     t0 = time.perf_counter()
-    case = make_config(args.config, seed=args.seed)
+    case = make_config(base_cfg, seed=args.seed)
     log(f"built {args.config} in {time.perf_counter() - t0:.1f}s")
     d = ops.case_to_device(case, dev)
     kv_scales = d.pop("kv_scales", None)
@@ -271,14 +326,17 @@ def main() -> int:
 
     n = int(case.num_seqs[0])
     T = int(case.cu_q_lens[n])
-    kv_bytes = case.kv_read_bytes()
-    qo_bytes = 2 * T * case.num_q_heads * case.head_dim * 2
-    flops = case.prefill_flops()
+    work = case.work(window)  # the work convention (tpu_cake_amd.cost_model.rpa_work)
+    kv_bytes = work.kv_read_bytes + work.scale_bytes
+    qo_bytes = work.q_bytes + work.o_bytes
+    flops = work.prefill_flops
+    rates = _rates()
+    peak = rates.hbm_bytes_per_second / 1e9
 
     def call(i, ev=None):
         ops.ragged_paged_attention(d["q"], pools[i % copies], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
                                    d["num_seqs"], sm_scale=case.sm_scale, kv_scales=kv_scales, out=out,
-                                   kernel_events=ev)
+                                   kernel_events=ev, sliding_window=window)
 
     for i in range(args.warmup):
         call(i)
@@ -298,11 +356,12 @@ def main() -> int:
     kern_ms = [a.elapsed_time(b) for a, b in evs]
     kern_avg = float(np.mean(kern_ms))
     kern_med = float(np.median(kern_ms))
+    del pools
+    ceiling = copy_probe_gbps(dev)
 
     value = kv_bytes / (ms_step * 1e-3) / 1e9
     achieved_bw = (kv_bytes + qo_bytes) / (kern_avg * 1e-3) / 1e9
-    if flops and args.config == "c3":
-        roof_flops = flops / (kern_avg * 1e-3) / 1e12
+    desc = CONFIG_DESCRIPTIONS[base_cfg] + (f"; sliding_window {window}" if window else "")
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -317,7 +376,7 @@ def main() -> int:
         "dtype": "fp8" if case.kv_dtype == "fp8" else "bf16",
         "data": "synthetic: seeded N(0,1) bf16 q/K/V, page tables a seeded permutation of a 1.25x pool",
         "config": {
-            "workload": f"{args.config}: {CONFIG_DESCRIPTIONS[args.config]}",
+            "workload": f"{args.config}: {desc}",
             "num_seqs": n,
             "query_tokens": T,
             "sum_kv_len": int(case.kv_lens[:n].sum()),
@@ -325,22 +384,24 @@ def main() -> int:
             "kv_pool_copies_rotated": copies,
         },
         "tokens_per_s": round(T / (ms_step * 1e-3), 1),
-        "hbm_fraction": round(value / HBM_PEAK_GBPS, 4),
+        "hbm_fraction": round(value / peak, 4),
         "attn_kernel_ms": {"avg": round(kern_avg, 5), "median": round(kern_med, 5),
                            "p90": round(float(np.percentile(kern_ms, 90)), 5)},
         "wall_s_timed_region": round(wall, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved_bw, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved_bw / HBM_PEAK_GBPS, 4), "traffic": None},
+        "roofline": {"bound": "hbm", "achieved": round(achieved_bw, 2), "peak": peak, "unit": "GB/s",
+                     "frac": round(achieved_bw / peak, 4), "traffic": measured_traffic(args.config),
+                     "copy_probe_gbps": round(ceiling, 1),
+                     "basis": "algorithmic KV + Q + O bytes (tpu_cake_amd.cost_model.rpa_work) / average "
+                              "rpa_attn_kernel duration (HIP events on its stream); copy_probe_gbps: torch's "
+                              "1 GiB device-to-device copy on this box, read + write bytes / time"},
     }
-    traffic = measured_traffic(args.config)
-    if traffic is not None:
-        result["roofline"]["traffic"] = traffic
-    if flops and args.config == "c3":
-        result["prefill_mfma"] = {"flops": flops, "achieved_tflops_over_attn_kernel": round(roof_flops, 2),
-                                  "peak_tflops": BF16_PEAK_TFLOPS}
+    if flops:
+        result["prefill_mfma"] = {"flops": flops, "achieved_tflops_over_attn_kernel":
+                                  round(flops / (kern_avg * 1e-3) / 1e12, 2),
+                                  "peak_tflops": rates.compute_flops_per_second / 1e12}
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
-        result["cpu_baseline"] = cpu_baseline(case)
+        result["cpu_baseline"] = cpu_baseline(case, sliding_window=window)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -44,8 +44,32 @@ def test_artifacts_are_deterministic_and_self_consistent(name):
         assert src.sha256 == hashlib.sha256((ROOT / src.path).read_bytes()).hexdigest()
 
 
+# The reference's checked-in artifacts for its own row (data: sha256 of the files and the id they
+# carry): examples/inkling-rpa.mlir and contracts/inkling-rpa-experiment.json.
+REF_SCHEDULE_SHA256 = "b97d16b523329ed57890184ad9d6b0ed893d3c666874e919ccf857aa6591f4cc"
+REF_EXPERIMENT_ID = "b288837a2a06fc716e66c3508f761d0d4d01e110df248dadb9fa542b31296932"
+REF_EXPERIMENT_FILE_SHA256 = "9e098004545330efb41513a9b436a8c5f651e46768467f086638f41e3c351717"
+
+
+def test_reference_inkling_rpa_row_reproduces_the_reference_artifacts(tmp_path, capsys):
+    """render-workload / experiment inkling-rpa print the reference's TPU7x schedule text and
+    experiment JSON byte for byte (its CLI's two outputs, src/tpu_cake/cli.py:655-676)."""
+    text = contracts.render_workload("inkling-rpa")
+    assert hashlib.sha256(text.encode()).hexdigest() == REF_SCHEDULE_SHA256
+    exp = contracts.experiment("inkling-rpa")
+    assert exp.experiment_id == REF_EXPERIMENT_ID and exp.schedule_sha256 == REF_SCHEDULE_SHA256
+    out = tmp_path / "exp.json"
+    assert contracts.main(["experiment", "inkling-rpa", "--output", str(out)]) == 0
+    assert f"EXPERIMENT_WRITTEN workload=inkling-rpa id={REF_EXPERIMENT_ID}" in capsys.readouterr().out
+    assert hashlib.sha256(out.read_bytes()).hexdigest() == REF_EXPERIMENT_FILE_SHA256
+    assert exp.target.accelerator == "TPU7x" and exp.workload.execution is None
+    # a change to the schedule changes both hashes
+    assert hashlib.sha256(text.replace("kv_block_size = #builtin.int<8>", "kv_block_size = #builtin.int<16>")
+                          .encode()).hexdigest() != REF_SCHEDULE_SHA256
+
+
 def test_ids_differ_between_workloads_and_follow_content():
-    ids = {n: contracts.experiment(n).experiment_id for n in contracts.WORKLOADS}
+    ids = {n: contracts.experiment(n).experiment_id for n in contracts.ALL_WORKLOADS}
     assert len(set(ids.values())) == len(ids)
     exp = contracts.experiment("mi355x-rpa-c2")
     changed = exp.model_copy(update={"benchmark": exp.benchmark.model_copy(update={"measured_iterations": 51})})
@@ -137,13 +161,13 @@ def test_mixed_plan_splits_prefill_and_decode():
 
 def test_cli_writes_artifacts(tmp_path, capsys):
     out = tmp_path / "exp.json"
-    assert contracts.main(["experiment", "inkling-rpa", "--output", str(out)]) == 0
+    assert contracts.main(["experiment", "mi355x-inkling-rpa", "--output", str(out)]) == 0
     art = json.loads(out.read_text())
     assert f"id={art['experiment_id']}" in capsys.readouterr().out
     assert [t["name"] for t in art["workload"]["inputs"]] == [
         "query", "key_cache", "value_cache", "page_table", "sequence_lengths", "relative_bias"]
     plan = tmp_path / "plan.txt"
-    assert contracts.main(["render-workload", "inkling-rpa", "--output", str(plan)]) == 0
+    assert contracts.main(["render-workload", "mi355x-inkling-rpa", "--output", str(plan)]) == 0
     assert hashlib.sha256(plan.read_bytes()).hexdigest() == art["schedule_sha256"]
     with pytest.raises(SystemExit):
         contracts.main(["experiment", "no-such-workload"])

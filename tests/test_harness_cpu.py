@@ -296,3 +296,52 @@ def test_receipt_rejections(tmp_path, mutate, reason):
     _phase(tmp_path, "counters", ident)
     rec = evidence.build_receipt(tmp_path)
     assert rec["status"] == "rejected" and any(reason in r for r in rec["reasons"]), rec["reasons"]
+
+
+def _fake_raw(root):
+    """Raw outputs of a profile run for C2 and the copy calibration, shaped like rocprofv3's CSVs."""
+    attn = "void rpa::(anonymous namespace)::rpa_attn_kernel<0, true>(rpa::Params)"
+    comb = "rpa::(anonymous namespace)::rpa_combine_kernel(rpa::Params)"
+    copyk = "__amd_rocclr_copyBuffer"
+    d = root / "prof_c2"
+    d.mkdir(parents=True)
+    (d / "c2_kernel_stats.csv").write_text(
+        '"Name","Calls","TotalDurationNs","AverageNs","Percentage","MinNs","MaxNs","StdDev"\n'
+        f'"{attn}",23,2367000,102913.0,90,99000,124000,10\n"{comb}",23,123000,5347.8,9,4800,6600,1\n')
+    (root / "prof_c2.out").write_text('[bench] x\n{"attn_kernel_ms": {"avg": 0.1076}, "ms_per_step": 0.1183}\n')
+
+    def cc(name, rows):
+        (root / name).mkdir(parents=True)
+        lines = ['"Correlation_Id","Dispatch_Id","Kernel_Name","Counter_Name","Counter_Value"']
+        ncounters = len({c for _, c, _ in rows})
+        for i, (k, c, v) in enumerate(rows):  # one row per (dispatch, counter)
+            lines.append(f'{i},{i // ncounters},"{k}","{c}",{v}')
+        (root / name / "run_counter_collection.csv").write_text("\n".join(lines) + "\n")
+
+    cc("fetch_c2", [(attn, "FETCH_SIZE", 307979.0)] * 5)
+    cc("write_c2", [(attn, "WRITE_SIZE", 5090.0)] * 5)
+    cc("tcc_c2", [(attn, "TCC_EA0_RDREQ_128B_sum", 4924078.0), (attn, "TCC_EA0_RDREQ_64B_sum", 3598.0),
+                  (attn, "TCC_EA0_RDREQ_32B_sum", 0.0), (attn, "TCC_EA0_WRREQ_64B_sum", 81000.0)])
+    cc("mfma_c2", [(attn, "SQ_VALU_MFMA_BUSY_CYCLES", 2.0e7), (attn, "GRBM_GUI_ACTIVE", 2.1e5),
+                   (attn, "SQ_INSTS_VALU_MFMA_MOPS_BF16", 1.2e5)])
+    cc("fetch_copy", [(copyk, "FETCH_SIZE", 524288.0)] * 6)
+    cc("write_copy", [(copyk, "WRITE_SIZE", 1048576.0)] * 6)
+
+
+def test_profile_summaries_regenerate_identically(tmp_path):
+    from tpu_cake_amd import profiling
+
+    raw = tmp_path / "raw"
+    _fake_raw(raw)
+    a, b = tmp_path / "a", tmp_path / "b"
+    t1 = profiling.summarize(raw, a, raw_label="gpurun_out/prof")
+    profiling.summarize(raw, b, raw_label="gpurun_out/prof")
+    for f in sorted(p.name for p in a.iterdir()):
+        assert (a / f).read_bytes() == (b / f).read_bytes(), f
+    assert sorted(p.name for p in a.iterdir()) == ["pmc_traffic.json", "rpa_attn_c2.md"]
+    c2 = t1["configs"]["c2"]
+    assert t1["fetch_factor"] == 2.0 and t1["write_factor"] == 1.0
+    assert c2["traffic_bytes"] == round(307979.0 * 1024 * 2 + 5090.0 * 1024)
+    assert c2["mfma"]["mfma_busy_fraction"] == round(2.0e7 / (2.1e5 / 8 * 1024), 4)
+    md = (a / "rpa_attn_c2.md").read_text()
+    assert "rocprofv3 --kernel-trace --stats -d gpurun_out/prof/prof_c2" in md and "| rpa_attn_kernel | 23 | 102.91" in md

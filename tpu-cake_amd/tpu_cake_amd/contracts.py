@@ -11,10 +11,13 @@ results on those ids.
 This module keeps that schema (the same field names, so a consumer of the reference's
 artifacts reads these unchanged) for this build's workloads on one MI355X:
 
-* ``inkling-rpa`` -- the v1 Inkling decode contract (``workloads/inkling_rpa.py:693-722``: B 4,
-  H 4, D 32, separate K/V caches ``[32, 16, 4, 32]``, relative bias ``[4, 128]``), executed by
-  ``tpu_cake_amd.inkling.inkling_rpa`` (C ABI ``rpa_inkling_decode``);
-* ``inkling-fused-rpa`` -- the v3 fused decode on the reference's fixture shapes
+* ``inkling-rpa`` -- the reference's own row, reproduced exactly: its TPU7x schedule text
+  (``examples/inkling-rpa.mlir``, written by ``tpu_cake_amd.schedule_text``) and its experiment
+  (``contracts/inkling-rpa-experiment.json``);
+* ``mi355x-inkling-rpa`` -- the v1 Inkling decode contract (``workloads/inkling_rpa.py:693-722``:
+  B 4, H 4, D 32, separate K/V caches ``[32, 16, 4, 32]``, relative bias ``[4, 128]``) as executed
+  here by ``tpu_cake_amd.inkling.inkling_rpa`` (C ABI ``rpa_inkling_decode``);
+* ``mi355x-inkling-fused-rpa`` -- the v3 fused decode on the reference's fixture shapes
   (``workloads/inkling_rpa.py:413-468``), executed by ``tpu_cake_amd.fused`` (C ABI
   ``rpa_inkling_fused_decode``);
 * ``mi355x-rpa-c1`` .. ``mi355x-rpa-c5`` -- the benchmark configurations of the operator
@@ -43,6 +46,8 @@ from enum import Enum
 from typing import Callable
 
 from pydantic import BaseModel, ConfigDict, Field, computed_field, model_validator
+
+from .cost_model import floors, mi355x_rates
 
 PACKAGE = pathlib.Path(__file__).resolve().parent
 ROOT = PACKAGE.parent.parent
@@ -174,27 +179,35 @@ class KernelExperiment(BaseModel):
     @property
     def experiment_id(self) -> str:
         """sha256 of the experiment's JSON without this field (sorted keys, compact)."""
-        payload = self.model_dump(mode="json", exclude={"experiment_id"})
-        if payload["workload"]["execution"] is None:
-            del payload["workload"]["execution"]
-        encoded = json.dumps(payload, sort_keys=True, separators=(",", ":")).encode()
+        encoded = json.dumps(_artifact_payload(self), sort_keys=True, separators=(",", ":")).encode()
         return hashlib.sha256(encoded).hexdigest()
+
+
+def _artifact_payload(experiment: KernelExperiment) -> dict:
+    """The fields an artifact carries: a workload without an execution contract omits it, and a
+    profile expectation omits ``minimum_counter_device_planes`` while it holds its default 0 -- the
+    form of the reference's checked-in artifact (``contracts/inkling-rpa-experiment.json``), which
+    predates that field, so the ``inkling-rpa`` artifact and its id reproduce it exactly."""
+    payload = experiment.model_dump(mode="json", exclude={"experiment_id"})
+    if payload["workload"]["execution"] is None:
+        del payload["workload"]["execution"]
+    if payload["profile"].get("minimum_counter_device_planes") == 0:
+        del payload["profile"]["minimum_counter_device_planes"]
+    return payload
 
 
 def experiment_artifact_json(experiment: KernelExperiment, *, indent: int = 2) -> str:
     """The artifact: the experiment's fields and its id, indented."""
-    payload = experiment.model_dump(mode="json")
-    if payload["workload"]["execution"] is None:
-        del payload["workload"]["execution"]
-    return json.dumps(payload, indent=indent)
+    return json.dumps(dict(_artifact_payload(experiment), experiment_id=experiment.experiment_id), indent=indent)
 
 
 # ----------------------------------------------------------------------------------- target
-MI355X_CUS = 256
-MI355X_LDS_PER_CU = 160 * 1024
+_RATES = mi355x_rates()
+MI355X_CUS = _RATES.compute_units
+MI355X_LDS_PER_CU = _RATES.lds_bytes_per_cu
 MI355X_SGPR_BYTES_PER_CU = 4 * 800 * 4      # 800 scalar registers per SIMD, four SIMDs
-MI355X_HBM_BYTES_PER_S = 8_000_000_000_000  # HBM3E, AMD's published peak
-MI355X_BF16_FLOPS = 2_500_000_000_000_000   # dense bf16 MFMA, AMD's published peak
+MI355X_HBM_BYTES_PER_S = _RATES.hbm_bytes_per_second
+MI355X_BF16_FLOPS = _RATES.compute_flops_per_second
 WAVES_PER_CU = 8                            # the attention kernel: 2 waves per SIMD
 KV_CHUNK = 32                               # keys per stream-K unit (csrc/rpa_schedule.h)
 ROW_BLOCK = 16
@@ -323,16 +336,18 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
                                     source_manifest=_source_manifest()),
     )
     split = _work_split(m.kv_lens, m.q_lens, m.num_q_heads, m.num_kv_heads, m.kv_dtype, prefill_tiles=True)
-    kv_bytes = m.kv_read_bytes()
-    qo_bytes = 2 * m.num_tokens * m.num_q_heads * m.head_dim * 2
-    flops = m.prefill_flops()
+    work = m.work()
+    kv_bytes = work.kv_read_bytes + work.scale_bytes
+    qo_bytes = work.q_bytes + work.o_bytes
+    flops = work.prefill_flops
+    fl = floors(work, _RATES)
     hg = split["heads_per_workgroup"]
     unit_bytes = hg * KV_CHUNK * 2 * m.head_dim * (1 if m.kv_dtype == "fp8" else 2)
     mode = "KV_FP8" if m.kv_dtype == "fp8" else "KV_BF16"
     upg = m.page_size % KV_CHUNK == 0
     line = upg and m.kv_dtype != "fp8"
-    floor_hbm = (kv_bytes + qo_bytes) / MI355X_HBM_BYTES_PER_S * 1e6
-    floor_mfma = flops / MI355X_BF16_FLOPS * 1e6
+    floor_hbm = fl["hbm_s"] * 1e6
+    floor_mfma = fl["mfma_s"] * 1e6
     lines = [
         f"description = {CONFIG_DESCRIPTIONS[cfg]}",
         "entry = rpa_ragged_paged_attention (include/rpa.h); one call = the two launches below, stream-ordered",
@@ -352,9 +367,9 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
         f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg)} x block 256 (one workgroup per "
         f"(split descriptor, kv head), then {HEAVY_SLICES} per (heavy slot, kv head) for splits of "
         f">= {HEAVY_CONTRIB} workgroups)",
-        f"algorithmic = KV {kv_bytes} B + Q/O {qo_bytes} B; prefill {flops} FLOP",
-        f"roofline floor = HBM {floor_hbm:.2f} us; MFMA {floor_mfma:.2f} us; "
-        f"bound = {'mfma' if floor_mfma > floor_hbm else 'hbm'}",
+        f"algorithmic = KV {kv_bytes} B + Q/O {qo_bytes} B + metadata {work.metadata_bytes} B; "
+        f"QK/PV {work.flops} FLOP (prefill rows {flops})",
+        f"roofline floor = HBM {floor_hbm:.2f} us; MFMA {floor_mfma:.2f} us; bound = {fl['bound']}",
     ]
     return _plan_text(f"mi355x-rpa-{cfg}", lines), contract, dict(kernels=("rpa_attn_kernel", "rpa_combine_kernel"))
 
@@ -393,7 +408,7 @@ def _inkling_v1_workload() -> tuple[str, WorkloadContract, dict]:
         "launch 3 = rpa_fused_unpad_kernel: output rows 128 -> D",
     ]
     kernels = ("rpa_inkling_v1_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_unpad_kernel")
-    return _plan_text("inkling-rpa", lines), contract, dict(kernels=kernels)
+    return _plan_text("mi355x-inkling-rpa", lines), contract, dict(kernels=kernels)
 
 
 def _inkling_fused_workload() -> tuple[str, WorkloadContract, dict]:
@@ -439,27 +454,73 @@ def _inkling_fused_workload() -> tuple[str, WorkloadContract, dict]:
         "launch 3 = rpa_fused_unpad_kernel: output rows 128 -> D",
     ]
     kernels = ("rpa_fused_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_unpad_kernel")
-    return _plan_text("inkling-fused-rpa", lines), contract, dict(kernels=kernels)
+    return _plan_text("mi355x-inkling-fused-rpa", lines), contract, dict(kernels=kernels)
 
 
+# ----------------------------------------------------------------- the reference's own row
+def _reference_inkling_rpa() -> tuple[str, KernelExperiment]:
+    """``render-workload`` / ``experiment inkling-rpa`` as the reference prints them: its TPU7x
+    schedule text and ``KernelExperiment`` (``inkling_rpa_contract`` / ``inkling_rpa_experiment``,
+    src/tpu_cake/workloads/inkling_rpa.py:693-722, :937-964), reproducing
+    ``examples/inkling-rpa.mlir`` and ``contracts/inkling-rpa-experiment.json`` byte for byte."""
+    from .schedule_text import inkling_rpa_schedule_text
+
+    def t(name, shape, logical):
+        return _tensor(name, shape, logical.split(), "i32" if name in ("page_table", "sequence_lengths") else "bf16")
+
+    text = inkling_rpa_schedule_text()
+    workload = WorkloadContract(
+        name="inkling-ragged-paged-relative-bias-attention", stage=WorkloadStage.STEADY_DECODE,
+        inputs=(t("query", (4, 4, 32), "B H D"), t("key_cache", (32, 16, 4, 32), "P S H D"),
+                t("value_cache", (32, 16, 4, 32), "P S H D"), t("page_table", (4, 8), "B MP"),
+                t("sequence_lengths", (4,), "B"), t("relative_bias", (4, 128), "H L")),
+        outputs=(t("output", (4, 4, 32), "B H D"),),
+        numerical=NumericalContract(reference="tpu_cake.workloads.inkling_rpa.inkling_rpa_reference",
+                                    absolute_tolerance=0.02, relative_tolerance=0.02),
+    )
+    exp = KernelExperiment(
+        workload=workload,
+        target=TargetHardware(accelerator="TPU7x", topology="4x1", chip_count=4, vmem_budget_bytes_per_core=2 << 20,
+                              smem_budget_bytes_per_core=1 << 16, runtime_target="Pallas Mosaic TPU"),
+        benchmark=BenchmarkProtocol(warmup_iterations=5, measured_iterations=50,
+                                    synchronization="block until device result is ready",
+                                    statistic="median device duration"),
+        search=SearchPolicy(objective_metric="median_device_duration_ns"),
+        profile=ProfileExpectation(name="inkling-rpa-steady-decode", stage=WorkloadStage.STEADY_DECODE,
+                                   minimum_tpu_device_planes=8, required_timed_hlo_markers=("ragged_paged_attention",),
+                                   forbidden_timed_hlo_fragments=("12582912,16", "native_backend.py:500")),
+        schedule_sha256=hashlib.sha256(text.encode()).hexdigest(),
+    )
+    return text, exp
+
+
+# the reference's rows (its CLI's _WORKLOADS, src/tpu_cake/cli.py:148-151, RPA part)
+REFERENCE_WORKLOADS = {"inkling-rpa": _reference_inkling_rpa}
+
+# this build's rows: the MI355X launch plans
 WORKLOADS: dict[str, Callable[[], tuple[str, WorkloadContract, dict]]] = {
-    "inkling-rpa": _inkling_v1_workload,
-    "inkling-fused-rpa": _inkling_fused_workload,
+    "mi355x-inkling-rpa": _inkling_v1_workload,
+    "mi355x-inkling-fused-rpa": _inkling_fused_workload,
     **{f"mi355x-rpa-c{i}": (lambda c=f"c{i}": _operator_workload(c)) for i in range(1, 6)},
 }
+ALL_WORKLOADS = (*REFERENCE_WORKLOADS, *WORKLOADS)
 
 
 def render_workload(name: str) -> str:
-    """The workload's launch plan on MI355X (canonical text; its sha256 is the experiment's
-    ``schedule_sha256``)."""
+    """The workload's schedule: the reference's TPU schedule text for its own rows, the launch plan
+    on MI355X for this build's (canonical text; its sha256 is the experiment's ``schedule_sha256``)."""
+    if name in REFERENCE_WORKLOADS:
+        return REFERENCE_WORKLOADS[name]()[0]
     if name not in WORKLOADS:
-        raise ValueError(f"unknown workload {name!r}; expected one of {sorted(WORKLOADS)}")
+        raise ValueError(f"unknown workload {name!r}; expected one of {sorted(ALL_WORKLOADS)}")
     return WORKLOADS[name]()[0]
 
 
 def experiment(name: str) -> KernelExperiment:
+    if name in REFERENCE_WORKLOADS:
+        return REFERENCE_WORKLOADS[name]()[1]
     if name not in WORKLOADS:
-        raise ValueError(f"unknown workload {name!r}; expected one of {sorted(WORKLOADS)}")
+        raise ValueError(f"unknown workload {name!r}; expected one of {sorted(ALL_WORKLOADS)}")
     text, contract, extra = WORKLOADS[name]()
     return KernelExperiment(
         workload=contract,
@@ -489,11 +550,11 @@ def main(argv=None) -> int:
     sub.add_parser("list-workloads")
     for cmd in ("render-workload", "experiment"):
         sp = sub.add_parser(cmd)
-        sp.add_argument("workload", choices=sorted(WORKLOADS))
+        sp.add_argument("workload", choices=sorted(ALL_WORKLOADS))
         sp.add_argument("--output", type=pathlib.Path)
     args = ap.parse_args(argv)
     if args.cmd == "list-workloads":
-        for name in WORKLOADS:
+        for name in ALL_WORKLOADS:
             print(name)
         return 0
     if args.cmd == "render-workload":

@@ -48,6 +48,10 @@ CSRC = PACKAGE.parent / "csrc"
 PHASES = ("timing", "trace", "counters")
 KERNELS = ("rpa_attn_kernel", "rpa_combine_kernel")
 COUNTERS = ("FETCH_SIZE", "WRITE_SIZE")
+# MFMA activity of the attention kernel (the reference fails a capture without MXU-busy series,
+# src/tpu_cake/xprof_evidence.py:339-349): busy cycles summed over SIMDs, the GPU's active cycles,
+# and the bf16 MFMA math ops / 512
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16")
 
 
 # --------------------------------------------------------------------------- identity
@@ -79,7 +83,8 @@ def source_identity() -> dict:
 
 # --------------------------------------------------------------------------- profiles
 def _kernel_key(name: str) -> str | None:
-    for k in ("rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_prep_kernel", "rpa_inkling_v1_prep_kernel"):
+    for k in ("rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_prep_kernel", "rpa_inkling_v1_prep_kernel",
+              "rpa_fused_unpad_kernel", "rpa_scratch_clear_kernel", "__amd_rocclr_copyBuffer"):
         if k in name:
             return k
     return None
@@ -96,7 +101,7 @@ def inspect_profile(path) -> dict:
     for stats in root.rglob("*kernel_stats.csv"):
         for r in csv.DictReader(open(stats)):
             k = _kernel_key(r["Name"])
-            if k is None:
+            if k is None or not k.startswith("rpa"):
                 continue
             e = kernels.setdefault(k, {"calls": 0, "total_ns": 0.0, "min_ns": math.inf, "max_ns": 0.0})
             e["calls"] += int(r["Calls"])
@@ -111,7 +116,7 @@ def inspect_profile(path) -> dict:
         seen: dict = {}
         for r in csv.DictReader(open(cc)):
             k = _kernel_key(r["Kernel_Name"])
-            if k is None:
+            if k is None or not k.startswith("rpa"):
                 continue
             acc.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
             seen.setdefault(k, set()).add(r.get("Dispatch_Id") or r.get("Correlation_Id"))
@@ -126,7 +131,7 @@ def inspect_profile(path) -> dict:
 def assess_profile(profile: dict, *, dispatches: int, counters: tuple = ()) -> dict:
     """Accept a profile if every kernel of the call was captured at least ``dispatches`` times
     (the timed steps) and, for a counters run, every named counter was read for the attention
-    kernel."""
+    kernel (a counters run names the HBM counters and the MFMA-activity ones)."""
     reasons = []
     for k in KERNELS:
         calls = profile["kernels"].get(k, {}).get("calls", 0)
@@ -229,13 +234,15 @@ def run_profiled(root, mode: str, config: str, steps: int, warmup: int) -> dict:
         cmds = [["rocprofv3", "--kernel-trace", "--stats", "-d", str(phase_root / "kt"), "-o", "run",
                  "--output-format", "csv", "--"] + child]
     else:
-        cmds = [["rocprofv3", "--pmc", c, "-d", str(phase_root / c.lower()), "-o", "run", "--output-format", "csv",
-                 "--"] + child for c in COUNTERS]
+        passes = [(c.lower(), [c]) for c in COUNTERS] + [("mfma", list(MFMA_COUNTERS))]
+        cmds = [["rocprofv3", "--pmc", *cs, "-d", str(phase_root / d), "-o", "run", "--output-format", "csv",
+                 "--"] + child for d, cs in passes]
     for cmd in cmds:
         subprocess.run(["timeout", "-s", "KILL", "120"] + cmd, check=True, env=env, stdout=subprocess.DEVNULL)
     steps_res = json.loads((phase_root / "steps.json").read_text())
     prof = inspect_profile(phase_root)
-    assessment = assess_profile(prof, dispatches=steps, counters=COUNTERS if mode == "counters" else ())
+    assessment = assess_profile(prof, dispatches=steps,
+                                counters=COUNTERS + MFMA_COUNTERS if mode == "counters" else ())
     body = {**steps_res, "profile": prof, "assessment": assessment, "passed": assessment["accepted"]}
     return _write_result(phase_root, mode, body)
 
@@ -327,7 +334,21 @@ def main(argv=None) -> int:
     i.add_argument("path")
     v = sub.add_parser("validate")
     v.add_argument("root")
+    pr = sub.add_parser("profile", help="run every rocprofv3 pass behind profiles/ (GPU box)")
+    pr.add_argument("--raw", required=True)
+    pr.add_argument("--configs", nargs="*", default=None)
+    sm = sub.add_parser("summarize", help="write profiles/*.md and pmc_traffic.json from a profile run")
+    sm.add_argument("--raw", required=True)
+    sm.add_argument("--write", required=True)
     a = ap.parse_args(argv)
+    if a.cmd in ("profile", "summarize"):
+        from . import profiling
+
+        if a.cmd == "profile":
+            profiling.run_profiles(a.raw, tuple(a.configs) if a.configs else profiling.CONFIGS)
+        else:
+            profiling.summarize(a.raw, a.write, raw_label=a.raw)
+        return 0
     if a.cmd == "_steps":
         res, _, _ = _steps(a.config, a.steps, a.warmup, events=False)
         pathlib.Path(a.out).write_text(json.dumps(res) + "\n")

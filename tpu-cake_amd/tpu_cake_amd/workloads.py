@@ -88,29 +88,24 @@ class RpaCase:
         n = int(self.num_seqs[0])
         return np.diff(self.cu_q_lens[: n + 1]).astype(np.int64)
 
-    def kv_read_bytes(self) -> int:
-        """Algorithmic KV bytes one call must read: sum(L) * Hkv * 2 * D * elem (+ scales)."""
-        n = int(self.num_seqs[0])
-        toks = int(np.sum(self.kv_lens[:n], dtype=np.int64))
-        elem = 1 if self.kv_dtype == "fp8" else 2
-        b = toks * self.num_kv_heads * 2 * self.head_dim * elem
-        if self.kv_scales is not None:
-            pages = int(np.sum(-(-self.kv_lens[:n].astype(np.int64) // self.page_size)))
-            b += pages * self.num_kv_heads * 2 * 4
-        return b
+    def work(self, sliding_window: int | None = None):
+        """The call's algorithmic work (``tpu_cake_amd.cost_model.rpa_work``)."""
+        from .cost_model import rpa_work
 
-    def prefill_flops(self) -> int:
-        """Causal QK^T + PV flops of rows with q_len > 1: 4*Hq*D*sum(visible keys)."""
         n = int(self.num_seqs[0])
-        total = 0
-        for i in range(n):
-            ql = int(self.cu_q_lens[i + 1] - self.cu_q_lens[i])
-            if ql <= 1:
-                continue
-            L = int(self.kv_lens[i])
-            prior = L - ql
-            total += ql * prior + ql * (ql + 1) // 2
-        return 4 * self.num_q_heads * self.head_dim * total
+        return rpa_work(self.kv_lens[:n], self.q_lens, num_q_heads=self.num_q_heads,
+                        num_kv_heads=self.num_kv_heads, head_dim=self.head_dim, page_size=self.page_size,
+                        kv_dtype=self.kv_dtype, sliding_window=sliding_window)
+
+    def kv_read_bytes(self, sliding_window: int | None = None) -> int:
+        """Algorithmic KV bytes one call must read: every key some query row sees, K and V of every
+        kv head (sum(L) * Hkv * 2 * D * elem without a window), plus the fp8 scales of those pages."""
+        w = self.work(sliding_window)
+        return w.kv_read_bytes + w.scale_bytes
+
+    def prefill_flops(self, sliding_window: int | None = None) -> int:
+        """Causal QK^T + PV flops of rows with q_len > 1: 4*Hq*D*sum(visible keys)."""
+        return self.work(sliding_window).prefill_flops
 
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
@@ -208,22 +203,21 @@ class ConfigMeta:
     def num_seqs(self) -> int:
         return len(self.kv_lens)
 
-    def kv_read_bytes(self) -> int:
-        """sum(L) * Hkv * 2 * D * elem (+ the fp8 pool's per-(page, head) K and V scales)."""
-        toks = int(np.sum(self.kv_lens, dtype=np.int64))
-        elem = 1 if self.kv_dtype == "fp8" else 2
-        b = toks * self.num_kv_heads * 2 * self.head_dim * elem
-        if self.kv_dtype == "fp8":
-            b += int(np.sum(-(-self.kv_lens.astype(np.int64) // self.page_size))) * self.num_kv_heads * 2 * 4
-        return b
+    def work(self, sliding_window: int | None = None):
+        from .cost_model import rpa_work
 
-    def prefill_flops(self) -> int:
+        return rpa_work(self.kv_lens, self.q_lens, num_q_heads=self.num_q_heads, num_kv_heads=self.num_kv_heads,
+                        head_dim=self.head_dim, page_size=self.page_size, kv_dtype=self.kv_dtype,
+                        sliding_window=sliding_window)
+
+    def kv_read_bytes(self, sliding_window: int | None = None) -> int:
+        """sum(L) * Hkv * 2 * D * elem (+ the fp8 pool's per-(page, head) K and V scales)."""
+        w = self.work(sliding_window)
+        return w.kv_read_bytes + w.scale_bytes
+
+    def prefill_flops(self, sliding_window: int | None = None) -> int:
         """Causal QK^T + PV flops of rows with q_len > 1: 4*Hq*D*sum(visible keys)."""
-        total = 0
-        for L, ql in zip(self.kv_lens.tolist(), self.q_lens.tolist()):
-            if ql > 1:
-                total += ql * (L - ql) + ql * (ql + 1) // 2
-        return 4 * self.num_q_heads * self.head_dim * total
+        return self.work(sliding_window).prefill_flops
 
 
 def _config_meta(cfg: str, rng) -> ConfigMeta:
@@ -359,3 +353,29 @@ def make_fused_case(seed: int = 102, *, nseq: int = 64, num_q_heads: int = 32, n
         "relative_projection": normal((relative_dim, relative_extent), 0.4, 8),
     }
     return FusedCase(arrays=arrays, sm_scale=1.0 / head_dim)
+
+
+def fused_lengths(seed: int = 102, nseq: int = 64) -> np.ndarray:
+    """The kv lengths make_fused_case draws for ``seed`` (its first draws), without the arrays."""
+    z = np.random.default_rng(seed).standard_normal(nseq)
+    return np.clip(np.round(np.exp(math.log(2048.0) + LOGNORMAL_SIGMA * z)), 128, 8192).astype(np.int64)
+
+
+def make_fused_meta(seed: int = 102, *, nseq: int = 64, num_q_heads: int = 32, num_kv_heads: int = 8) -> dict:
+    """Byte counts of the fused decode step of make_fused_case(seed) (KV read, Q, O and the new
+    K/V rows written), from its lengths alone."""
+    lens = fused_lengths(seed, nseq)
+    kv = int(lens.sum()) * num_kv_heads * 2 * 128 * 2
+    qo = 2 * nseq * num_q_heads * 128 * 2
+    new_rows = 2 * nseq * num_kv_heads * 128 * 2 * 2  # keys and values, read and written
+    return {"kv_read_bytes": kv, "moved_bytes": kv + qo + new_rows}
+
+
+WINDOWED_CONFIGS = {"c2w": ("c2", 512)}
+
+
+def make_config_meta_for(name: str):
+    """(ConfigMeta, sliding window or None) of a benchmark configuration, including the windowed
+    ones (``c2w``: C2 with a 512-key sliding window)."""
+    base, window = WINDOWED_CONFIGS.get(name, (name, None))
+    return config_meta(base), window
