@@ -278,6 +278,11 @@ def main() -> int:
     ap.add_argument("--rotate-bytes", type=float, default=2.0e9,
                     help="KV pool copies rotated so that at least this many bytes separate reuses")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--waves-per-cu", type=int, default=None, help="schedule knob (default: the tuned table)")
+    ap.add_argument("--prefill-tiles", type=int, default=None, choices=[-1, 0, 1, 2],
+                    help="1: prefill kernel, 2: the attention kernel's own prefill tiles, -1: stream-K rows "
+                         "(default: the tuned table)")
+    ap.add_argument("--prefill-cost", type=float, default=None, help="schedule knob (default: the tuned table)")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="BYTES",
                     help="instead of the benchmark, run 5 device-to-device copies of BYTES (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -333,10 +338,13 @@ def main() -> int:
     rates = _rates()
     peak = rates.hbm_bytes_per_second / 1e9
 
+    knobs = {k: v for k, v in (("waves_per_cu", args.waves_per_cu), ("prefill_tiles", args.prefill_tiles),
+                               ("prefill_cost", args.prefill_cost)) if v is not None}
+
     def call(i, ev=None):
         ops.ragged_paged_attention(d["q"], pools[i % copies], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
                                    d["num_seqs"], sm_scale=case.sm_scale, kv_scales=kv_scales, out=out,
-                                   kernel_events=ev, sliding_window=window)
+                                   kernel_events=ev, sliding_window=window, **knobs)
 
     for i in range(args.warmup):
         call(i)
@@ -382,6 +390,7 @@ def main() -> int:
             "sum_kv_len": int(case.kv_lens[:n].sum()),
             "kv_bytes_per_step": kv_bytes,
             "kv_pool_copies_rotated": copies,
+            **({"knobs": knobs} if knobs else {}),
         },
         "tokens_per_s": round(T / (ms_step * 1e-3), 1),
         "hbm_fraction": round(value / peak, 4),

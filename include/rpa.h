@@ -65,10 +65,12 @@ typedef struct rpa_shape {
  * num_queries_per_block (ragged_paged_attention.py:726-728, :801-816):
  *   waves_per_cu   1..7 caps the persistent attention grid at that many waves
  *                  per compute unit (0 or 8: the kernel's occupancy, 8);
- *   prefill_tiles  -1 = sequences with long query chunks run as causal row
- *                  blocks of the stream-K role, 0 or 1 = they take the
- *                  MFMA prefill tiles where those are built (bf16 KV without
- *                  scales, the default mask value, 8 kv heads per workgroup);
+ *   prefill_tiles  sequences with at least 16 query tokens (bf16 KV without
+ *                  scales, the default mask value): 2 = the attention kernel's
+ *                  own MFMA prefill tiles (8 kv heads per workgroup); 1 = the
+ *                  standalone prefill kernel (page size a multiple of 64);
+ *                  0 = the first of those two that applies; -1 = causal row
+ *                  blocks of the stream-K role (also whenever neither applies);
  *   prefill_cost   > 0: the cost of one prefill-tile chunk step in stream-K
  *                  units, which sets the work split between the two roles
  *                  (0 = 0.45). */

@@ -188,3 +188,53 @@ def test_c5_longest_sequence_131072_keys(cuda):
                        pages_per_seq=2048, seed=131)
     d = ops.case_to_device(case, "cuda")
     _assert_close(_run(d, case), _ref(case), "131072 keys")
+
+
+# ------------------------------------------------------------------------------------- prefill kernel
+@pytest.mark.parametrize("hq,hkv,q_lens,kv_lens,page", [
+    (32, 8, [512, 1, 300, 1], [1536, 900, 300, 77], 64),   # G=4: 64-token tiles, prior 1024 / none
+    (64, 8, [100, 1, 17], [100, 4000, 50], 128),           # G=8: 32-token tiles, q_len == kv_len, page 128
+    (8, 8, [300, 2], [337, 2], 64),                        # G=1: 256-token tiles
+    (128, 8, [40, 1], [1040, 8], 64),                      # G=16: 16-token tiles
+    (40, 8, [300, 1, 16], [3000, 600, 16], 64),            # G=5: 51-token tiles, one row per tile unused
+    (12, 4, [700, 64], [2000, 64], 64),                    # 4 kv heads (no 8-wave workgroup needed)
+    (32, 8, [2048], [6000], 64),                           # one long chunk: tiles split over many workgroups
+])
+def test_prefill_kernel_matches_oracle_and_other_paths(cuda, hq, hkv, q_lens, kv_lens, page):
+    _say(f"prefill kernel hq={hq} hkv={hkv} q={q_lens} kv={kv_lens} page={page}")
+    case = make_custom(kv_lens=kv_lens, q_lens=q_lens, num_q_heads=hq, num_kv_heads=hkv, page_size=page,
+                       seed=sum(q_lens) + hq + page)
+    d = ops.case_to_device(case, "cuda")
+    ref = _ref(case)
+    got = _run(d, case, prefill_tiles=1)
+    _assert_close(got, ref, "prefill kernel")
+    _assert_close(got, _run(d, case, prefill_tiles=-1)[: ref.shape[0]], "vs stream-K rows")
+    assert np.array_equal(got, _run(d, case, prefill_tiles=1)), "not deterministic"
+
+
+@pytest.mark.parametrize("kw", [dict(sliding_window=100), dict(soft_cap=30.0), dict(sliding_window=700, soft_cap=-8.0)])
+def test_prefill_kernel_window_and_soft_cap(cuda, kw):
+    _say(f"prefill kernel {kw}")
+    case = make_custom(kv_lens=[2500, 300, 900], q_lens=[400, 1, 300], num_q_heads=32, num_kv_heads=8,
+                       page_size=64, seed=77)
+    d = ops.case_to_device(case, "cuda")
+    _assert_close(_run(d, case, prefill_tiles=1, **kw), _ref(case, **kw), f"prefill kernel {kw}")
+
+
+@pytest.mark.parametrize("wpc", [0, 2, 5])
+def test_prefill_kernel_on_c3_with_other_knobs(cuda, c3_case, wpc):
+    case, d, ref = c3_case
+    _say(f"c3 prefill kernel, waves_per_cu={wpc}; in-kernel tiles")
+    a = _run(d, case, prefill_tiles=1, waves_per_cu=wpc)
+    _assert_close(a, ref, "prefill kernel")
+    _assert_close(_run(d, case, prefill_tiles=2, waves_per_cu=wpc), ref, "in-kernel tiles")
+
+
+def test_prefill_kernel_back_to_back_calls_leave_no_state(cuda):
+    """Consecutive calls with different tile splits: every split descriptor is cleared by the merge."""
+    _say("prefill kernel back-to-back")
+    for i, (q, kv) in enumerate([([512, 512], [4000, 600]), ([64, 1, 1000], [64, 5000, 3000]), ([512, 512], [4000, 600])]):
+        case = make_custom(kv_lens=kv, q_lens=q, num_q_heads=32, num_kv_heads=8, page_size=64, seed=400 + i)
+        d = ops.case_to_device(case, "cuda")
+        _assert_close(_run(d, case, prefill_tiles=1), _ref(case), f"call {i}")
+    assert ops.read_error_word() == 0

@@ -116,6 +116,22 @@ struct Params {
   int pf_tq;         // tokens per prefill tile (0 = prefill tiles off)
   int pf_min;        // sequences with at least this many query tokens take prefill tiles
   float pf_cost;     // cost of one prefill tile chunk in stream-K units (work split model)
+  // the prefill kernel (rpa_prefill_kernel): when pf_kernel is set, sequences with at least pf_min
+  // query tokens are its tiles of pf_tq tokens (256 rows), the attention kernel skips them and
+  // runs no prefill role of its own
+  bool pf_kernel;
+  int pk_grid;                 // prefill-kernel workgroups
+  float* pk_acc;               // [2 * pk_grid][256][kD] split-tile partials
+  float* pk_ml;                // [2 * pk_grid][256][2]
+  struct PkDesc* pk_desc;      // [pk_grid] split tile ending in prefill workgroup b
+};
+
+// A prefill tile split across prefill-kernel workgroups b0..b (b = the owner of its last chunk).
+struct PkDesc {
+  int valid[16];  // one per 16-row group of the tile; the combine workgroup of that group clears it
+  int q_start;    // first query token of the tile (the sequence's first token + tok0)
+  int ntok, h, pad;
+  long long b0;
 };
 
 // ---------------------------------------------------------------------------------------------
@@ -1560,7 +1576,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   bool any_pf = false;
 #pragma unroll
   for (int w = 0; w < kWin; ++w) any_pf = any_pf || wsi[w].q_len >= pf_min;
-  if (MODE == KV_BF16 && pf_min > 0 && __ballot(any_pf) != 0) {
+  if (MODE == KV_BF16 && pf_min > 0 && !p.pf_kernel && __ballot(any_pf) != 0) {
     // per lane over the four windows, then one wave sum each (skipped when no sequence is a
     // prefill sequence)
     float st = 0.f;
@@ -1688,6 +1704,551 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     u32x4* o = (u32x4*)p.out;
     for (size_t k = first + (size_t)b * blockDim.x + threadIdx.x; k < last; k += (size_t)p.grid * blockDim.x)
       o[k] = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (err) atomicOr(p.err, err);
+}
+
+// ---------------------------------------------------------------------------------------------
+// prefill kernel: the MFMA-dense rows
+// ---------------------------------------------------------------------------------------------
+// Sequences with at least pf_min query tokens are cut into TILES: (sequence, kv head h, pf_tq =
+// 256 / G consecutive tokens), 256 rows r = token * G + g (q head h*G + g).  A tile's work is its
+// 64-key CHUNK STEPS over the keys its rows see (causal limit of its last row, sliding window of
+// its first).  Chunk steps are ordered tile by tile (sequence, head, token block) and split evenly
+// over the grid (the balanced partition of rpa_schedule.h, one workgroup per CU), so a long causal
+// prefix is shared by several workgroups; a tile split across workgroups leaves one (m, l, acc)
+// partial per workgroup, merged by rpa_combine_kernel.
+//
+// Workgroup = 4 waves, one per SIMD, wave w owning rows 64w .. 64w+63 as four 16-row MFMA blocks
+// (the whole register file of a SIMD: 64 rows of fp32 accumulators, the queries and a chunk's
+// scores stay in registers).  Per chunk the workgroup stages K (key rows, 272-byte stride) and V^T
+// (dim rows of 64 keys in the tau order of the QK output, 144-byte stride, 16-byte groups XOR-
+// swizzled by row bits 4-5: conflict-free transposing writes and fragment reads) in one of two LDS
+// buffers; the 8x8 transposes of V happen in registers across lanes.  Every K and V^T fragment
+// feeds the wave's four row blocks: 64 + 64 MFMAs per chunk per wave.  Loads run two chunk steps
+// ahead (page ids three), stores of the next chunk follow the compute, one barrier per step.
+constexpr int kPkRows = 256;
+constexpr int kPkChunk = 64;
+constexpr int kPkKRow = kD * 2 + 16;            // 272 B per K row
+constexpr int kPkKTile = kPkChunk * kPkKRow;    // 17408 B
+constexpr int kPkVtRow = kPkChunk * 2 + 16;     // 144 B per V^T dim row (64 keys + pad)
+constexpr int kPkVtTile = kD * kPkVtRow;        // 18432 B
+constexpr int kPkStage = kPkKTile + kPkVtTile;  // 35840 B
+constexpr int kPkLds = 2 * kPkStage;
+
+// Position of 16-byte key group q (= 4 * half + g) in V^T row `row`.
+__device__ __forceinline__ int pk_vt_pos(int row, int q) {
+  return q ^ (((row >> 4) & 1) << 1) ^ (((row >> 5) & 1) << 2);
+}
+
+// 8x8 bf16 transpose across the lanes l % 8 == const: before, lane l holds 8 dims of key row
+// l / 8; after, 8 keys (rows 0..7) of dim l / 8 -- exchanging element bit i with lane-group bit i
+// for i = 0 (lanes ^8), 1 (^16), 2 (^32).
+__device__ __forceinline__ u32x4 transpose8x8_bf16(u32x4 v, int l) {
+  uint32_t d[4] = {v[0], v[1], v[2], v[3]};
+  const uint32_t sel = (l & 8) ? 0x03020706u : 0x05040100u;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t pv = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[m], 0x128, 0xf, 0xf, false);  // lane ^ 8
+    d[m] = __builtin_amdgcn_perm(pv, d[m], sel);
+  }
+  {
+    const auto x = __builtin_amdgcn_permlane16_swap(d[0], d[1], false, false);
+    const auto y = __builtin_amdgcn_permlane16_swap(d[2], d[3], false, false);
+    d[0] = x[0];
+    d[1] = x[1];
+    d[2] = y[0];
+    d[3] = y[1];
+  }
+  {
+    const auto x = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+    const auto y = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+    d[0] = x[0];
+    d[2] = x[1];
+    d[1] = y[0];
+    d[3] = y[1];
+  }
+  return u32x4{d[0], d[1], d[2], d[3]};
+}
+
+struct PkTile {
+  int seq, h, t, nt;       // sequence, kv head, token block, token blocks of the sequence
+  int kv_len, q_len, q_start;
+  int tok0, ntok;          // first token (sequence-relative) and tokens of the tile
+  int c_lo, c_hi;          // chunks visited
+};
+
+// Chunk range of token block t (0 units when its rows see no key).
+__device__ __forceinline__ void pk_range(const Params& p, PkTile& tl) {
+  tl.tok0 = tl.t * p.pf_tq;
+  tl.ntok = tl.q_len - tl.tok0 < p.pf_tq ? tl.q_len - tl.tok0 : p.pf_tq;
+  const int prior = tl.kv_len - tl.q_len;
+  int hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
+  hi = hi < tl.kv_len - 1 ? hi : tl.kv_len - 1;
+  int lo = 0;
+  if (p.sliding_window > 0) {  // keys below are masked for every row of the tile
+    lo = prior + tl.tok0 - p.sliding_window + 1;
+    lo = lo < 0 ? 0 : lo;
+  }
+  tl.c_lo = lo / kPkChunk;
+  tl.c_hi = hi >= lo ? hi / kPkChunk + 1 : tl.c_lo;
+}
+
+// Chunk steps of one kv head of a sequence (a prefill sequence: q_len >= pf_min).
+__device__ __forceinline__ int pk_units_per_head(const Params& p, int kv_len, int q_len) {
+  if (q_len < p.pf_min || kv_len <= 0) return 0;
+  PkTile tl;
+  tl.kv_len = kv_len;
+  tl.q_len = q_len;
+  const int nt = (q_len + p.pf_tq - 1) / p.pf_tq;
+  int u = 0;
+  for (int t = 0; t < nt; ++t) {
+    tl.t = t;
+    pk_range(p, tl);
+    u += tl.c_hi - tl.c_lo;
+  }
+  return u;
+}
+
+// A sequence's metadata out of the four per-lane windows (s wave-uniform, < 256).
+__device__ __forceinline__ void pk_seq(const SeqInfo wsi[4], const int units[4], int s, PkTile& tl, int& u) {
+  const int w = s >> 6, k = s & 63;
+  int kv = 0, ql = 0, qs = 0, un = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // value selects keep the windows in registers
+    kv = w == i ? wsi[i].kv_len : kv;
+    ql = w == i ? wsi[i].q_len : ql;
+    qs = w == i ? wsi[i].q_start : qs;
+    un = w == i ? units[i] : un;
+  }
+  tl.seq = s;
+  tl.kv_len = rl(kv, k);
+  tl.q_len = rl(ql, k);
+  tl.q_start = rl(qs, k);
+  u = rl(un, k);
+}
+
+struct PkCur {
+  PkTile tl;
+  int c;      // chunk
+  int units;  // chunk steps per kv head of tl.seq
+  bool live;  // false past the workgroup's range
+};
+
+// The next chunk step (tile by tile: token block, then kv head, then sequence).
+__device__ __forceinline__ void pk_advance(const Params& p, const SeqInfo wsi[4], const int units[4], int nseq,
+                                           PkCur& x) {
+  if (!x.live) return;
+  if (x.c + 1 < x.tl.c_hi) {
+    x.c++;
+    return;
+  }
+  for (;;) {
+    if (x.tl.t + 1 < x.tl.nt) {
+      x.tl.t++;
+    } else if (x.tl.h + 1 < p.Hkv) {
+      x.tl.h++;
+      x.tl.t = 0;
+    } else {
+      int s = x.tl.seq;
+      int un = 0;
+      do {
+        if (++s >= nseq) {
+          x.live = false;
+          return;
+        }
+        pk_seq(wsi, units, s, x.tl, un);
+      } while (un == 0);
+      x.units = un;
+      x.tl.nt = (x.tl.q_len + p.pf_tq - 1) / p.pf_tq;
+      x.tl.h = 0;
+      x.tl.t = 0;
+    }
+    pk_range(p, x.tl);
+    if (x.tl.c_hi > x.tl.c_lo) {
+      x.c = x.tl.c_lo;
+      return;
+    }
+  }
+}
+
+// The chunk steps' K and V pieces of one thread (4 + 4 x 16 bytes).
+struct PkRegs {
+  u32x4 k[4], v[4];
+};
+
+// Issue the loads of chunk step x (page id pg, read a step earlier).  K piece i: key
+// (tid / 16) + 16 i, dims 8 (tid % 16) ..; V piece i: key 32 (i & 1) + tau(w, lane / 8), dims
+// 8 ((lane % 8) + 8 (i >> 1)) ..  Keys past kv_len read key kv_len - 1 (masked by their scores).
+// The chunk's base address is wave-uniform; each piece is a 32-bit byte offset from it.
+__device__ __forceinline__ void pk_load(const Params& p, const PkCur& x, int pg, int tid, PkRegs& r, int& err) {
+  pg = uni(pg);
+  if (pg < 0 || pg >= p.P) {  // out-of-range page id: never dereferenced
+    if (x.live) err |= ERR_PAGE;
+    pg = 0;
+  }
+  const int key0 = x.live ? x.c * kPkChunk : 0;
+  const int kmax = x.live ? x.tl.kv_len - 1 - key0 : 0;
+  const uint8_t* base = p.kv + 2 * kv_elem(p, pg, key0, 2 * (x.live ? x.tl.h : 0));
+  const uint32_t row = (uint32_t)(2 * p.Hkv) * kD * 2;  // bytes between consecutive keys of a page
+  const int w = tid >> 6, l = tid & 63, e = l >> 3;
+  const uint32_t kcol = 16u * (tid & 15), vcol = 2u * kD + 16u * (l & 7);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int kk = (tid >> 4) + 16 * i;
+    kk = kk < kmax ? kk : kmax;
+    r.k[i] = ld_stream((const u32x4*)(base + ((uint32_t)kk * row + kcol)));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int kk = 32 * (i & 1) + 16 * (e >> 2) + 4 * w + (e & 3);
+    kk = kk < kmax ? kk : kmax;
+    r.v[i] = *(const u32x4*)(base + ((uint32_t)kk * row + vcol + 128u * (i >> 1)));
+  }
+}
+
+__device__ __forceinline__ int pk_page_id(const Params& p, const PkCur& x) {
+  const size_t idx = x.live ? (size_t)x.tl.seq * p.PPS + page_of(x.c * kPkChunk, p) : 0;
+  return p.page_indices[idx + opaque_zero()];
+}
+
+__device__ __forceinline__ void pk_store(uint8_t* stage, const PkRegs& r, int tid) {
+  const int w = tid >> 6, l = tid & 63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *(u32x4*)(stage + ((tid >> 4) + 16 * i) * kPkKRow + 16 * (tid & 15)) = r.k[i];
+  uint8_t* vt = stage + kPkKTile;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 t = transpose8x8_bf16(r.v[i], l);  // keys tau(w, 0..7) of dim d
+    const int d = 8 * ((l & 7) + 8 * (i >> 1)) + (l >> 3);
+    *(u32x4*)(vt + d * kPkVtRow + 16 * pk_vt_pos(d, 4 * (i & 1) + w)) = t;
+  }
+}
+
+struct PkRow {
+  f32x4 acc[8];  // O^T: dims 16 db + 4 j + r, row n
+  float m, l;
+  int pos;       // last visible key of this lane's row
+  bool ok;       // the row exists
+};
+
+// One 16-row block's softmax over 32 keys k0 ..: scores sc[kb] (keys k0 + 16 kb + 4 j + r of row n)
+// -> P^T for the PV step (k-slots in the tau order of the scores).
+__device__ __forceinline__ bf16x8 pk_softmax(const Params& p, const PkTile& tl, int k0, bool plain, const f32x4 sc[2],
+                                             PkRow& st, int j) {
+  float xs[2][4];
+  if (plain) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xs[kb][r] = sc[kb][r] * p.scale_log2;
+  } else {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sv = sc[kb][r];
+        float xv;
+        if (p.soft_cap > 0.f) {
+          const float t = sv * p.sm_scale;
+          xv = p.soft_cap * tanhf(t / p.soft_cap) * kLog2e;
+        } else {
+          xv = sv * p.scale_log2;
+        }
+        const int kt = k0 + 4 * j + 16 * kb + r;
+        const bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
+        if (masked) xv += p.mask_log2;
+        if (kt >= tl.kv_len) xv = -INFINITY;
+        xs[kb][r] = xv;
+      }
+  }
+  float mc = fmaxf(fmaxf(fmaxf(xs[0][0], xs[0][1]), fmaxf(xs[0][2], xs[0][3])),
+                   fmaxf(fmaxf(xs[1][0], xs[1][1]), fmaxf(xs[1][2], xs[1][3])));
+  mc = rows4_max(mc);
+  const bool grow = mc > st.m + kRescaleLog2;
+  if (__ballot(grow)) {
+    const float mn = grow ? mc : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
+    st.l *= alpha;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+    st.m = mn;
+  }
+  const float mu = st.m == -INFINITY ? 0.f : st.m;
+  float pr[2][4];
+  float lsum = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[kb][r] = __builtin_amdgcn_exp2f(xs[kb][r] - mu);
+      lsum += pr[kb][r];
+    }
+  st.l += lsum;
+  u32x4 pw;
+  pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
+  pw[1] = pack_bf16x2(pr[0][2], pr[0][3]);
+  pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
+  pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
+  return __builtin_bit_cast(bf16x8, pw);
+}
+
+// Row r = 64 wv + 16 rb + n of tile tl: its token (tile-relative) and whether it exists.
+__device__ __forceinline__ bool pk_row(const Params& p, const PkTile& tl, int r, int& tok, int& g, int& pos) {
+  tok = r / p.G;
+  g = r - tok * p.G;
+  pos = tl.kv_len - tl.q_len + tl.tok0 + tok;
+  return tok < tl.ntok && pos >= 0;
+}
+
+// Queries of the wave's four row blocks for tile tl (rows past the tile read its first row).
+__device__ __forceinline__ void pk_load_q(const Params& p, const PkTile& tl, int wv, int n, int j, bf16x8 q[4][4]) {
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    int tok, g, pos;
+    const bool ok = pk_row(p, tl, 64 * wv + 16 * rb + n, tok, g, pos);
+    const int qtok = ok ? tl.q_start + tl.tok0 + tok : tl.q_start;
+    const uint16_t* qp = p.q + ((size_t)qtok * p.Hq + tl.h * p.G + (ok ? g : 0)) * kD + 8 * j;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) q[rb][s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
+  }
+}
+
+// Row states at the start of tile tl.
+__device__ __forceinline__ void pk_begin(const Params& p, const PkTile& tl, PkRow st[4], int wv, int n) {
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    int tok, g, pos;
+    st[rb].ok = pk_row(p, tl, 64 * wv + 16 * rb + n, tok, g, pos);
+    st[rb].pos = pos;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st[rb].acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[rb].m = -INFINITY;
+    st[rb].l = 0.f;
+  }
+}
+
+// One chunk step from LDS stage `stage` for the wave's four row blocks, as two 32-key halves (QK^T,
+// softmax, PV each); when the next chunk step starts a new tile (next_q), its queries are loaded
+// into q once the last QK^T products have read them.
+__device__ __forceinline__ void pk_compute(const Params& p, const PkTile& tl, int c, const uint8_t* stage,
+                                           bf16x8 q[4][4], PkRow st[4], int wv, int n, int j, bool next_q,
+                                           const PkTile& ntl) {
+  const uint8_t* vt = stage + kPkKTile;
+  const int pos_min = tl.kv_len - tl.q_len + tl.tok0 + (64 * wv) / p.G;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    f32x4 sc[4][2];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) sc[rb][0] = sc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 ka[4][2];  // the half's K fragments, all read before its MFMAs
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        ka[s][kb] = *(const bf16x8*)(stage + (32 * hf + 16 * kb + n) * kPkKRow + (32 * s + 8 * j) * 2);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) sc[rb][kb] = mfma(ka[s][kb], q[rb][s], sc[rb][kb]);
+    if (hf == 1 && next_q) pk_load_q(p, ntl, wv, n, j, q);
+    const int k0 = c * kPkChunk + 32 * hf;
+    const bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 && k0 + 31 <= pos_min && k0 + 32 <= tl.kv_len;
+    bf16x8 pb[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) pb[rb] = pk_softmax(p, tl, k0, plain, sc[rb], st[rb], j);
+    bf16x8 va[8];  // the half's V^T fragments
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      const int row = 16 * db + n;
+      va[db] = *(const bf16x8*)(vt + row * kPkVtRow + 16 * pk_vt_pos(row, 4 * hf + j));
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) st[rb].acc[db] = mfma(va[db], pb[rb], st[rb].acc[db]);
+  }
+}
+
+// The tile's rows of this workgroup: written out (complete) or left as a partial (split).
+__device__ __forceinline__ void pk_finish(const Params& p, const PkTile& tl, PkRow st[4], bool complete, int b,
+                                          bool started_here, int wv, int n, int j) {
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const float lt = rows4_sum(st[rb].l);
+    const int r = 64 * wv + 16 * rb + n;
+    if (complete) {
+      if (!st[rb].ok) continue;
+      const int tok = r / p.G, g = r - tok * p.G;
+      const float inv = 1.f / lt;
+      uint16_t* op = p.out + ((size_t)(tl.q_start + tl.tok0 + tok) * p.Hq + tl.h * p.G + g) * kD + 4 * j;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        u32x2 w2;
+        w2[0] = pack_bf16x2(st[rb].acc[d][0] * inv, st[rb].acc[d][1] * inv);
+        w2[1] = pack_bf16x2(st[rb].acc[d][2] * inv, st[rb].acc[d][3] * inv);
+        *(u32x2*)(op + 16 * d) = w2;
+      }
+    } else {
+      const size_t slot = (size_t)partial_slot(b, started_here);
+      float* ap = p.pk_acc + (slot * kPkRows + r) * kD + 4 * j;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) *(f32x4*)(ap + 16 * d) = st[rb].acc[d];
+      if (j == 0) {
+        float* mp = p.pk_ml + (slot * kPkRows + r) * 2;
+        mp[0] = st[rb].m;
+        mp[1] = lt;
+      }
+    }
+  }
+}
+
+// Workgroup b describes the split tile whose last chunk step u it owns (thread 0).
+__device__ __forceinline__ void pk_describe(const Params& p, const PkTile& tl, long long first_unit, const Partition& pt,
+                                            int b) {
+  PkDesc* d = p.pk_desc + b;
+  d->q_start = tl.q_start + tl.tok0;
+  d->ntok = tl.ntok;
+  d->h = tl.h;
+  d->b0 = owner_of(first_unit, pt);
+#pragma unroll
+  for (int g = 0; g < 16; ++g) d->valid[g] = 1;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void rpa_prefill_kernel(Params p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = uni(tid >> 6);
+  const int n = lane & 15, j = lane >> 4;
+  const int b = blockIdx.x;
+  int err = 0;
+
+  // metadata of the first 256 sequences in one round trip (the attention kernel leaves prefill
+  // sequences to this kernel only when num_seqs <= 256)
+  constexpr int kWin = 4;
+  SeqInfo wsi[kWin];
+  int units[kWin];
+  const int ns_raw = p.num_seqs[0];
+  int kvv[kWin], c0[kWin], c1[kWin];
+#pragma unroll
+  for (int w = 0; w < kWin; ++w) {
+    kvv[w] = c0[w] = c1[w] = 0;
+    const int i = 64 * w + lane;
+    if (i < p.Nmax) {
+      kvv[w] = p.kv_lens[i];
+      c0[w] = p.cu_q_lens[i];
+      c1[w] = p.cu_q_lens[i + 1];
+    }
+  }
+  int nseq = uni(ns_raw);
+  nseq = nseq < 0 ? 0 : (nseq > p.Nmax ? p.Nmax : nseq);
+  if (nseq > 64 * kWin) return;
+  long long W = 0, tile_units[kWin];
+#pragma unroll
+  for (int w = 0; w < kWin; ++w) {
+    wsi[w] = SeqInfo{0, 0, 0, 0};
+    units[w] = 0;
+    if (nseq > 64 * w) {
+      wsi[w] = make_seq(p, kvv[w], c0[w], c1[w], 64 * w + lane < nseq, 0, err);
+      units[w] = pk_units_per_head(p, wsi[w].kv_len, wsi[w].q_len);
+    }
+    tile_units[w] = nseq > 64 * w ? (long long)wave_sum32(units[w] * p.Hkv) : 0;
+    W += tile_units[w];
+  }
+  const Partition pt = make_partition_fast(W, p.pk_grid);
+  const long long u0 = uni64(range_start(b, pt)), u1 = uni64(range_start(b + 1, pt));
+  if (W == 0 || u0 >= u1) return;
+
+  // the chunk step u0: its sequence (window scan), kv head, token block
+  PkCur cur;
+  {
+    long long off = 0;
+    int s = -1;
+    long long s_start = 0;
+#pragma unroll
+    for (int w = 0; w < kWin; ++w) {
+      if (s < 0 && u0 < off + tile_units[w]) {
+        const int cnt = units[w] * p.Hkv;
+        const int incl = wave_incl_scan32(cnt, lane);
+        const int idx = __popcll(__ballot(off + incl <= u0));
+        s = 64 * w + idx;
+        s_start = off + rl(incl - cnt, idx);
+      }
+      off += tile_units[w];
+    }
+    int un = 0;
+    pk_seq(wsi, units, s, cur.tl, un);
+    cur.units = un;
+    cur.live = true;
+    const int ul = (int)(u0 - s_start);
+    cur.tl.h = ul / un;
+    int rem = ul - cur.tl.h * un;
+    cur.tl.nt = (cur.tl.q_len + p.pf_tq - 1) / p.pf_tq;
+    cur.tl.t = 0;
+    for (;;) {
+      pk_range(p, cur.tl);
+      const int cnt = cur.tl.c_hi - cur.tl.c_lo;
+      if (rem < cnt) {
+        cur.c = cur.tl.c_lo + rem;
+        break;
+      }
+      rem -= cnt;
+      cur.tl.t++;
+    }
+  }
+  // first unit of cur's tile (for its split descriptor)
+  long long tile_first = u0 - (cur.c - cur.tl.c_lo);
+
+  auto ahead = [&](const PkCur& x, long long ux) {  // the cursor of chunk step ux + 1
+    PkCur y = x;
+    if (ux + 1 < u1)
+      pk_advance(p, wsi, units, nseq, y);
+    else
+      y.live = false;
+    return y;
+  };
+  // Pipeline invariant at the start of step u: LDS stage u & 1 holds chunk step u and pg_n1 is the
+  // page id of step u+1.  Step u loads the page id of u+2 and the data of u+1 (into registers),
+  // computes u, finishes u's tile if it ends there, stores u+1 to the other stage, barrier.
+  PkCur n1 = ahead(cur, u0);
+  int pg_n1;
+  PkRegs r;
+  {
+    const int pg_cur = pk_page_id(p, cur);
+    pg_n1 = pk_page_id(p, n1);
+    pk_load(p, cur, pg_cur, tid, r, err);
+  }
+  bf16x8 q[4][4];
+  PkRow st[4];
+  pk_load_q(p, cur.tl, wv, n, j, q);
+  pk_begin(p, cur.tl, st, wv, n);
+  bool started_here = cur.c == cur.tl.c_lo;
+  pk_store(smem + (u0 & 1) * kPkStage, r, tid);
+  __syncthreads();
+
+  for (long long u = u0;; ++u) {
+    const PkCur n2 = ahead(n1, u + 1);
+    const int pg_n2 = pk_page_id(p, n2);
+    pk_load(p, n1, pg_n1, tid, r, err);
+    const bool tile_end = cur.c + 1 >= cur.tl.c_hi;
+    const bool range_end = u + 1 >= u1;
+    pk_compute(p, cur.tl, cur.c, smem + (u & 1) * kPkStage, q, st, wv, n, j, tile_end && !range_end, n1.tl);
+    if (tile_end || range_end) {
+      const bool complete = started_here && tile_end;
+      pk_finish(p, cur.tl, st, complete, b, started_here, wv, n, j);
+      if (!complete && !started_here && tile_end && tid == 0) pk_describe(p, cur.tl, tile_first, pt, b);
+      if (range_end) break;
+      pk_begin(p, n1.tl, st, wv, n);  // the next tile starts here (its queries are loading)
+      started_here = true;
+      tile_first = u + 1;
+    }
+    pk_store(smem + ((u + 1) & 1) * kPkStage, r, tid);
+    __syncthreads();
+    cur = n1;
+    n1 = n2;
+    pg_n1 = pg_n2;
   }
   if (err) atomicOr(p.err, err);
 }
@@ -1839,15 +2400,61 @@ __device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*r
   if (t == 0) *flag = 0;
 }
 
+// Prefill merge workgroup idx: split tile pk_desc[b] (b = pk_grid - 1 - idx / 16), rows
+// 16 g .. 16 g + 15 (g = idx % 16).  The tile's partials [slot][256][kD] are sixteen 16-row
+// blocks, so the decode merge reads them as slots of 16 rows (slot * 16 + g); its rows map to
+// (token, q head) as the tile's rows do: row 16 g + i -> token tok0 + (16 g + i) / G, head
+// h G + (16 g + i) % G.
+__device__ __forceinline__ void combine_prefill(const Params& p, int idx, float (*red)[64][33], float (*redml)[64][16]) {
+  const int b = p.pk_grid - 1 - idx / 16, g = idx % 16;
+  int valid = p.pk_desc[b].valid[g];
+  PkDesc pd = p.pk_desc[b];
+  asm volatile("" : "+v"(valid), "+v"(pd.q_start), "+v"(pd.ntok), "+v"(pd.h), "+v"(pd.b0));
+  if (!__builtin_amdgcn_readfirstlane(valid)) return;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  SplitDesc d;
+  d.q_start = pd.q_start;
+  d.q_len = pd.ntok;
+  d.h = pd.h;
+  d.rb = g;
+  d.b0 = pd.b0;
+  Params pm = p;  // partial slots of 16 rows: slot * 16 + g
+  pm.part_acc = p.pk_acc;
+  pm.part_ml = p.pk_ml;
+  pm.HG = 16;
+  Params ps = p;  // output rows: head h * G + row % G
+  ps.HG = 1;
+  const int ncontrib = (int)(b - d.b0 + 1), nrows = rows_of(p, d);
+  if (nrows > 0 && nrows <= 4) {
+    MergeAcc<2> a;
+    merge_rows<2, 4, 2>(pm, d, g, ncontrib, wv, lane, 0, 0, a);
+    merge_waves_store<2, 2>(ps, d, 0, nrows, wv, lane, 0, 0, a, red, redml);
+  } else if (nrows > 0) {
+#pragma unroll 1
+    for (int row0 = 0; row0 < nrows; row0 += 8) {
+      MergeAcc<4> a;
+      merge_rows<4, 1, 2>(pm, d, g, ncontrib, wv, lane, row0, 0, a);
+      merge_waves_store<4, 2>(ps, d, 0, nrows, wv, lane, row0, 0, a, red, redml);
+    }
+  }
+  if (t == 0) p.pk_desc[b].valid[g] = 0;
+}
+
 // Workgroup b merges the row block described by desc[b] for head hw: contributors b0..b, b0's
 // share in slot 2*b0+1 and every later one's in slot 2*bb (merge_rows, merge_waves_store), unless
-// the block is heavy (its slot's helper workgroups merge it).
+// the block is heavy (its slot's helper workgroups merge it).  After the (descriptor, head)
+// workgroups come the heavy-merge helpers, then (with the prefill kernel) 16 per prefill
+// workgroup for its split tiles.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
   __shared__ float red[3][64][33];    // waves 1..3's o (33: conflict-free row stride)
   __shared__ float redml[3][64][16];  // waves 1..3's (m, l) per row slot
   if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
   if ((int)blockIdx.x >= p.grid * p.HG) {
-    combine_heavy(p, blockIdx.x - p.grid * p.HG, red, redml);
+    const int hb = blockIdx.x - p.grid * p.HG, nheavy = heavy_slots(p.grid) * p.HG * kHeavySlices;
+    if (hb < nheavy)
+      combine_heavy(p, hb, red, redml);
+    else
+      combine_prefill(p, hb - nheavy, red, redml);
     return;
   }
   // descriptor (last first: long splits end in late workgroups), wave (head) of its group
@@ -1991,11 +2598,11 @@ int device_info(DeviceInfo& out) {
 }
 
 // Workspace: [error word | pad to 256] [split descriptors, one per workgroup] [heavy-merge helper
-// flags] [partial m,l] [partial acc].  Header, descriptors and flags are zeroed once
-// (rpa_workspace_init); every call leaves each descriptor invalid and each flag clear again when
-// its combine has run.
+// flags and descriptors] [prefill split descriptors] [partial m,l] [partial acc] [prefill partial
+// m,l] [prefill partial acc].  Header, descriptors and flags are zeroed once (rpa_workspace_init);
+// every call leaves each descriptor invalid and each flag clear again when its combine has run.
 struct WsLayout {
-  size_t desc, heavy, heavy_desc, ml, acc, total;
+  size_t desc, heavy, heavy_desc, pk_desc, ml, acc, pk_ml, pk_acc, total;
 };
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
@@ -2006,9 +2613,13 @@ WsLayout ws_layout(const DeviceInfo& d) {
   w.desc = kHeaderBytes;
   w.heavy = w.desc + round256(gmax * sizeof(SplitDesc));
   w.heavy_desc = w.heavy + round256((size_t)heavy_slots((int)gmax) * 8 * kHeavySlices * sizeof(int32_t));
-  w.ml = w.heavy_desc + round256((size_t)heavy_slots((int)gmax) * sizeof(SplitDesc));
+  w.pk_desc = w.heavy_desc + round256((size_t)heavy_slots((int)gmax) * sizeof(SplitDesc));
+  const size_t pk = (size_t)d.cus;  // prefill-kernel workgroups: one per CU
+  w.ml = w.pk_desc + round256(pk * sizeof(PkDesc));
   w.acc = w.ml + round256(2 * gmax * ROW_BLOCK * 2 * sizeof(float));
-  w.total = w.acc + 2 * gmax * ROW_BLOCK * kD * sizeof(float);
+  w.pk_ml = w.acc + round256(2 * gmax * ROW_BLOCK * kD * sizeof(float));
+  w.pk_acc = w.pk_ml + round256(2 * pk * kPkRows * 2 * sizeof(float));
+  w.total = w.pk_acc + 2 * pk * kPkRows * kD * sizeof(float);
   return w;
 }
 
@@ -2348,9 +2959,10 @@ V1Layout v1_layout(const DeviceInfo& d, const rpa_inkling_shape_t* f) {
 // allocation-free entry (rpa_ragged_paged_attention_noalloc): the operator's workspace lives in a
 // file-scope device array, one copy per GPU, found with hipGetSymbolAddress once per device
 // ---------------------------------------------------------------------------------------------
-// Bytes of the array: the workspace of a device with up to 352 CUs (about 140 KiB per CU: split
-// descriptors, heavy-merge flags and split-K partials for a persistent grid of 8 waves per CU).
-constexpr size_t kScratchBytes = 48ull << 20;
+// Bytes of the array: the workspace of a device with up to 320 CUs (about 400 KiB per CU: split
+// descriptors, heavy-merge flags and split-K partials for a persistent grid of 8 waves per CU, and
+// the prefill kernel's 256-row tile partials for one workgroup per CU).
+constexpr size_t kScratchBytes = 128ull << 20;
 
 __global__ __launch_bounds__(256) void rpa_scratch_clear_kernel(u32x4* p, size_t n16) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
@@ -2458,7 +3070,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (opt->sliding_window < 0) return fail(RPA_E_INVALID, "sliding_window must be positive");
   if (opt->waves_per_cu < 0 || opt->waves_per_cu > kMaxWavesPerCU)
     return fail(RPA_E_INVALID, "waves_per_cu must be in [0, 8]");
-  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 1) return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0 or 1");
+  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 2)
+    return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0, 1 or 2");
   if (!(opt->prefill_cost >= 0.f && opt->prefill_cost <= 64.f))
     return fail(RPA_E_INVALID, "prefill_cost must be in [0, 64]");
   if (shape->num_tokens == 0 || shape->max_num_seqs == 0) return RPA_OK;
@@ -2486,6 +3099,9 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   p.heavy_desc = (SplitDesc*)((uint8_t*)workspace + w.heavy_desc);
   p.part_ml = (float*)((uint8_t*)workspace + w.ml);
   p.part_acc = (float*)((uint8_t*)workspace + w.acc);
+  p.pk_desc = (PkDesc*)((uint8_t*)workspace + w.pk_desc);
+  p.pk_ml = (float*)((uint8_t*)workspace + w.pk_ml);
+  p.pk_acc = (float*)((uint8_t*)workspace + w.pk_acc);
   p.sm_scale = opt->sm_scale;
   p.scale_log2 = opt->sm_scale * kLog2e;
   const float mask = opt->has_mask_value ? opt->mask_value : kDefaultMask;
@@ -2511,9 +3127,20 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (opt->has_k_scale || opt->has_v_scale) mode = KV_BF16_SCALED;
   }
   p.grid = grid_for_call(d, mode, p.HG, opt->waves_per_cu);
-  // prefill tiles: bf16 KV without scales, masked keys at weight 0, eight waves (kv heads) per
-  // workgroup
-  if (mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG && opt->prefill_tiles >= 0) {
+  // Sequences with >= 16 query tokens (bf16 KV without scales, masked keys at weight 0):
+  //   prefill_tiles 2, or 0 with eight kv heads per workgroup: the attention kernel's own prefill
+  //     tiles (measured faster on C3 than the prefill kernel: 187 us against 272 us for the call);
+  //   prefill_tiles 1, or 0 otherwise: the prefill kernel, when chunks lie in one page (page size a
+  //     multiple of 64);
+  //   otherwise, and with -1: causal row blocks of the stream-K role.
+  const bool tiles_ok = mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG;
+  const bool pk_ok = mode == KV_BF16 && p.skip_masked && p.G <= kPkRows && p.S % kPkChunk == 0;
+  if (pk_ok && (opt->prefill_tiles == 1 || (opt->prefill_tiles == 0 && !tiles_ok))) {
+    p.pf_kernel = true;
+    p.pf_tq = kPkRows / p.G;
+    p.pf_min = 16;
+    p.pk_grid = d.cus;
+  } else if (tiles_ok && opt->prefill_tiles >= 0) {
     p.pf_tq = 32 * p.HG / p.G;
     p.pf_min = 16;
     p.pf_cost = opt->prefill_cost > 0.f ? opt->prefill_cost : kPfCost;
@@ -2539,11 +3166,18 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("attention launch failed: ") + hipGetErrorString(e));
+  if (p.pf_kernel) {
+    hipLaunchKernelGGL(rpa_prefill_kernel, dim3(p.pk_grid), dim3(256), kPkLds, st, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(RPA_E_HIP, std::string("prefill launch failed: ") + hipGetErrorString(e));
+  }
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(end) failed");
-  // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot
-  hipLaunchKernelGGL(rpa_combine_kernel, dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices), dim3(256), 0,
-                     st, p);
+  // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot, then 16 per
+  // prefill workgroup
+  hipLaunchKernelGGL(rpa_combine_kernel,
+                     dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0)),
+                     dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
   return RPA_OK;

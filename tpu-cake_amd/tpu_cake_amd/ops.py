@@ -174,6 +174,11 @@ def _static_plan(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_sca
     cost = knobs["prefill_cost"] if knobs["prefill_cost"] is not None else tuned_knobs["prefill_cost"]
     if not (isinstance(wpc, int) and 0 <= wpc <= 8):
         raise ValueError(f"waves_per_cu={wpc!r} must be an int in [0, 8]")
+    # True / 0: the library's choice; 1: the prefill kernel; 2: the attention kernel's own prefill
+    # tiles; False / -1: causal row blocks of the stream-K role
+    tiles = {True: 0, False: -1}.get(tiles, tiles) if isinstance(tiles, bool) else tiles
+    if tiles not in (-1, 0, 1, 2):
+        raise ValueError(f"prefill_tiles={tiles!r} must be a bool or one of -1, 0, 1, 2")
     if not (0.0 <= float(cost) <= 64.0):
         raise ValueError(f"prefill_cost={cost!r} must be in [0, 64]")
     mask_value = knobs["mask_value"]
@@ -185,7 +190,7 @@ def _static_plan(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_sca
         1, float(mask_value),
         int(k_scale is not None), float(k_scale if k_scale is not None else 1.0),
         int(v_scale is not None), float(v_scale if v_scale is not None else 1.0),
-        int(wpc), 1 if tiles else -1, float(cost),
+        int(wpc), int(tiles), float(cost),
     )
     return shape, opts
 
@@ -217,7 +222,7 @@ def ragged_paged_attention(
     kernel_events: tuple | None = None,      # (begin, end) events around the attention kernel: torch.cuda.Event
                                              # or timing.KernelEvent (anything with a .cuda_event handle)
     waves_per_cu: int | None = None,         # tuning knobs (rpa_options_t); None = the tuned table's entry
-    prefill_tiles: bool | None = None,
+    prefill_tiles: bool | int | None = None, # 1 prefill kernel, 2 in-kernel tiles, True/0 either, False/-1 rows
     prefill_cost: float | None = None,
 ) -> torch.Tensor:
     """Ragged paged attention (mixed prefill and decode) on MI355X.

@@ -448,7 +448,7 @@ def _parse_candidate(text: str):
         k, _, v = item.partition("=")
         if k not in KNOBS:
             raise ValueError(f"unknown knob {k!r} (knobs: {', '.join(KNOBS)})")
-        knobs[k] = {"waves_per_cu": int, "prefill_cost": float}.get(k, lambda s: s.lower() in ("1", "true", "on"))(v)
+        knobs[k] = {"waves_per_cu": int, "prefill_cost": float, "prefill_tiles": int}[k](v)
     return name, knobs
 
 

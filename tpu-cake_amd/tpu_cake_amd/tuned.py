@@ -22,7 +22,7 @@ import pathlib
 DEVICE = "gfx950"
 TABLE_PATH = pathlib.Path(__file__).with_name(f"tuned_{DEVICE}.json")
 KNOBS = ("waves_per_cu", "prefill_tiles", "prefill_cost")
-DEFAULTS = {"waves_per_cu": 0, "prefill_tiles": True, "prefill_cost": 0.0}
+DEFAULTS = {"waves_per_cu": 0, "prefill_tiles": 0, "prefill_cost": 0.0}
 
 
 def next_power_of_2(x: int) -> int:
@@ -47,8 +47,10 @@ def validate_entry(entry: dict) -> dict:
     e = dict(DEFAULTS, **entry)
     if not (isinstance(e["waves_per_cu"], int) and 0 <= e["waves_per_cu"] <= 8):
         raise ValueError(f"waves_per_cu={e['waves_per_cu']!r} must be an int in [0, 8]")
-    if not isinstance(e["prefill_tiles"], bool):
-        raise ValueError(f"prefill_tiles={e['prefill_tiles']!r} must be a bool")
+    if isinstance(e["prefill_tiles"], bool):  # True: the library's choice; False: stream-K rows
+        e["prefill_tiles"] = 0 if e["prefill_tiles"] else -1
+    if e["prefill_tiles"] not in (-1, 0, 1, 2):
+        raise ValueError(f"prefill_tiles={e['prefill_tiles']!r} must be -1, 0, 1 or 2 (or a bool)")
     if not (isinstance(e["prefill_cost"], (int, float)) and 0.0 <= float(e["prefill_cost"]) <= 64.0):
         raise ValueError(f"prefill_cost={e['prefill_cost']!r} must be in [0, 64]")
     e["prefill_cost"] = float(e["prefill_cost"])
