@@ -266,6 +266,52 @@ def fused_bench(args, dev) -> int:
     return 0
 
 
+def host_submit(args, dev, calls: int = 400) -> int:
+    """Host time per call: ``calls`` back-to-back ops.ragged_paged_attention calls on C1 (kernels of
+    a few microseconds, so the host is the bound), wall time / calls, median of 5 batches; and the
+    same with the validation plan dropped each call (the first call of a new signature)."""
+    import statistics
+
+    import torch
+
+    from tpu_cake_amd import ops
+    from tpu_cake_amd.workloads import make_config
+
+    case = make_config("c1", seed=args.seed)
+    d = ops.case_to_device(case, dev)
+    out = torch.empty_like(d["q"])
+
+    def call():
+        ops.ragged_paged_attention(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
+                                   d["num_seqs"], sm_scale=case.sm_scale, out=out)
+
+    for _ in range(20):
+        call()
+    torch.cuda.synchronize()
+    res = {}
+    for label, cold in (("cached_plan", False), ("plan_each_call", True)):
+        per = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                if cold:
+                    ops._plans.clear()
+                call()
+            per.append((time.perf_counter() - t0) / calls * 1e6)
+            torch.cuda.synchronize()
+        res[label] = round(statistics.median(per), 2)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(calls):
+        call()
+    ev1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"host_submit_us_per_call": res, "device_us_per_call_back_to_back":
+                      round(ev0.elapsed_time(ev1) * 1e3 / calls, 2), "calls": calls,
+                      "workload": "c1 (kernels of a few us: the host is the bound)"}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -283,6 +329,9 @@ def main() -> int:
                     help="1: prefill kernel, 2: the attention kernel's own prefill tiles, -1: stream-K rows "
                          "(default: the tuned table)")
     ap.add_argument("--prefill-cost", type=float, default=None, help="schedule knob (default: the tuned table)")
+    ap.add_argument("--host-submit", action="store_true",
+                    help="instead of the benchmark, measure the host time to submit one call (C1 shapes, "
+                         "calls back to back, no synchronisation in between) and exit")
     ap.add_argument("--copy-probe", type=float, default=0.0, metavar="BYTES",
                     help="instead of the benchmark, run 5 device-to-device copies of BYTES (the known-size "
                          "kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -311,6 +360,9 @@ def main() -> int:
         gbps = copy_probe_gbps(dev, n)
         print(json.dumps({"copy_probe_bytes": n, "copies": 6, "achieved_gbps": round(gbps, 1)}))
         return 0
+
+    if args.host_submit:
+        return host_submit(args, dev)
 
     if args.config == "inkling":
         return fused_bench(args, dev)

@@ -37,7 +37,7 @@ def test_search_with_trace_runs_and_the_oracle_gate(cuda, tmp_path):
     assert res["winner"] is None  # no confirmation rounds were asked for
 
     class NoRuns:
-        def run(self, *a):
+        def run(self, *a, **k):
             raise AssertionError("a completed run was run again")
 
     again = search.run_search(tmp_path, c, runner=NoRuns(), checker=evidence_run.oracle_checker)

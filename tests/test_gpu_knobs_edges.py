@@ -238,3 +238,16 @@ def test_prefill_kernel_back_to_back_calls_leave_no_state(cuda):
         d = ops.case_to_device(case, "cuda")
         _assert_close(_run(d, case, prefill_tiles=1), _ref(case), f"call {i}")
     assert ops.read_error_word() == 0
+
+
+def test_metadata_on_the_host_is_rejected_after_a_cached_call(cuda):
+    """The wrapper caches its checks per call signature; the signature includes every tensor's
+    device, so metadata moved to the host after a valid call is refused before any launch."""
+    _say("host metadata after a cached call")
+    case = make_custom(kv_lens=[100, 30], q_lens=[1, 1], num_q_heads=8, num_kv_heads=2, page_size=16, seed=501)
+    d = ops.case_to_device(case, "cuda")
+    _run(d, case)
+    bad = dict(d, kv_lens=d["kv_lens"].cpu())
+    with pytest.raises(ValueError, match="kv_lens must be on a GPU"):
+        _run(bad, case)
+    _assert_close(_run(d, case), _ref(case), "after the refusal")

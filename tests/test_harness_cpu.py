@@ -139,14 +139,16 @@ class _FakeRunner:
     def __init__(self, case, times):
         self.case, self.times, self.calls = case, times, []
 
-    def run(self, run_root, contract, knobs):
+    def run(self, run_root, contract, knobs, save_output=False):
         self.calls.append(str(run_root))
         run_root.mkdir(parents=True, exist_ok=True)
         cost = knobs["prefill_cost"]
+        out = np.full(4, 7 if cost != 0.7 else 9, np.uint16)
         (run_root / "steps.json").write_text(json.dumps({
             "identity": {"kernel_source_digest": "k", "library_sha256": "l"}, "input_sha256": self.case.sha(),
-            "config": contract.config, "knobs": knobs}))
-        np.save(run_root / "output.npy", np.full(4, 7 if cost != 0.7 else 9, np.uint16))
+            "config": contract.config, "knobs": knobs, "output_sha256": hashlib.sha256(out.tobytes()).hexdigest()}))
+        if save_output:
+            np.save(run_root / "output.npy", out)
         n = len(self.calls)
         _trace_csv(run_root / "trace" / "h" / "run_kernel_trace.csv",
                    [(self.times[cost] + (n % 3), 10)] * (contract.warmup + contract.steps))
@@ -194,10 +196,12 @@ def test_search_refuses_a_candidate_whose_output_changes(tmp_path):
                   steps=3, warmup=0)
 
     class Flaky(_FakeRunner):
-        def run(self, run_root, contract, knobs):
-            super().run(run_root, contract, knobs)
+        def run(self, run_root, contract, knobs, save_output=False):
+            super().run(run_root, contract, knobs, save_output)
             if "round-01" in str(run_root) and knobs["prefill_cost"] == 0.25:
-                np.save(run_root / "output.npy", np.full(4, 8, np.uint16))
+                st = json.loads((run_root / "steps.json").read_text())
+                st["output_sha256"] = hashlib.sha256(np.full(4, 8, np.uint16).tobytes()).hexdigest()
+                (run_root / "steps.json").write_text(json.dumps(st))
 
     with pytest.raises(ValueError, match="CANDIDATE_OUTPUT_MISMATCH"):
         search.run_search(tmp_path, c, runner=Flaky(case, {0.0: 100, 0.25: 90}), checker=_checker, case=case)
@@ -345,3 +349,12 @@ def test_profile_summaries_regenerate_identically(tmp_path):
     assert c2["mfma"]["mfma_busy_fraction"] == round(2.0e7 / (2.1e5 / 8 * 1024), 4)
     md = (a / "rpa_attn_c2.md").read_text()
     assert "rocprofv3 --kernel-trace --stats -d gpurun_out/prof/prof_c2" in md and "| rpa_attn_kernel | 23 | 102.91" in md
+
+
+def test_search_summary_markdown(tmp_path):
+    case = _Case()
+    c = _contract(candidates=(("incumbent", {}), ("pf25", {"prefill_cost": 0.25})), rounds=4, confirmation_rounds=2,
+                  steps=3, warmup=0)
+    res = search.run_search(tmp_path, c, runner=_FakeRunner(case, {0.0: 100, 0.25: 90}), checker=_checker, case=case)
+    md = search.summary_markdown(res, "python -m tpu_cake_amd.search ...")
+    assert "| pf25 |" in md and "confirmed winner: pf25" in md and "Confirmation (2 paired rounds)" in md

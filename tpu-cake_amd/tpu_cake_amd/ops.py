@@ -122,6 +122,41 @@ def make_shape(q, kv_pages, page_indices) -> _lib.RpaShape:
     return _lib.RpaShape(T, Hq, C // 2, D, P, S, n_max, pps, kvd)
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(dev: int) -> int:
+    """The current stream's raw handle on device ``dev`` (torch's internal accessor when present:
+    no Stream object per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev)
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+_ws_fast: dict[tuple[int, int], tuple[int, int]] = {}
+
+
+def _workspace_ptr(shape: _lib.RpaShape, dev: int, stream: int) -> tuple[int, int]:
+    """(pointer, bytes) of the cached workspace of (device, stream)."""
+    hit = _ws_fast.get((dev, stream))
+    if hit is None:
+        ws = workspace_for(shape, torch.device("cuda", dev), stream)
+        hit = _ws_fast[(dev, stream)] = (ws.data_ptr(), ws.numel())
+    return hit
+
+
+_fns: tuple | None = None
+
+
+def _entry_points() -> tuple:
+    """(rpa_ragged_paged_attention, rpa_ragged_paged_attention_timed) of the loaded library."""
+    global _fns
+    if _fns is None:
+        lib = _lib.load()
+        _fns = (lib.rpa_ragged_paged_attention, lib.rpa_ragged_paged_attention_timed)
+    return _fns
+
+
 def workspace_for(shape: _lib.RpaShape, device: torch.device, stream: int) -> torch.Tensor:
     """Cached per-(device, stream) workspace; calls that share one must not overlap.  Its size
     depends only on the device (the persistent grid), so it is asked for once per device."""
@@ -138,6 +173,7 @@ def workspace_for(shape: _lib.RpaShape, device: torch.device, stream: int) -> to
         ws = torch.empty(need, dtype=torch.uint8, device=device)
         _lib.check(lib.rpa_workspace_init(ws.data_ptr(), ws.numel(), stream))
         _workspaces[(index, stream)] = ws
+        _ws_fast.pop((index, stream), None)
     return ws
 
 
@@ -233,9 +269,12 @@ def ragged_paged_attention(
     and have no effect; the schedule knobs ``waves_per_cu`` / ``prefill_tiles`` /
     ``prefill_cost`` take their place (``tpu_cake_amd.tuned`` holds per-shape values).
     """
-    sig = (q.shape, q.dtype, q.device, kv_pages.shape, kv_pages.dtype, kv_pages.device, kv_lens.shape, kv_lens.dtype,
-           page_indices.shape, page_indices.dtype, cu_q_lens.shape, cu_q_lens.dtype, num_seqs.shape, num_seqs.dtype,
-           None if kv_scales is None else (kv_scales.shape, kv_scales.dtype, kv_scales.device),
+    dev = q.get_device()  # -1 for a CPU tensor: rejected by the plan's checks
+    sig = (q.shape, q.dtype, dev, kv_pages.shape, kv_pages.dtype, kv_pages.get_device(), kv_lens.shape,
+           kv_lens.dtype, kv_lens.get_device(), page_indices.shape, page_indices.dtype, page_indices.get_device(),
+           cu_q_lens.shape, cu_q_lens.dtype, cu_q_lens.get_device(), num_seqs.shape, num_seqs.dtype,
+           num_seqs.get_device(),
+           None if kv_scales is None else (kv_scales.shape, kv_scales.dtype, kv_scales.get_device()),
            sm_scale, sliding_window, soft_cap, mask_value, k_scale, v_scale, num_kv_pages_per_block,
            num_queries_per_block, vmem_limit_bytes, waves_per_cu, prefill_tiles, prefill_cost)
     plan = _plans.get(sig)
@@ -259,12 +298,11 @@ def ragged_paged_attention(
                 _require_cuda(name, t)
     if out is None:
         out = torch.empty_like(q)
-    elif (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or not out.is_contiguous()
+    elif (out.shape != q.shape or out.dtype != q.dtype or out.get_device() != dev or not out.is_contiguous()
           or out.data_ptr() == q.data_ptr()):
         raise ValueError("out must be a separate contiguous tensor shaped like q on q's device")
-    device = q.device
-    if device.index != torch.cuda.current_device():
-        with torch.cuda.device(device):
+    if dev != torch.cuda.current_device():
+        with torch.cuda.device(dev):
             return ragged_paged_attention(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, sm_scale=sm_scale,
                                           sliding_window=sliding_window, soft_cap=soft_cap, mask_value=mask_value,
                                           k_scale=k_scale, v_scale=v_scale,
@@ -273,20 +311,20 @@ def ragged_paged_attention(
                                           vmem_limit_bytes=vmem_limit_bytes, kv_scales=kv_scales, out=out,
                                           kernel_events=kernel_events, waves_per_cu=waves_per_cu,
                                           prefill_tiles=prefill_tiles, prefill_cost=prefill_cost)
-    stream = torch.cuda.current_stream(device).cuda_stream
-    ws = workspace_for(shape, device, stream)
-    lib = _lib.load()
+    stream = _current_stream(dev)
+    ws_ptr, ws_bytes = _workspace_ptr(shape, dev, stream)
+    fn = _entry_points()
     args = (shape, opts, q.data_ptr(), kv_pages.data_ptr(),
             kv_scales.data_ptr() if kv_scales is not None else None,
             kv_lens.data_ptr(), page_indices.data_ptr(), cu_q_lens.data_ptr(), num_seqs.data_ptr(),
-            out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+            out.data_ptr(), ws_ptr, ws_bytes, stream)
     if kernel_events is None:
-        rc = lib.rpa_ragged_paged_attention(*args)
+        rc = fn[0](*args)
     else:
         begin, end = kernel_events
         if not begin.cuda_event or not end.cuda_event:
             raise ValueError("kernel_events must be recorded once before use (HIP events are created lazily)")
-        rc = lib.rpa_ragged_paged_attention_timed(*args, begin.cuda_event, end.cuda_event)
+        rc = fn[1](*args, begin.cuda_event, end.cuda_event)
     if rc:
         _lib.check(rc)
     return out

@@ -16,10 +16,10 @@ parameters are the per-call knobs of ``rpa_options_t`` (``waves_per_cu``, ``pref
   attention and combine dispatch durations of each measured call -- as the reference takes its
   from the XProf device events (``_device_timing``, :228-265); ``device_timing.json`` must replay
   from the trace (``RPA_SEARCH_DEVICE_TIMING_REPLAY_MISMATCH``).
-* **correctness gate**: before the squares each candidate runs once (``gate/NN-name``) and the
-  caller's checker judges its output (the reference's run gate, :610-631); a failing candidate is
-  dropped and never timed.  Every later run of a candidate must reproduce the gated output bits
-  (its sha256; the reference pins the output hash per candidate, :418-429).
+* **correctness gate**: before the squares each candidate runs once (``gate/NN-name``, which keeps
+  its output) and the caller's checker judges that output (the reference's run gate, :610-631); a
+  failing candidate is dropped and never timed.  Every later run of a candidate must reproduce the
+  gated output bits (their sha256; the reference pins the output hash per candidate, :418-429).
 * **statistics** (:266-327): per round, the candidate's run median is paired with the baseline's run
   median of the same round, improvement = (baseline - candidate) / baseline; a bootstrap of the
   median of those paired improvements gives a 95% interval, and a candidate is promotable when the
@@ -279,12 +279,14 @@ class TraceRunner:
     def __init__(self, rocprof: str = "rocprofv3", timeout_s: int = 300):
         self.rocprof, self.timeout_s = rocprof, timeout_s
 
-    def run(self, run_root: pathlib.Path, contract: SearchContract, knobs: dict) -> None:
+    def run(self, run_root: pathlib.Path, contract: SearchContract, knobs: dict, save_output: bool = False) -> None:
         run_root.mkdir(parents=True, exist_ok=True)
         pkg = pathlib.Path(__file__).resolve().parent
         child = [sys.executable, "-m", "tpu_cake_amd.search", "_run", "--config", contract.config,
                  "--knobs", json.dumps(knobs, sort_keys=True), "--steps", str(contract.steps),
                  "--warmup", str(contract.warmup), "--out", str(run_root)]
+        if save_output:
+            child.append("--save-output")
         if contract.seed is not None:
             child += ["--seed", str(contract.seed)]
         env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
@@ -295,14 +297,17 @@ class TraceRunner:
         subprocess.run(cmd, check=True, env=env, stdout=subprocess.DEVNULL)
 
 
-def _child_run(config: str, knobs: dict, steps: int, warmup: int, out: pathlib.Path, seed) -> None:
-    """The child process of a run: the steps, their identity and the output's bits."""
+def _child_run(config: str, knobs: dict, steps: int, warmup: int, out: pathlib.Path, seed,
+               save_output: bool) -> None:
+    """The child process of a run: the steps, their identity, the output's sha256 and (gate runs) the
+    output's bits."""
     from . import evidence
 
     res, case, o = evidence._steps(config, steps, warmup, events=False, seed=seed, knobs=knobs)
-    import torch
+    if save_output:
+        import torch
 
-    np.save(out / "output.npy", o.view(torch.int16).cpu().numpy().view(np.uint16))
+        np.save(out / "output.npy", o.view(torch.int16).cpu().numpy().view(np.uint16))
     res["identity"] = evidence.source_identity()
     (out / "steps.json").write_text(json.dumps(res, sort_keys=True) + "\n")
 
@@ -314,10 +319,11 @@ def load_output(run_root: pathlib.Path) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------- the search
-def run_search(root, contract: SearchContract, *, runner, checker, case=None) -> dict:
+def run_search(root, contract: SearchContract, *, runner, checker, case=None, keep_outputs: bool = False) -> dict:
     """Run (or resume) a search; ``checker(case, output_f32) -> {"passed": bool, ...}`` is the
-    correctness gate (``case`` defaults to the configuration's workload, built once here).
-    Writes ``result.json`` under ``root`` and returns it."""
+    correctness gate (``case`` defaults to the configuration's workload, built once here).  A gate
+    run's output is deleted once its verdict is written (its sha256 stays in ``steps.json``) unless
+    ``keep_outputs``.  Writes ``result.json`` under ``root`` and returns it."""
     root = pathlib.Path(root).resolve()
     root.mkdir(parents=True, exist_ok=True)
     cpath = root / "contract.json"
@@ -340,7 +346,7 @@ def run_search(root, contract: SearchContract, *, runner, checker, case=None) ->
             raise ValueError(f"RPA_SEARCH_EXECUTION_IDENTITY_MISMATCH run={run_root.relative_to(root)}")
         if steps["knobs"] != contract.knobs(name):
             raise ValueError(f"RPA_SEARCH_KNOB_MISMATCH run={run_root.relative_to(root)}")
-        out_sha = _sha256(run_root / "output.npy")
+        out_sha = steps["output_sha256"]
         if name in identities and identities[name] != out_sha:
             raise ValueError(f"RPA_SEARCH_CANDIDATE_OUTPUT_MISMATCH candidate={name}")
         identities.setdefault(name, out_sha)
@@ -353,14 +359,14 @@ def run_search(root, contract: SearchContract, *, runner, checker, case=None) ->
             raise ValueError(f"RPA_SEARCH_DEVICE_TIMING_REPLAY_MISMATCH candidate={name}")
         return timing
 
-    def ensure_run(rel: str, name: str) -> DeviceTiming:
+    def ensure_run(rel: str, name: str, save_output: bool = False) -> DeviceTiming:
         run_root = root / rel
         if (run_root / "result.json").exists():
             return validate_run(run_root, name)
         if run_root.exists():
             archive_incomplete_run(root, run_root, "incomplete run found during resume")
         try:
-            runner.run(run_root, contract, contract.knobs(name))
+            runner.run(run_root, contract, contract.knobs(name), save_output=save_output)
             timing = validate_run(run_root, name)
         except Exception as err:
             if run_root.exists():
@@ -381,7 +387,7 @@ def run_search(root, contract: SearchContract, *, runner, checker, case=None) ->
                               + case.page_indices.tobytes()).hexdigest()
     for pos, name in enumerate(contract.names):
         rel = f"gate/{pos:02d}-{name}"
-        ensure_run(rel, name)
+        ensure_run(rel, name, save_output=True)
         if shared["input_sha256"] != case_sha:
             raise ValueError("RPA_SEARCH_INPUT_IDENTITY_MISMATCH: the checker's case is not the runs' input")
         verdict_path = root / rel / "correctness.json"
@@ -390,6 +396,8 @@ def run_search(root, contract: SearchContract, *, runner, checker, case=None) ->
         else:
             verdict = dict(checker(case, load_output(root / rel)))
             verdict_path.write_text(json.dumps(verdict, indent=1, sort_keys=True, default=float) + "\n")
+            if not keep_outputs:
+                (root / rel / "output.npy").unlink()
         gate[name] = verdict
     if not gate[contract.baseline].get("passed"):
         raise ValueError(f"RPA_SEARCH_BASELINE_FAILED_CORRECTNESS {gate[contract.baseline]}")
@@ -441,6 +449,37 @@ def promote(result: dict, *, path=None) -> str | None:
     return key
 
 
+def summary_markdown(result: dict, command: str) -> str:
+    """A short summary of a search result (for profiles/): protocol, per-candidate statistics,
+    confirmation and the correctness gate."""
+    c = result["contract"]
+    lines = [f"# Knob search on {c['config']} (search id {result['search_id'][:16]})", "",
+             f"Command: `{command}`", "",
+             f"Protocol: {len(c['candidates'])} candidates, {c['rounds']} rounds (forward + reversed Latin squares), "
+             f"{c['confirmation_rounds']} confirmation rounds, {c['warmup']} warmup + {c['steps']} measured calls per "
+             f"run, every run a rocprofv3-traced process (device time per call = attention + combine dispatches), "
+             f"paired per-round improvements, bootstrap 95% interval ({c['bootstrap_samples']} samples), "
+             f"promotion above {c['minimum_practical_improvement']:.0%}.", "",
+             "| candidate | knobs | gate max-abs | runs | median call (us) | paired improvement | 95% CI | promotable |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, knobs in c["candidates"]:
+        gate = result["correctness"].get(name, {})
+        st = result["statistics"].get(name)
+        if st is None:
+            lines.append(f"| {name} | {knobs} | {gate.get('max_abs', float('nan')):.2e} (rejected) | - | - | - | - | - |")
+            continue
+        lo, hi = st["improvement_ci95"]
+        lines.append(f"| {name} | {knobs} | {gate.get('max_abs', float('nan')):.2e} | {st['runs']} | "
+                     f"{st['median_ns'] / 1e3:.2f} | {st['improvement']:+.2%} | [{lo:+.2%}, {hi:+.2%}] | "
+                     f"{'yes' if st['promotable'] else 'no'} |")
+    conf = result.get("confirmation")
+    lines += ["", f"Provisional winner: {result['provisional_winner']}; confirmed winner: {result['winner']}."]
+    if conf:
+        lo, hi = conf["improvement_ci95"]
+        lines.append(f"Confirmation ({conf['runs']} paired rounds): {conf['improvement']:+.2%} [{lo:+.2%}, {hi:+.2%}].")
+    return "\n".join(lines) + "\n"
+
+
 def _parse_candidate(text: str):
     name, _, rest = text.partition(":")
     knobs = {}
@@ -471,6 +510,7 @@ def main(argv=None) -> int:
     r.add_argument("--warmup", type=int, required=True)
     r.add_argument("--seed", type=int, default=None)
     r.add_argument("--out", required=True)
+    r.add_argument("--save-output", action="store_true")
     ap.add_argument("--config", default="c3")
     ap.add_argument("--root")
     ap.add_argument("--checker", help="a Python file defining oracle_checker(case, output) (the correctness gate)")
@@ -482,9 +522,10 @@ def main(argv=None) -> int:
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--bootstrap-samples", type=int, default=10_000)
     ap.add_argument("--promote", action="store_true", help="write a confirmed winner into the tuned table")
+    ap.add_argument("--summary", help="also write a markdown summary of the result to this path")
     a = ap.parse_args(argv)
     if a.cmd == "_run":
-        _child_run(a.config, json.loads(a.knobs), a.steps, a.warmup, pathlib.Path(a.out), a.seed)
+        _child_run(a.config, json.loads(a.knobs), a.steps, a.warmup, pathlib.Path(a.out), a.seed, a.save_output)
         return 0
     if not (a.root and a.checker and a.candidate):
         ap.error("--root, --checker and --candidate are required")
@@ -494,6 +535,9 @@ def main(argv=None) -> int:
                               seed=a.seed, warmup=a.warmup, steps=a.steps, bootstrap_samples=a.bootstrap_samples)
     res = run_search(a.root, contract, runner=TraceRunner(), checker=_load_checker(a.checker))
     key = promote(res) if a.promote else None
+    if a.summary:
+        pathlib.Path(a.summary).write_text(summary_markdown(res, "python -m tpu_cake_amd.search " + " ".join(
+            argv if argv is not None else sys.argv[1:])))
     print(json.dumps({"winner": res["winner"], "provisional_winner": res["provisional_winner"],
                       "rejected": res["rejected_candidates"], "promoted_key": key,
                       "medians_ns": {k: v["median_ns"] for k, v in res["statistics"].items()}}, sort_keys=True))
