@@ -154,11 +154,11 @@ int rpa_ragged_paged_attention_timed(const rpa_shape_t* shape, const rpa_options
  * for callers that cannot allocate or pass device memory -- code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc.  Same arguments, kernels and results (bitwise)
  * as rpa_ragged_paged_attention, minus the workspace: that lives in a file-scope device array of
- * 48 MiB which each GPU the library is loaded on holds until the process ends.  The call allocates
+ * 128 MiB which each GPU the library is loaded on holds until the process ends.  The call allocates
  * nothing (no hipMalloc / hipFree); on its first call on a device it resolves that device's copy
  * of the array and clears its header with a fill kernel on `stream`, so that first call must not
  * be under graph capture (RPA_E_INVALID; later calls may be).  Returns RPA_E_WORKSPACE if
- * the device needs more workspace than the array holds (more than 352 compute units).  Every call
+ * the device needs more workspace than the array holds (more than 320 compute units).  Every call
  * on a GPU shares that GPU's array: calls that overlap in time on one GPU (other streams, other
  * threads) race and must be ordered by the caller.  The device error word of these calls lives in
  * the array and is not readable; callers validate metadata on the host. */
