@@ -82,26 +82,37 @@ def test_contract_rejections(kw, msg):
 
 
 def _trace_csv(path, durations_by_call):
+    """A kernel trace of calls given as (attention, prefill, combine) durations (0: not dispatched)."""
     path.parent.mkdir(parents=True, exist_ok=True)
     rows = ['"Kind","Dispatch_Id","Kernel_Name","Start_Timestamp","End_Timestamp"']
-    t = 1000
-    for i, (a, c) in enumerate(durations_by_call):
-        rows.append(f'"KERNEL_DISPATCH",{2 * i},"void rpa::(anonymous namespace)::rpa_attn_kernel<0, true>(Params)",'
-                    f'{t},{t + a}')
-        t += a + 7
-        rows.append(f'"KERNEL_DISPATCH",{2 * i + 1},"rpa::(anonymous namespace)::rpa_combine_kernel(Params)",{t},{t + c}')
-        t += c + 50
+    names = ("void rpa::(anonymous namespace)::rpa_attn_kernel<0, true>(Params)",
+             "rpa::(anonymous namespace)::rpa_prefill_kernel(Params)",
+             "rpa::(anonymous namespace)::rpa_combine_kernel(Params)")
+    t, did = 1000, 0
+    for i, durs in enumerate(durations_by_call):
+        for name, d in zip(names, durs):
+            if d:
+                rows.append(f'"KERNEL_DISPATCH",{did},"{name}",{t},{t + d}')
+                did += 1
+                t += d + 7
         rows.append(f'"KERNEL_DISPATCH",{900 + i},"__amd_rocclr_copyBuffer",{t},{t + 3}')
-        t += 10
+        t += 50
     path.write_text("\n".join(rows) + "\n")
 
 
 def test_device_timing_from_the_kernel_trace(tmp_path):
-    _trace_csv(tmp_path / "trace" / "x" / "run_kernel_trace.csv", [(500, 50)] * 2 + [(100 + i, 10) for i in range(4)])
+    _trace_csv(tmp_path / "trace" / "x" / "run_kernel_trace.csv", [(500, 0, 50)] * 2 + [(100 + i, 0, 10) for i in range(4)])
     t = search.device_timing(tmp_path, 4)  # the last 4 calls, attention + combine each
     assert t.durations_ns == (110.0, 111.0, 112.0, 113.0) and t.median_ns == 111.5
     with pytest.raises(ValueError, match="DISPATCH_PROTOCOL"):
         search.device_timing(tmp_path, 7)
+    # calls with the prefill kernel: attention + prefill + combine each
+    _trace_csv(tmp_path / "pk" / "run_kernel_trace.csv", [(100 + i, 40, 10) for i in range(3)])
+    assert search.device_timing(tmp_path / "pk", 3).durations_ns == (150.0, 151.0, 152.0)
+    # calls that dispatch different kernel sequences are not one protocol
+    _trace_csv(tmp_path / "mix" / "run_kernel_trace.csv", [(100, 0, 10), (100, 40, 10)])
+    with pytest.raises(ValueError, match="DISPATCH_PROTOCOL"):
+        search.device_timing(tmp_path / "mix", 2)
 
 
 def test_incomplete_run_is_archived_with_a_manifest(tmp_path):
@@ -151,7 +162,7 @@ class _FakeRunner:
             np.save(run_root / "output.npy", out)
         n = len(self.calls)
         _trace_csv(run_root / "trace" / "h" / "run_kernel_trace.csv",
-                   [(self.times[cost] + (n % 3), 10)] * (contract.warmup + contract.steps))
+                   [(self.times[cost] + (n % 3), 0, 10)] * (contract.warmup + contract.steps))
 
 
 def _checker(case, out):

@@ -83,8 +83,9 @@ def source_identity() -> dict:
 
 # --------------------------------------------------------------------------- profiles
 def _kernel_key(name: str) -> str | None:
-    for k in ("rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_prep_kernel", "rpa_inkling_v1_prep_kernel",
-              "rpa_fused_unpad_kernel", "rpa_scratch_clear_kernel", "__amd_rocclr_copyBuffer"):
+    for k in ("rpa_attn_kernel", "rpa_prefill_kernel", "rpa_combine_kernel", "rpa_fused_prep_kernel",
+              "rpa_inkling_v1_prep_kernel", "rpa_fused_unpad_kernel", "rpa_scratch_clear_kernel",
+              "__amd_rocclr_copyBuffer"):
         if k in name:
             return k
     return None

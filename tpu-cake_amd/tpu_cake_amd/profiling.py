@@ -74,6 +74,7 @@ def run_profiles(raw: str, configs=CONFIGS, limit_s: int = 120) -> None:
     """Run every pass (GPU box).  Stops at the first failing pass; the trace passes' bench lines go
     to ``RAW/prof_<config>.out``."""
     env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    raw = str(pathlib.Path(raw).resolve())  # the passes run from the repository root
     pathlib.Path(raw).mkdir(parents=True, exist_ok=True)
     for name, argv in commands(raw, configs):
         argv = [sys.executable if a == "python3" else a for a in argv]

@@ -13,7 +13,7 @@ parameters are the per-call knobs of ``rpa_options_t`` (``waves_per_cu``, ``pref
 * **runs**: one per (round, position), ``round-RR/PP-name``, each a fresh child process under
   ``rocprofv3 --kernel-trace`` running warmup + measured calls of the configuration with the
   candidate's knobs.  The objective is the DEVICE time per call taken from that trace -- the
-  attention and combine dispatch durations of each measured call -- as the reference takes its
+  dispatch durations of each measured call's kernels -- as the reference takes its
   from the XProf device events (``_device_timing``, :228-265); ``device_timing.json`` must replay
   from the trace (``RPA_SEARCH_DEVICE_TIMING_REPLAY_MISMATCH``).
 * **correctness gate**: before the squares each candidate runs once (``gate/NN-name``, which keeps
@@ -207,13 +207,14 @@ def confirmation_statistics(contract: SearchContract, candidate: str, orders, ba
 
 
 # --------------------------------------------------------------------------- run artifacts
-CALL_KERNELS = ("rpa_attn_kernel", "rpa_combine_kernel")
+CALL_KERNELS = ("rpa_attn_kernel", "rpa_prefill_kernel", "rpa_combine_kernel")
 
 
 def device_timing(run_root: pathlib.Path, steps: int) -> DeviceTiming:
-    """Device time per measured call from the run's rocprofv3 kernel trace: every call dispatches
-    the attention kernel then the combine kernel; the last ``steps`` calls are the measured ones,
-    and a call's time is the sum of its two dispatch durations."""
+    """Device time per measured call from the run's rocprofv3 kernel trace: a call is an attention
+    dispatch and the call's other dispatches up to the next one (the prefill kernel and its
+    combine, when the call uses them); the last ``steps`` calls are the measured ones, and a call's
+    time is the sum of its dispatch durations."""
     traces = sorted(pathlib.Path(run_root).rglob("*kernel_trace.csv"))
     if len(traces) != 1:
         raise ValueError(f"RPA_SEARCH_TRACE_COUNT_MISMATCH path={run_root} traces={len(traces)}")
@@ -224,13 +225,18 @@ def device_timing(run_root: pathlib.Path, steps: int) -> DeviceTiming:
         if kind is not None:
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), kind))
     rows.sort()
-    kinds = [k for _, _, k in rows]
-    if len(rows) < 2 * steps or kinds != list(CALL_KERNELS) * (len(rows) // 2) or len(rows) % 2:
-        raise ValueError(f"RPA_SEARCH_DISPATCH_PROTOCOL_MISMATCH path={run_root} dispatches={len(rows)} "
-                         f"expected a multiple of 2 >= {2 * steps}")
-    tail = rows[-2 * steps:]
-    return DeviceTiming.of([(tail[2 * i][1] - tail[2 * i][0]) + (tail[2 * i + 1][1] - tail[2 * i + 1][0])
-                            for i in range(steps)])
+    calls: list[list] = []
+    for start, end, kind in rows:
+        if kind == CALL_KERNELS[0]:
+            calls.append([])
+        elif not calls:
+            raise ValueError(f"RPA_SEARCH_DISPATCH_PROTOCOL_MISMATCH path={run_root} {kind} before any attention")
+        calls[-1].append((kind, end - start))
+    shapes = {tuple(k for k, _ in c) for c in calls}
+    if len(calls) < steps or len(shapes) != 1:
+        raise ValueError(f"RPA_SEARCH_DISPATCH_PROTOCOL_MISMATCH path={run_root} calls={len(calls)} "
+                         f"expected >= {steps} of one dispatch sequence, got {sorted(shapes)}")
+    return DeviceTiming.of([sum(d for _, d in c) for c in calls[-steps:]])
 
 
 def _sha256(path: pathlib.Path) -> str:
@@ -457,7 +463,7 @@ def summary_markdown(result: dict, command: str) -> str:
              f"Command: `{command}`", "",
              f"Protocol: {len(c['candidates'])} candidates, {c['rounds']} rounds (forward + reversed Latin squares), "
              f"{c['confirmation_rounds']} confirmation rounds, {c['warmup']} warmup + {c['steps']} measured calls per "
-             f"run, every run a rocprofv3-traced process (device time per call = attention + combine dispatches), "
+             f"run, every run a rocprofv3-traced process (device time per call = the dispatches of its kernels), "
              f"paired per-round improvements, bootstrap 95% interval ({c['bootstrap_samples']} samples), "
              f"promotion above {c['minimum_practical_improvement']:.0%}.", "",
              "| candidate | knobs | gate max-abs | runs | median call (us) | paired improvement | 95% CI | promotable |",
