@@ -268,8 +268,9 @@ def fused_bench(args, dev) -> int:
 
 def host_submit(args, dev, calls: int = 400) -> int:
     """Host time per call: ``calls`` back-to-back ops.ragged_paged_attention calls on C1 (kernels of
-    a few microseconds, so the host is the bound), wall time / calls, median of 5 batches; and the
-    same with the validation plan dropped each call (the first call of a new signature)."""
+    a few microseconds, so the host is the bound), wall time / calls, median of 5 batches; the
+    same with the validation plan dropped each call (the first call of a new signature); and the
+    call captured into a HIP graph (ops.CapturedCall), per replay."""
     import statistics
 
     import torch
@@ -306,9 +307,29 @@ def host_submit(args, dev, calls: int = 400) -> int:
         call()
     ev1.record()
     torch.cuda.synchronize()
-    print(json.dumps({"host_submit_us_per_call": res, "device_us_per_call_back_to_back":
-                      round(ev0.elapsed_time(ev1) * 1e3 / calls, 2), "calls": calls,
-                      "workload": "c1 (kernels of a few us: the host is the bound)"}), flush=True)
+    device_us = round(ev0.elapsed_time(ev1) * 1e3 / calls, 2)
+    # the same call captured into a HIP graph and replayed (ops.CapturedCall)
+    cc = ops.CapturedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                          sm_scale=case.sm_scale, out=torch.empty_like(d["q"]))
+    for _ in range(20):
+        cc.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            cc.replay()
+        per.append((time.perf_counter() - t0) / calls * 1e6)
+        torch.cuda.synchronize()
+    res["graph_replay"] = round(statistics.median(per), 2)
+    ev0.record()
+    for _ in range(calls):
+        cc.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"host_submit_us_per_call": res, "device_us_per_call_back_to_back": device_us,
+                      "device_us_per_call_graph_replays": round(ev0.elapsed_time(ev1) * 1e3 / calls, 2),
+                      "calls": calls, "workload": "c1 (kernels of a few us: the host is the bound)"}), flush=True)
     return 0
 
 

@@ -1,0 +1,78 @@
+"""GPU: the operator captured into a HIP graph (ops.CapturedCall) and replayed over buffers whose
+values and metadata change in place -- every replay bitwise equal to an eager call on the same
+inputs, and within the oracle's tolerance.  Replays are interleaved with the program's own eager
+work and synchronisations, as graph replays after the first are where recorded memset nodes have
+gone wrong (the captured call records kernels only)."""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rpa_oracle as orc
+from tpu_cake_amd import ops
+from tpu_cake_amd.workloads import make_config, make_custom
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _eager(d, case, out):
+    return ops.ragged_paged_attention(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
+                                      d["num_seqs"], sm_scale=case.sm_scale, kv_scales=d.get("kv_scales"), out=out)
+
+
+def _oracle_err(case, d, got):
+    meta = {k: d[k].cpu().numpy() for k in ("kv_lens", "page_indices", "cu_q_lens", "num_seqs")}
+    q = d["q"].view(torch.int16).cpu().numpy().view(np.uint16)
+    kv = d["kv_pages"].view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = orc.ref_ragged_paged_attention(q, kv, meta["kv_lens"], meta["page_indices"], meta["cu_q_lens"],
+                                         meta["num_seqs"], sm_scale=case.sm_scale)
+    g = got.float().cpu().numpy()[: ref.shape[0]]
+    return orc.errors(g, orc.bf16_round(ref))
+
+
+@pytest.mark.parametrize("name", ["c1", "split"])
+def test_captured_call_replays_match_eager(cuda, name):
+    _say(f"graph replay {name}")
+    if name == "c1":
+        case = make_config("c1")
+    else:  # long and short sequences over many workgroups: split row blocks, heavy merges, combine
+        case = make_custom(kv_lens=[9000, 40, 1, 3000, 700, 64], q_lens=[1] * 6, num_q_heads=32, num_kv_heads=8,
+                           page_size=64, seed=5)
+    d = ops.case_to_device(case, "cuda")
+    out_graph = torch.empty_like(d["q"])
+    out_eager = torch.empty_like(d["q"])
+    cc = ops.CapturedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                          sm_scale=case.sm_scale, out=out_graph)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    kv_lens0 = d["kv_lens"].clone()
+    for r in range(5):
+        # the loop's own work between replays: new values, and (from the third step) shorter
+        # sequences -- the metadata of the same shapes
+        d["q"].copy_(torch.randn(d["q"].shape, generator=gen, device="cuda").to(torch.bfloat16))
+        if r >= 2:
+            d["kv_lens"].copy_(torch.clamp(kv_lens0 - 37 * r, min=1))
+        torch.cuda.synchronize()
+        want = _eager(d, case, out_eager).clone()
+        torch.cuda.synchronize()
+        got = cc.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {r} differs from the eager call"
+        if r in (0, 4):
+            err = _oracle_err(case, d, got)
+            print(f"  replay {r}: max_abs={err['max_abs']:.3e}", flush=True)
+            assert err["finite"] and err["max_abs"] <= 2e-2, err
+
+
+def test_captured_call_rejects_events(cuda):
+    case = make_config("c1")
+    d = ops.case_to_device(case, "cuda")
+    with pytest.raises(ValueError, match="kernel_events"):
+        ops.CapturedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                         sm_scale=case.sm_scale, kernel_events=(object(), object()))

@@ -12,6 +12,7 @@ from . import fused, inkling  # noqa: F401
 
 from .ops import (  # noqa: F401
     DEFAULT_MASK_VALUE,
+    CapturedCall,
     dynamic_validate_inputs,
     gather_kv,
     ragged_paged_attention,
@@ -20,6 +21,7 @@ from .ops import (  # noqa: F401
 )
 
 __all__ = [
+    "CapturedCall",
     "DEFAULT_MASK_VALUE",
     "fused",
     "inkling",

@@ -123,6 +123,7 @@ def make_shape(q, kv_pages, page_indices) -> _lib.RpaShape:
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 
 
 def _current_stream(dev: int) -> int:
@@ -301,7 +302,7 @@ def ragged_paged_attention(
     elif (out.shape != q.shape or out.dtype != q.dtype or out.get_device() != dev or not out.is_contiguous()
           or out.data_ptr() == q.data_ptr()):
         raise ValueError("out must be a separate contiguous tensor shaped like q on q's device")
-    if dev != torch.cuda.current_device():
+    if dev != _get_device():
         with torch.cuda.device(dev):
             return ragged_paged_attention(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, sm_scale=sm_scale,
                                           sliding_window=sliding_window, soft_cap=soft_cap, mask_value=mask_value,
@@ -328,6 +329,41 @@ def ragged_paged_attention(
     if rc:
         _lib.check(rc)
     return out
+
+
+class CapturedCall:
+    """One ``ragged_paged_attention`` call captured into a HIP graph over fixed buffers.
+
+    A serving loop writes each step's queries, K/V pages and metadata into the same tensors and
+    calls ``replay()``: the graph re-runs the call's kernels on whatever those tensors hold, at the
+    host cost of one graph launch instead of the wrapper's per-call work.  Capture happens on a
+    stream of this object (default priority) after one warm-up call on it, so the validated plan and
+    the stream's workspace (allocated and initialised by ``rpa_workspace_init``) exist beforehand:
+    the graph records only the call's kernel launches -- no allocation, no memset node.  The
+    workspace is this stream's, so replays must not overlap other calls on it.  Metadata changes
+    keep the shapes (``num_seqs``, ``kv_lens``, ``cu_q_lens`` and ``page_indices`` values may
+    change; their sizes, the dtypes and the knobs are fixed at capture).
+    """
+
+    def __init__(self, q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *, out=None, **kwargs):
+        if kwargs.get("kernel_events") is not None:
+            raise ValueError("a captured call takes no kernel_events")
+        self.out = out if out is not None else torch.empty_like(q)
+        self._args = (q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs)
+        self._kwargs = dict(kwargs, out=self.out)
+        self.stream = torch.cuda.Stream(device=q.device)
+        self.stream.wait_stream(torch.cuda.current_stream(q.device))
+        with torch.cuda.stream(self.stream):
+            ragged_paged_attention(*self._args, **self._kwargs)  # plan + this stream's workspace
+        self.stream.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            ragged_paged_attention(*self._args, **self._kwargs)
+
+    def replay(self) -> torch.Tensor:
+        """Launch the captured call (ordered after the current stream's work) and return ``out``."""
+        self.graph.replay()
+        return self.out
 
 
 def read_error_word(device: torch.device | None = None) -> int:
