@@ -65,6 +65,7 @@ constexpr float kRescaleLog2 = 8.f;  // lazy softmax rescale threshold (log2 uni
 constexpr float kDefaultMask = -0.7f * 3.4028234663852886e38f;  // ragged_paged_attention.py:32
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -295,9 +296,9 @@ __device__ __forceinline__ size_t kv_elem(const Params& p, int pg, int kt, int c
          (size_t)kD;
 }
 
+// Two floats to bf16 (round to nearest even), lo in the low half: one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1097,13 +1098,16 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
   compute_unit_line<MODE>(p, cur, v, bias, q, nxt, nx_addr, st, vt, kt, lane, n, j, wv);
+  // The next unit's K goes to the tile before a row block's finish stores: its wait then counts
+  // the same younger operations (the next unit's V) on every path.  Issued before it, the stores
+  // made that wait also retire most of the V just loaded on the steps that end a row block.
+  store_k_tile<MODE>(p, k, kt, lane);
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
     finish_row_block(p, cur, st, b, complete, n, j, wv);
     if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
-  store_k_tile<MODE>(p, k, kt, lane);
   if constexpr (MODE == KV_BF16_BIAS) {
     bias[0] = bias_nx[0];
     bias[1] = bias_nx[1];
@@ -1129,6 +1133,8 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
 constexpr int kPfKRow = kD * 2 + 16;
 constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
 constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
+constexpr int kPfQWave = 2 * 4 * 64 * 16;  // one wave's Q^T fragments: 2 row blocks x 4 k-steps x 64 lanes x 16 B
+constexpr int kPfQBase = 2 * kPfBufBytes;    // the tile's Q fragments follow the two chunk buffers
 constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
 constexpr float kPfCost = 0.45f;  // prefill chunk-step cost in stream-K units (Latin-square search on C3)
 
@@ -1270,18 +1276,43 @@ struct PfRow {
   bool ok;   // the row exists (token in the tile, pos >= 0)
 };
 
+// One chunk for one 16-row block that every row sees in full (no masking, scale_log2 > 0).
+__device__ __forceinline__ bf16x8 pf_softmax_plain(const Params& p, const f32x4 sc[2], PfRow& st) {
+  // no masking: the raw scores' maximum, scaled once (scale_log2 > 0, so it commutes with the
+  // rounding of each scaled score), and each probability as exp2(fma(s, scale, -m))
+  float mr = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+                   fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+  const float mc = rows4_max(mr) * p.scale_log2;
+  const bool grow = mc > st.m + kRescaleLog2;
+  if (__ballot(grow)) {
+    const float mn = grow ? mc : st.m;
+    const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
+    st.l *= alpha;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+    st.m = mn;
+  }
+  const float nmu = st.m == -INFINITY ? 0.f : -st.m;
+  float pr[2][4];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) pr[kb][rr] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][rr], p.scale_log2, nmu));
+  st.l += ((pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3])) + ((pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]));
+  u32x4 pw;
+  pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
+  pw[1] = pack_bf16x2(pr[0][2], pr[0][3]);
+  pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
+  pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
+  return __builtin_bit_cast(bf16x8, pw);
+}
+
 // One chunk for one 16-row block: scores sc[kb] (keys 16kb + 4j + rr of row n), softmax update,
 // P^T packed for the PV MFMA.
-__device__ __forceinline__ bf16x8 pf_softmax(const Params& p, const PfTile& tl, int c, bool plain, const f32x4 sc[2],
-                                             PfRow& st, int j) {
+__device__ __forceinline__ bf16x8 pf_softmax(const Params& p, const PfTile& tl, int c, const f32x4 sc[2], PfRow& st,
+                                             int j) {
   float xs[2][4];
-  if (plain) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      xs[0][rr] = sc[0][rr] * p.scale_log2;
-      xs[1][rr] = sc[1][rr] * p.scale_log2;
-    }
-  } else {
+  {
     const int key0 = c * KV_CHUNK + 4 * j;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -1334,33 +1365,53 @@ __device__ __forceinline__ bf16x8 pf_softmax(const Params& p, const PfTile& tl, 
 }
 
 // One chunk from LDS buffer buf for the wave's two row blocks.
+// One chunk from LDS buffer buf for the wave's two row blocks.  The wave's Q^T fragments (B
+// operands) come from its LDS copy qs, lane-contiguous per (row block, k-step): registers are the
+// prefill role's limit, LDS is not.  PLAIN: every row of the tile sees the chunk in full (no soft
+// cap, window or masking; scale_log2 > 0), so the softmax needs no per-score work beyond the
+// exponent (pf_softmax_plain); the tile loop runs such chunks in a loop of their own, so neither
+// path carries the other's registers.
+template <bool PLAIN>
 __device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, int c, const uint8_t* buf,
-                                           const bf16x8 q[2][4], PfRow st[2], int n, int j) {
+                                           const uint8_t* qs, PfRow st[2], int n, int j) {
+  const int lane = 16 * j + n;
   f32x4 sc[2][2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) sc[rb][0] = sc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < 4; ++s) {
+    const bf16x8 q0 = *(const bf16x8*)(qs + ((0 * 4 + s) * 64 + lane) * 16);
+    const bf16x8 q1 = *(const bf16x8*)(qs + ((1 * 4 + s) * 64 + lane) * 16);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const bf16x8 a = *(const bf16x8*)(buf + (16 * kb + n) * kPfKRow + (32 * s + 8 * j) * 2);
-      sc[0][kb] = mfma(a, q[0][s], sc[0][kb]);
-      sc[1][kb] = mfma(a, q[1][s], sc[1][kb]);
+      sc[0][kb] = mfma(a, q0, sc[0][kb]);
+      sc[1][kb] = mfma(a, q1, sc[1][kb]);
     }
-  // every row of the tile sees this chunk in full: no per-score masking
-  const int pos_min = tl.kv_len - tl.q_len + tl.tok0;
-  const bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 && (c + 1) * KV_CHUNK - 1 <= pos_min &&
-                     (c + 1) * KV_CHUNK <= tl.kv_len;
-  const bf16x8 pb0 = pf_softmax(p, tl, c, plain, sc[0], st[0], j);
-  const bf16x8 pb1 = pf_softmax(p, tl, c, plain, sc[1], st[1], j);
+  }
   const uint8_t* vt = buf + kPfKBytes;
+  bf16x8 pb0, pb1;
+  if constexpr (PLAIN) {
+    pb0 = pf_softmax_plain(p, sc[0], st[0]);
+    pb1 = pf_softmax_plain(p, sc[1], st[1]);
+  } else {
+    pb0 = pf_softmax(p, tl, c, sc[0], st[0], j);
+    pb1 = pf_softmax(p, tl, c, sc[1], st[1], j);
+  }
+  bf16x8 va[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
     const int row = 16 * d + n;
-    const bf16x8 a = *(const bf16x8*)(vt + row * kVTRow + 16 * pf_vt_group(row, j));
-    st[0].acc[d] = mfma(a, pb0, st[0].acc[d]);
-    st[1].acc[d] = mfma(a, pb1, st[1].acc[d]);
+    va[d] = *(const bf16x8*)(vt + row * kVTRow + 16 * pf_vt_group(row, j));
   }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    st[0].acc[d] = mfma(va[d], pb0, st[0].acc[d]);
+    st[1].acc[d] = mfma(va[d], pb1, st[1].acc[d]);
+  }
+  // the eight fragment reads go out together, then the sixteen MFMAs (not read, wait, MFMA x 8)
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
 }
 
 // Step on chunk c (in LDS buffer c & 1).  Ring slot x % 4 holds chunk x's data and, from two
@@ -1369,14 +1420,14 @@ __device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, in
 // data (into `ld`, with the page ids it received two steps ago); compute chunk c; store chunk
 // c + 1 (`nx`) to the other LDS buffer.  No wait here needs a load younger than the chunk it
 // waits for.
-template <int NP, bool UPG>
-__device__ __forceinline__ void pf_step(const Params& p, const PfTile& tl, int c, uint8_t* lds, const bf16x8 q[2][4],
+template <int NP, bool UPG, bool PLAIN>
+__device__ __forceinline__ void pf_step(const Params& p, const PfTile& tl, int c, uint8_t* lds, const uint8_t* qs,
                                         PfRow st[2], PfRegs<NP>& ld, PfRegs<NP>& nx, int tid, int nthreads, int n,
                                         int j, int& err) {
   const int last = tl.c_hi - 1;
   nx.pg = pf_load_pages<NP, UPG>(p, tl, c + 5 < last ? c + 5 : last, tid, nthreads);
   pf_load_chunk<NP, UPG>(p, tl, c + 3 < last ? c + 3 : last, ld.pg, tid, nthreads, ld, err);
-  pf_compute(p, tl, c, lds + (c & 1) * kPfBufBytes, q, st, n, j);
+  pf_compute<PLAIN>(p, tl, c, lds + (c & 1) * kPfBufBytes, qs, st, n, j);
   if (c + 1 < tl.c_hi) pf_store_chunk<NP>(lds + ((c + 1) & 1) * kPfBufBytes, nx, tid, nthreads);
   __syncthreads();
 }
@@ -1385,8 +1436,9 @@ template <int NP, bool UPG>
 __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8_t* lds, int wv, int n, int j,
                                         int& err) {
   const int tid = threadIdx.x, nthreads = 64 * p.HG;
-  // queries: row r = 32*wv + 16*rb + n of the tile; B operand dims 32s + 8j .. +8
-  bf16x8 q[2][4];
+  // queries: row r = 32*wv + 16*rb + n of the tile; B operand dims 32s + 8j .. +8, kept in the
+  // wave's LDS region (written before the prologue's barriers, read by this wave only)
+  uint8_t* qs = lds + kPfQBase + wv * kPfQWave;
   PfRow st[2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -1398,7 +1450,7 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
     const int qtok = st[rb].ok ? tl.q_start + tl.tok0 + tok : tl.q_start;
     const uint16_t* qp = p.q + ((size_t)qtok * p.Hq + tl.h * p.G + (st[rb].ok ? g : 0)) * kD + 8 * j;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) q[rb][s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + 32 * s));
+    for (int s = 0; s < 4; ++s) *(u32x4*)(qs + ((rb * 4 + s) * 64 + 16 * j + n) * 16) = *(const u32x4*)(qp + 32 * s);
 #pragma unroll
     for (int d = 0; d < 8; ++d) st[rb].acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
     st[rb].m = -INFINITY;
@@ -1422,18 +1474,34 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
   pf_store_chunk<NP>(lds + (c0 & 1) * kPfBufBytes, r0, tid, nthreads);
   __syncthreads();
 
-  // chunk c lives in ring slot (c - c0) % 4
-  int c = c0;
-  for (;;) {
-    pf_step<NP, UPG>(p, tl, c, lds, q, st, r3, r1, tid, nthreads, n, j, err);
-    if (++c >= tl.c_hi) break;
-    pf_step<NP, UPG>(p, tl, c, lds, q, st, r0, r2, tid, nthreads, n, j, err);
-    if (++c >= tl.c_hi) break;
-    pf_step<NP, UPG>(p, tl, c, lds, q, st, r1, r3, tid, nthreads, n, j, err);
-    if (++c >= tl.c_hi) break;
-    pf_step<NP, UPG>(p, tl, c, lds, q, st, r2, r0, tid, nthreads, n, j, err);
-    if (++c >= tl.c_hi) break;
+  // chunk c lives in ring slot (c - c0) % 4.  Chunks below cp are seen in full by every row of the
+  // tile: they run four at a time in the plain loop; the rest (the diagonal, a window, a soft cap,
+  // and up to three plain chunks left over) in the general one, entered at the same ring phase.
+  int cp = c0;
+  if (!(p.soft_cap > 0.f) && p.sliding_window <= 0 && p.scale_log2 > 0.f) {
+    const int pos_min = tl.kv_len - tl.q_len + tl.tok0;  // last key the tile's first row sees
+    cp = (pos_min + 1) / KV_CHUNK;
+    cp = cp < tl.kv_len / KV_CHUNK ? cp : tl.kv_len / KV_CHUNK;
   }
+  int c = c0;
+  while (c + 4 <= cp) {
+    pf_step<NP, UPG, true>(p, tl, c, lds, qs, st, r3, r1, tid, nthreads, n, j, err);
+    pf_step<NP, UPG, true>(p, tl, c + 1, lds, qs, st, r0, r2, tid, nthreads, n, j, err);
+    pf_step<NP, UPG, true>(p, tl, c + 2, lds, qs, st, r1, r3, tid, nthreads, n, j, err);
+    pf_step<NP, UPG, true>(p, tl, c + 3, lds, qs, st, r2, r0, tid, nthreads, n, j, err);
+    c += 4;
+  }
+  if (c < tl.c_hi)
+    for (;;) {
+      pf_step<NP, UPG, false>(p, tl, c, lds, qs, st, r3, r1, tid, nthreads, n, j, err);
+      if (++c >= tl.c_hi) break;
+      pf_step<NP, UPG, false>(p, tl, c, lds, qs, st, r0, r2, tid, nthreads, n, j, err);
+      if (++c >= tl.c_hi) break;
+      pf_step<NP, UPG, false>(p, tl, c, lds, qs, st, r1, r3, tid, nthreads, n, j, err);
+      if (++c >= tl.c_hi) break;
+      pf_step<NP, UPG, false>(p, tl, c, lds, qs, st, r2, r0, tid, nthreads, n, j, err);
+      if (++c >= tl.c_hi) break;
+    }
 
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
