@@ -713,6 +713,35 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
   const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
   bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
                x.key0() + KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
+  if (MODE != KV_BF16_BIAS && plain && p.scale_log2 > 0.f) {
+    // the raw scores' maximum, scaled once (a positive scale commutes with each score's rounding),
+    // and each probability as exp2(fma(s, scale, -m))
+    const float mr = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+    const float mc = rows4_max(mr) * p.scale_log2;
+    const bool grow = mc > st.m + kRescaleLog2;
+    if (__ballot(grow)) {
+      const float mn = grow ? mc : st.m;
+      const float alpha = __builtin_amdgcn_exp2f(st.m - (mn == -INFINITY ? 0.f : mn));
+      st.l *= alpha;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) st.acc[d] *= alpha;
+      st.m = mn;
+    }
+    const float nmu = st.m == -INFINITY ? 0.f : -st.m;
+    float pr[2][4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      pr[0][rr] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[rr], p.scale_log2, nmu));
+      pr[1][rr] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[rr], p.scale_log2, nmu));
+    }
+    st.l += ((pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3])) + ((pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]));
+    u32x4 pw;
+    pw[0] = pack_bf16x2(pr[0][0], pr[0][1]);
+    pw[1] = pack_bf16x2(pr[0][2], pr[0][3]);
+    pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
+    pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
+    return __builtin_bit_cast(bf16x8, pw);
+  }
   if (plain) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -834,11 +863,14 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j);
 
   wave_lds_fence();
+  bf16x8 va[8];
 #pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    bf16x8 a = *(const bf16x8*)(vt + (16 * d + n) * kVTRow + 16 * j);
-    st.acc[d] = mfma(a, pb, st.acc[d]);
-  }
+  for (int d = 0; d < 8; ++d) va[d] = *(const bf16x8*)(vt + (16 * d + n) * kVTRow + 16 * j);
+#pragma unroll
+  for (int d = 0; d < 8; ++d) st.acc[d] = mfma(va[d], pb, st.acc[d]);
+  // the eight V^T fragment reads go out together, then the MFMAs (not read, wait, MFMA x 8)
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 }
 
 __device__ __forceinline__ void begin_row_block(const Params& p, const Cursor& x, RowState& st, int n) {
@@ -1070,12 +1102,16 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
 
   wave_lds_fence();
+  bf16x8 va[8];
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
     const int row = 16 * d + n;
-    const bf16x8 a = *(const bf16x8*)(vt + row * kVTRow + 16 * vt_swz(row, j));
-    st.acc[d] = mfma(a, pb, st.acc[d]);
+    va[d] = *(const bf16x8*)(vt + row * kVTRow + 16 * vt_swz(row, j));
   }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) st.acc[d] = mfma(va[d], pb, st.acc[d]);
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 }
 
 template <int MODE, bool UPG>
