@@ -356,6 +356,24 @@ def test_prefill_tiles(cuda, hq, q_lens, kv_lens, page):
                        seed=sum(q_lens) + hq))
 
 
+# A tile runs the chunks all its rows see in full four at a time in a loop of its own (the scale
+# folded into the exponent) and the rest in the general loop: priors that leave 0..3 such chunks
+# over a multiple of four; a negative scale (no fully visible chunk takes the plain loop) and a
+# large one (the running maximum moves inside the plain loop).
+@pytest.mark.parametrize("prior", [0, 31, 32, 95, 96, 160, 223])
+def test_prefill_tile_plain_and_general_loops(cuda, prior):
+    _say(f"prefill tile loops, prior {prior}")
+    _check(make_custom(kv_lens=[prior + 128, 40], q_lens=[128, 1], num_q_heads=32, num_kv_heads=8, page_size=64,
+                       seed=prior + 5))
+
+
+@pytest.mark.parametrize("scale", [-0.0884, 0.5])
+def test_prefill_tile_scale_sign_and_rescale(cuda, scale):
+    _say(f"prefill tiles, sm_scale {scale}")
+    _check(make_custom(kv_lens=[900, 64], q_lens=[300, 1], num_q_heads=32, num_kv_heads=8, page_size=64, seed=83,
+                       sm_scale=scale))
+
+
 def test_prefill_tiles_window_and_soft_cap(cuda):
     _say("prefill tiles with sliding window and soft cap")
     case = make_custom(kv_lens=[900, 300, 50], q_lens=[200, 300, 1], num_q_heads=32, num_kv_heads=8, page_size=64,
