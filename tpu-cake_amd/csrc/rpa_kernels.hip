@@ -1171,6 +1171,8 @@ constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
 constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
 constexpr int kPfQWave = 2 * 4 * 64 * 16;  // one wave's Q^T fragments: 2 row blocks x 4 k-steps x 64 lanes x 16 B
 constexpr int kPfQBase = 2 * kPfBufBytes;    // the tile's Q fragments follow the two chunk buffers
+// prefill tiles run in workgroups of eight waves, whose dynamic LDS is eight decode-wave regions
+static_assert(kPfQBase + 8 * kPfQWave <= 8 * kWaveLds, "prefill tile LDS exceeds the workgroup's allocation");
 constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
 constexpr float kPfCost = 0.45f;  // prefill chunk-step cost in stream-K units (Latin-square search on C3)
 

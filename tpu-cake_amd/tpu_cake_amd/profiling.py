@@ -17,8 +17,8 @@ the two counters (bytes per KiB counted).  Every pass is its own process under
 ``bench.py`` reports as ``roofline.traffic``, keyed by the kernel-source digest).  The same raw
 directory always gives the same files.
 
-    python -m tpu_cake_amd.evidence profile --raw gpurun_out/prof          # GPU box
-    python -m tpu_cake_amd.evidence summarize --raw gpurun_out/prof --write profiles
+    PYTHONPATH=tpu-cake_amd python -m tpu_cake_amd.evidence profile --raw gpurun_out/prof   # GPU box
+    PYTHONPATH=tpu-cake_amd python -m tpu_cake_amd.evidence summarize --raw gpurun_out/prof --write profiles
 """
 
 from __future__ import annotations
@@ -203,9 +203,9 @@ def summarize(raw, out_dir, *, raw_label: str | None = None) -> dict:
         md = f"""# rocprofv3 summary: {cfg} ({desc})
 
 Kernel sources digest = {digest} (sha256[:16] of the sources without comments and blank space,
-`tpu_cake_amd.evidence.kernel_source_digest`).  Made by `python -m tpu_cake_amd.evidence profile --raw {label}`
+`tpu_cake_amd.evidence.kernel_source_digest`).  Made by `PYTHONPATH=tpu-cake_amd python -m tpu_cake_amd.evidence profile --raw {label}`
 on the MI355X box (the passes below, from the repository root) and
-`python -m tpu_cake_amd.evidence summarize --raw {label} --write profiles`.
+`PYTHONPATH=tpu-cake_amd python -m tpu_cake_amd.evidence summarize --raw {label} --write profiles`.
 
 {_cmd_block(label, cfg)}
 
@@ -246,8 +246,8 @@ WRITE_SIZE = {copy_w:.0f} KiB (factor {wf:.3f}).
                                          "kernels_avg_us": {k: round(v["avg"], 3) for k, v in st.items()}}
         md = f"""# rocprofv3 summary: inkling ({FUSED_DESCRIPTION})
 
-Kernel sources digest = {digest}.  Made by `python -m tpu_cake_amd.evidence profile --raw {label}` and
-`python -m tpu_cake_amd.evidence summarize --raw {label} --write profiles`:
+Kernel sources digest = {digest}.  Made by `PYTHONPATH=tpu-cake_amd python -m tpu_cake_amd.evidence profile --raw {label}` and
+`PYTHONPATH=tpu-cake_amd python -m tpu_cake_amd.evidence summarize --raw {label} --write profiles`:
 
 {_cmd_block(label, 'inkling')}
 
