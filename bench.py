@@ -269,8 +269,9 @@ def fused_bench(args, dev) -> int:
 def host_submit(args, dev, calls: int = 400) -> int:
     """Host time per call: ``calls`` back-to-back ops.ragged_paged_attention calls on C1 (kernels of
     a few microseconds, so the host is the bound), wall time / calls, median of 5 batches; the
-    same with the validation plan dropped each call (the first call of a new signature); and the
-    call captured into a HIP graph (ops.CapturedCall), per replay."""
+    same with the validation plan dropped each call (the first call of a new signature); the call
+    prepared once (ops.PreparedCall); and the call captured into a HIP graph (ops.CapturedCall),
+    per replay."""
     import statistics
 
     import torch
@@ -308,6 +309,20 @@ def host_submit(args, dev, calls: int = 400) -> int:
     ev1.record()
     torch.cuda.synchronize()
     device_us = round(ev0.elapsed_time(ev1) * 1e3 / calls, 2)
+    # the same call prepared once (ops.PreparedCall: one foreign call per step)
+    pc = ops.PreparedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                          sm_scale=case.sm_scale, out=torch.empty_like(d["q"]))
+    for _ in range(20):
+        pc()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            pc()
+        per.append((time.perf_counter() - t0) / calls * 1e6)
+        torch.cuda.synchronize()
+    res["prepared_call"] = round(statistics.median(per), 2)
     # the same call captured into a HIP graph and replayed (ops.CapturedCall)
     cc = ops.CapturedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
                           sm_scale=case.sm_scale, out=torch.empty_like(d["q"]))

@@ -1,8 +1,8 @@
-"""GPU: the operator captured into a HIP graph (ops.CapturedCall) and replayed over buffers whose
-values and metadata change in place -- every replay bitwise equal to an eager call on the same
-inputs, and within the oracle's tolerance.  Replays are interleaved with the program's own eager
-work and synchronisations, as graph replays after the first are where recorded memset nodes have
-gone wrong (the captured call records kernels only)."""
+"""GPU: the operator captured into a HIP graph (ops.CapturedCall) and prepared once
+(ops.PreparedCall), run over buffers whose values and metadata change in place -- every call
+bitwise equal to an eager call on the same inputs, and within the oracle's tolerance.  Replays
+are interleaved with the program's own eager work and synchronisations, as graph replays after the
+first are where recorded memset nodes have gone wrong (the captured call records kernels only)."""
 
 import sys
 
@@ -75,4 +75,41 @@ def test_captured_call_rejects_events(cuda):
     d = ops.case_to_device(case, "cuda")
     with pytest.raises(ValueError, match="kernel_events"):
         ops.CapturedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                         sm_scale=case.sm_scale, kernel_events=(object(), object()))
+
+
+@pytest.mark.parametrize("name", ["c1", "split"])
+def test_prepared_call_matches_eager(cuda, name):
+    """ops.PreparedCall over buffers whose values and metadata change in place: every call bitwise
+    equal to an eager call on the same inputs."""
+    _say(f"prepared call {name}")
+    if name == "c1":
+        case = make_config("c1")
+    else:
+        case = make_custom(kv_lens=[9000, 40, 1, 3000, 700, 64], q_lens=[1] * 6, num_q_heads=32, num_kv_heads=8,
+                           page_size=64, seed=5)
+    d = ops.case_to_device(case, "cuda")
+    out_eager = torch.empty_like(d["q"])
+    pc = ops.PreparedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                          sm_scale=case.sm_scale)
+    gen = torch.Generator(device="cuda").manual_seed(13)
+    kv_lens0 = d["kv_lens"].clone()
+    for r in range(4):
+        d["q"].copy_(torch.randn(d["q"].shape, generator=gen, device="cuda").to(torch.bfloat16))
+        if r >= 2:
+            d["kv_lens"].copy_(torch.clamp(kv_lens0 - 53 * r, min=1))
+        want = _eager(d, case, out_eager).clone()
+        got = pc()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {r} differs from the eager call"
+        if r == 3:
+            err = _oracle_err(case, d, got)
+            assert err["finite"] and err["max_abs"] <= 2e-2, err
+
+
+def test_prepared_call_rejects_unknown_keywords(cuda):
+    case = make_config("c1")
+    d = ops.case_to_device(case, "cuda")
+    with pytest.raises(ValueError, match="kernel_events"):
+        ops.PreparedCall(d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
                          sm_scale=case.sm_scale, kernel_events=(object(), object()))

@@ -366,6 +366,58 @@ class CapturedCall:
         return self.out
 
 
+class PreparedCall:
+    """One ``ragged_paged_attention`` call with its host work done once, for a serving loop that
+    passes the same tensors every step.
+
+    Construction runs the call once through the operator (every check, the plan, the current
+    stream's workspace) and keeps the library entry point, the shape and option structures, each
+    tensor's address, the workspace and the stream as ready foreign-call arguments; ``__call__``
+    launches the kernels with one foreign call.  Fixed at construction: the tensors (their storage,
+    shapes and dtypes), the keywords and the stream (the current one then); free between calls:
+    every value they hold -- queries, K/V pages and all metadata.  Calls on one stream share its
+    workspace and must not overlap.  Unlike ``CapturedCall`` no graph is involved: the launches are
+    ordinary stream work, so the call costs less host time than a graph replay on this platform.
+    """
+
+    def __init__(self, q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *, out=None, kv_scales=None,
+                 **kwargs):
+        if kwargs.get("kernel_events") is not None:
+            raise ValueError("a prepared call takes no kernel_events")
+        self.out = out if out is not None else torch.empty_like(q)
+        ragged_paged_attention(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, out=self.out,
+                               kv_scales=kv_scales, **kwargs)
+        knobs = dict(sm_scale=1.0, sliding_window=None, soft_cap=None, mask_value=DEFAULT_MASK_VALUE, k_scale=None,
+                     v_scale=None, num_kv_pages_per_block=None, num_queries_per_block=None, vmem_limit_bytes=None,
+                     waves_per_cu=None, prefill_tiles=None, prefill_cost=None)
+        unknown = set(kwargs) - set(knobs)
+        if unknown:
+            raise TypeError(f"unexpected keyword arguments {sorted(unknown)}")
+        knobs.update(kwargs)
+        self._shape, self._opts = _static_plan(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_scales,
+                                               knobs)
+        dev = q.get_device()
+        self.stream = _current_stream(dev)
+        ws_ptr, ws_bytes = _workspace_ptr(self._shape, dev, self.stream)
+        # a function object of its own without argument types: the prepared ctypes values pass as-is
+        fn = _lib.load()["rpa_ragged_paged_attention"]
+        fn.restype = ctypes.c_int
+        vp = ctypes.c_void_p
+        self._fn = fn
+        self._keep = (q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_scales, self.out)
+        self._args = (ctypes.byref(self._shape), ctypes.byref(self._opts), vp(q.data_ptr()), vp(kv_pages.data_ptr()),
+                      vp(kv_scales.data_ptr() if kv_scales is not None else None), vp(kv_lens.data_ptr()),
+                      vp(page_indices.data_ptr()), vp(cu_q_lens.data_ptr()), vp(num_seqs.data_ptr()),
+                      vp(self.out.data_ptr()), vp(ws_ptr), ctypes.c_size_t(ws_bytes), vp(self.stream))
+
+    def __call__(self) -> torch.Tensor:
+        """Launch the call on its stream and return ``out``."""
+        rc = self._fn(*self._args)
+        if rc:
+            _lib.check(rc)
+        return self.out
+
+
 def read_error_word(device: torch.device | None = None) -> int:
     """Synchronously read the device-side metadata error word of the current stream's workspace."""
     device = device or torch.device("cuda", torch.cuda.current_device())
