@@ -310,22 +310,30 @@ struct SeqInfo {
 
 // Sequence metadata from raw kv_lens[i], cu_q_lens[i], cu_q_lens[i + 1] (valid = i < num_seqs).
 // A sequence with at least pf_min query tokens (pf_min > 0) belongs to the prefill tiles and
-// contributes no stream-K units.
+// contributes no stream-K units.  Straight-line selects per lane; the row-block loop of
+// seq_units_per_head runs only when some lane holds a sequence of more than one row block.
 __device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int c1, bool valid, int pf_min,
                                             int& err) {
-  SeqInfo s{0, 0, 0, 0};
-  if (valid) {
-    long long cap = (long long)p.PPS * p.S;
-    if (kv > cap) { kv = (int)cap; err |= ERR_KVLEN; }
-    if (kv < 0) kv = 0;
-    int ql = c1 - c0;
-    if (c0 < 0 || ql < 0 || c1 > p.T) { ql = 0; err |= ERR_QROW; }
-    if (ql > kv) err |= ERR_QLEN;
-    s.kv_len = kv;
-    s.q_start = c0;
-    s.q_len = ql;
-    s.units = (pf_min > 0 && ql >= pf_min) ? 0 : seq_units_per_head(kv, ql, p.G, p.skip_masked, p.sliding_window);
-  }
+  const long long cap = (long long)p.PPS * p.S;
+  int e = kv > cap ? ERR_KVLEN : 0;
+  kv = kv > cap ? (int)cap : (kv < 0 ? 0 : kv);
+  int ql = c1 - c0;
+  const bool bad_rows = c0 < 0 || ql < 0 || c1 > p.T;
+  e |= bad_rows ? ERR_QROW : 0;
+  ql = bad_rows ? 0 : ql;
+  e |= ql > kv ? ERR_QLEN : 0;
+  const bool one_block = ql <= ROW_BLOCK && ql * p.G <= ROW_BLOCK;
+  int units = 0;
+  if (ql > 0 && kv > 0) units = rb_units(kv, ql, p.G, 0, p.skip_masked, p.sliding_window);
+  if (__ballot(valid && !one_block) != 0 && !one_block)
+    units = seq_units_per_head(kv, ql, p.G, p.skip_masked, p.sliding_window);
+  if (pf_min > 0 && ql >= pf_min) units = 0;
+  err |= valid ? e : 0;
+  SeqInfo s;
+  s.kv_len = valid ? kv : 0;
+  s.q_start = valid ? c0 : 0;
+  s.q_len = valid ? ql : 0;
+  s.units = valid ? units : 0;
   return s;
 }
 
@@ -414,7 +422,8 @@ __device__ __forceinline__ Cursor cursor_at(const Params& p, const Window& w, in
   Cursor x;
   cursor_load_seq(p, w, seq, x);
   int per_head = rl(w.s.units, seq - w.base);
-  x.h = ul < (1ll << 31) ? (int)ul / per_head : (int)(ul / per_head);  // 32-bit division when it fits
+  // one kv-head group: no division; else a 32-bit division when it fits
+  x.h = p.NG == 1 ? 0 : (ul < (1ll << 31) ? (int)ul / per_head : (int)(ul / per_head));
   int rem = (int)(ul - (long long)x.h * per_head);
   x.rb = 0;
   for (;;) {

@@ -46,8 +46,10 @@ constexpr int ROW_BLOCK = 16;  // query rows per row block (the N extent of the 
 // Keys visible to row block rb (causal limit of its last valid row), or 0.
 RPA_HD int rb_visible_keys(int kv_len, int q_len, int group, int rb, bool skip_masked) {
   if (!skip_masked) return kv_len;
-  int last_row_tok = (rb * ROW_BLOCK + ROW_BLOCK - 1) / group;
-  int last_tok = q_len - 1 < last_row_tok ? q_len - 1 : last_row_tok;
+  // A block that holds the sequence's last row (row q_len*group - 1) ends at its last token:
+  // every decode row block, with no division.
+  const bool last_block = (long long)(rb + 1) * ROW_BLOCK >= (long long)q_len * group;
+  const int last_tok = last_block ? q_len - 1 : (rb * ROW_BLOCK + ROW_BLOCK - 1) / group;
   int vis = kv_len - q_len + last_tok + 1;
   return vis < kv_len ? vis : kv_len;
 }
@@ -56,7 +58,7 @@ RPA_HD int rb_visible_keys(int kv_len, int q_len, int group, int rb, bool skip_m
 // weight), else the chunk of key pos_first - window + 1, the lowest key any row of the block sees.
 RPA_HD int rb_first_chunk(int kv_len, int q_len, int group, int rb, bool skip_masked, int window) {
   if (!skip_masked || window <= 0) return 0;
-  const int first_tok = rb * ROW_BLOCK / group;
+  const int first_tok = rb == 0 ? 0 : rb * ROW_BLOCK / group;
   const long long lo = (long long)kv_len - q_len + first_tok - window + 1;
   return lo > 0 ? (int)(lo / KV_CHUNK) : 0;
 }
@@ -77,6 +79,8 @@ RPA_HD int num_row_blocks(int q_len, int group) {
 // Units of one kv head of a sequence (sum over its row blocks).
 RPA_HD int seq_units_per_head(int kv_len, int q_len, int group, bool skip_masked, int window) {
   if (q_len <= 0 || kv_len <= 0) return 0;
+  if (q_len <= ROW_BLOCK && q_len * group <= ROW_BLOCK)  // one row block (decode): no loop
+    return rb_units(kv_len, q_len, group, 0, skip_masked, window);
   int nrb = num_row_blocks(q_len, group);
   int u = 0;
   for (int rb = 0; rb < nrb; ++rb) u += rb_units(kv_len, q_len, group, rb, skip_masked, window);
