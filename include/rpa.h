@@ -202,6 +202,10 @@ int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* 
  * the device still range-checks what it dereferences (error word).  cu_q_lens and
  * distribution are part of the reference's input list and are validated by that preflight;
  * the device does not read them.  head_dim <= cache_width = 128.
+ * With head_dim = 128, a page size that is a multiple of 32, 16-byte aligned tensors and
+ * R in {0, 16} with E a multiple of 8, the step is one attention launch (new token read from
+ * keys/values, bias formed in the kernel) plus the merge launch, which also stores the token;
+ * other shapes take a preparation launch first (cache write, page table, bias table).
  * --------------------------------------------------------------------------------------- */
 typedef struct rpa_fused_shape {
   int32_t num_seqs;          /* B */

@@ -71,6 +71,36 @@ def test_decode_shapes(cuda, hq, hkv, d, page, lens):
     _run_and_check(inp)
 
 
+@pytest.mark.parametrize("hq,hkv,page,lens,rel_dim,extent", [
+    # one attention launch: no relative bias; windows of 40 and 8 distances (groups of 8)
+    (32, 8, 64, [1, 31, 32, 33, 96, 700], 0, 512),
+    (32, 8, 64, [1, 9, 40, 41, 300, 1025], 16, 40),
+    (16, 2, 128, [2, 8, 129, 257], 16, 8),
+    # the prep launch: a window that is not a multiple of 8, a 32-wide projection
+    (32, 8, 64, [5, 70, 200], 16, 20),
+    (32, 8, 64, [5, 70, 200], 32, 64),
+])
+def test_bias_windows_and_launch_forms(cuda, hq, hkv, page, lens, rel_dim, extent):
+    """Relative-bias windows at chunk edges and both forms of the call: the one-launch path (page
+    size a multiple of 32, D = 128, R in {0, 16}, E a multiple of 8) and the prep launch."""
+    _say(f"fused bias hq={hq} hkv={hkv} page={page} R={rel_dim} E={extent}")
+    pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(rel_dim * 5 + extent + page, nseq=len(lens), hq=hq, hkv=hkv, d=128,
+                               page_size=page, pool_pages=pool, lengths=lens, rel_dim=rel_dim, extent=extent)
+    _run_and_check(inp)
+
+
+def test_more_than_256_sequences(cuda):
+    """Metadata past the first four 64-sequence windows (loaded one window at a time)."""
+    rng = np.random.default_rng(11)
+    lens = [int(x) for x in rng.integers(1, 200, size=300)]
+    _say("fused 300 sequences")
+    pool = int(sum(-(-x // 32) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(12, nseq=300, hq=8, hkv=8, d=128, page_size=32, pool_pages=pool, lengths=lens,
+                               rel_dim=16, extent=64)
+    _run_and_check(inp)
+
+
 def test_rejected_metadata_never_reaches_the_kernel(cuda):
     _say("fused preflight before the kernel")
     inp = fo.inkling_fused_rpa_inputs(seed=97)

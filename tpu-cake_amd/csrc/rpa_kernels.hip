@@ -72,8 +72,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // KV_BF16_BIAS: bf16 KV plus an additive relative-position bias table (the fused Inkling decode).
-enum KvMode { KV_BF16 = 0, KV_BF16_SCALED = 1, KV_FP8 = 2, KV_BF16_BIAS = 3 };
-constexpr int kModes = 4;
+// KV_BF16_FUSED: the fused Inkling decode step in one attention launch (Params::fused).
+enum KvMode { KV_BF16 = 0, KV_BF16_SCALED = 1, KV_FP8 = 2, KV_BF16_BIAS = 3, KV_BF16_FUSED = 4 };
+
+// Modes that add a relative-position bias to the scores.
+template <int MODE>
+constexpr bool has_bias() {
+  return MODE == KV_BF16_BIAS || MODE == KV_BF16_FUSED;
+}
+constexpr int kModes = 5;
 
 enum ErrBits { ERR_PAGE = 1, ERR_QROW = 2, ERR_KVLEN = 4, ERR_QLEN = 8 };
 
@@ -114,6 +121,22 @@ struct Params {
                           // key, 0 outside the window of the rel_extent keys nearest the (single)
                           // query row, added to its scaled score
   int rel_extent;
+  // KV_BF16_FUSED, the fused decode step in one attention launch (src/tpu_cake/rpa_owned_kernel.py:473-522,
+  // :811-813 fuse the cache write the same way): the kernel reads the step's own metadata -- one
+  // query token per sequence (q row i), num_seqs = fused_nseq, sequence i's pages at
+  // page_indices[cu_kv[i] / S + j] -- takes key kv_len-1 of every sequence from new_k / new_v
+  // ([B, Hkv, kD] bf16: the token this step writes; the combine kernel stores it into the cache),
+  // and forms the relative bias of each score in the kernel (rel_states [B, Hq, 16] @
+  // rel_proj[:, kv_len-1-key] for distances below rel_extent, rel_proj [16, E]; rel_states NULL:
+  // no bias, rel_proj then 8 zero columns).  fused is set for the combine launch's token stores.
+  int fused;
+  int fused_nseq;
+  int fused_entries;  // length of page_indices in the fused layout
+  const int32_t* cu_kv;
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  const uint16_t* rel_states;
+  const uint16_t* rel_proj;
   int pf_tq;         // tokens per prefill tile (0 = prefill tiles off)
   int pf_min;        // sequences with at least this many query tokens take prefill tiles
   float pf_cost;     // cost of one prefill tile chunk in stream-K units (work split model)
@@ -345,26 +368,51 @@ __device__ __forceinline__ void select_seq(SeqInfo& d, const SeqInfo& s, bool c)
   d.units = c ? s.units : d.units;
 }
 
+// Fused decode step (Params::fused): sequence i owns q row i and the page entries from
+// cu_kv[i] / S.  Its q_start field carries that first page entry (the q row is i itself); a
+// sequence whose cu_kv is negative, not page-aligned, or whose pages run past the page table is
+// dropped (no units) and flagged.
+__device__ __forceinline__ SeqInfo make_fused_seq(const Params& p, int kv, int cu, int i, bool valid, int& err) {
+  SeqInfo s = make_seq(p, kv, i, i + 1, valid, 0, err);
+  const int pb = p.log2S >= 0 ? (cu >> p.log2S) : (cu / p.S);
+  const int npg = p.log2S >= 0 ? ((s.kv_len + p.S - 1) >> p.log2S) : ((s.kv_len + p.S - 1) / p.S);
+  const bool bad = cu < 0 || pb * p.S != cu || (long long)pb + npg > (long long)p.fused_entries;
+  err |= valid && bad ? ERR_PAGE : 0;
+  s.units = bad ? 0 : s.units;
+  s.q_start = bad ? 0 : pb;
+  return s;
+}
+
+// The fused decode step's metadata is read only by the mode that runs it.
+template <int MODE>
+__device__ __forceinline__ constexpr bool fused_on(const Params&) {
+  return MODE == KV_BF16_FUSED;
+}
+
+template <int MODE>
 __device__ __forceinline__ SeqInfo load_seq(const Params& p, int i, int nseq, int pf_min, int& err) {
   if (i >= nseq) return SeqInfo{0, 0, 0, 0};
+  if (fused_on<MODE>(p)) return make_fused_seq(p, p.kv_lens[i], p.cu_kv[i], i, true, err);
   return make_seq(p, p.kv_lens[i], p.cu_q_lens[i], p.cu_q_lens[i + 1], true, pf_min, err);
 }
 
+template <int MODE>
 __device__ __forceinline__ long long total_units(const Params& p, int nseq, int lane, int& err) {
   long long w = 0;
   for (int base = 0; base < nseq; base += 64) {
-    SeqInfo s = load_seq(p, base + lane, nseq, 0, err);
+    SeqInfo s = load_seq<MODE>(p, base + lane, nseq, 0, err);
     w += wave_sum_units((long long)s.units * p.NG);
   }
   return w;
 }
 
 // Sequence holding unit u and the first unit of that sequence (wave-uniform results).
+template <int MODE>
 __device__ __forceinline__ void locate_seq(const Params& p, int nseq, int lane, long long u, int& seq,
                                            long long& seq_start, int& err) {
   long long off = 0;
   for (int base = 0; base < nseq; base += 64) {
-    SeqInfo s = load_seq(p, base + lane, nseq, 0, err);
+    SeqInfo s = load_seq<MODE>(p, base + lane, nseq, 0, err);
     long long cnt = (long long)s.units * p.NG;
     long long incl = wave_incl_scan_units(cnt, lane);
     long long tile = rl64(incl, 63);
@@ -388,9 +436,10 @@ struct Window {
   SeqInfo s;
 };
 
+template <int MODE>
 __device__ __forceinline__ void load_window(const Params& p, int nseq, int base, int lane, Window& w, int& err) {
   w.base = base;
-  w.s = load_seq(p, base + lane, nseq, w.pf_min, err);
+  w.s = load_seq<MODE>(p, base + lane, nseq, w.pf_min, err);
 }
 
 struct Cursor {
@@ -399,6 +448,7 @@ struct Cursor {
   int c0;           // first chunk of the row block (rb_first_chunk: > 0 only with a sliding window)
   int nrb;
   int kv_len, q_len, q_start;
+  int pbase;  // fused step: the sequence's first page entry
   // first key of the cursor's chunk
   __device__ __forceinline__ int key0() const { return (c0 + c) * KV_CHUNK; }
 };
@@ -409,18 +459,23 @@ __device__ __forceinline__ void set_row_block(const Params& p, Cursor& x) {
   x.c0 = rb_first_chunk(x.kv_len, x.q_len, p.G, x.rb, p.skip_masked, p.sliding_window);
 }
 
+template <int MODE>
 __device__ __forceinline__ void cursor_load_seq(const Params& p, const Window& w, int i, Cursor& x) {
   int k = i - w.base;
   x.i = i;
   x.kv_len = rl(w.s.kv_len, k);
   x.q_len = rl(w.s.q_len, k);
-  x.q_start = rl(w.s.q_start, k);
+  const int qs = rl(w.s.q_start, k);
+  const bool fz = fused_on<MODE>(p);
+  x.q_start = fz ? i : qs;  // fused step: q row i; the field held the first page entry
+  x.pbase = fz ? qs : 0;
   x.nrb = num_row_blocks(x.q_len, p.G);
 }
 
+template <int MODE>
 __device__ __forceinline__ Cursor cursor_at(const Params& p, const Window& w, int seq, long long ul) {
   Cursor x;
-  cursor_load_seq(p, w, seq, x);
+  cursor_load_seq<MODE>(p, w, seq, x);
   int per_head = rl(w.s.units, seq - w.base);
   // one kv-head group: no division; else a 32-bit division when it fits
   x.h = p.NG == 1 ? 0 : (ul < (1ll << 31) ? (int)ul / per_head : (int)(ul / per_head));
@@ -438,6 +493,7 @@ __device__ __forceinline__ Cursor cursor_at(const Params& p, const Window& w, in
   return x;
 }
 
+template <int MODE>
 __device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Window& w, Cursor& x, int& err) {
   if (x.c + 1 < x.nch) {
     x.c++;
@@ -458,10 +514,10 @@ __device__ __forceinline__ void advance(const Params& p, int nseq, int lane, Win
           x.nch = 0;
           return;
         }
-        if (i >= w.base + 64) load_window(p, nseq, i, lane, w, err);
+        if (i >= w.base + 64) load_window<MODE>(p, nseq, i, lane, w, err);
         if (rl(w.s.units, i - w.base) > 0) break;
       }
-      cursor_load_seq(p, w, i, x);
+      cursor_load_seq<MODE>(p, w, i, x);
       x.h = 0;
       x.rb = 0;
     }
@@ -484,19 +540,25 @@ struct Pages {
 // outstanding loads exactly (s_waitcnt vmcnt(N)) so the next unit's loads stay in flight.
 // UPG: page_size is a multiple of KV_CHUNK, so a chunk lies in one page and its page id is
 // wave-uniform: one scalar load instead of two vector loads per lane.
-template <bool UPG>
+template <int MODE, bool UPG>
+__device__ __forceinline__ size_t page_row(const Params& p, const Cursor& x) {
+  if (fused_on<MODE>(p)) return (size_t)x.pbase;
+  return (size_t)x.i * p.PPS;
+}
+
+template <int MODE, bool UPG>
 __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, int n) {
   Pages r;
   if constexpr (UPG) {
     // one load at a wave-uniform address, kept per lane until it is used (a step later)
-    const size_t idx = x.nch > 0 ? (size_t)x.i * p.PPS + page_of(x.key0(), p) : 0;
+    const size_t idx = x.nch > 0 ? page_row<MODE, UPG>(p, x) + page_of(x.key0(), p) : 0;
     const int pg = p.page_indices[idx + opaque_zero()];
     r.pg[0] = r.pg[1] = pg;
     return r;
   }
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
-  const size_t row = live ? (size_t)x.i * p.PPS : 0;
+  const size_t row = live ? page_row<MODE, UPG>(p, x) : 0;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.key0() + 16 * blk + n;
@@ -531,6 +593,7 @@ struct HalfRegs<KV_BF16_BIAS> {
 // lies inside the row, and entries of keys outside the window are 0.  A lane's 4 consecutive keys
 // (a multiple-of-4 start) are one aligned 16-byte load; chunks before the window read the zero head.
 constexpr int kBiasHead = 32;
+constexpr int kRelRows = 16;  // relative-bias width of the fused step's in-kernel bias (rel_states [.., 16])
 __host__ __device__ __forceinline__ int bias_row_len(int E) { return ((E + 31) / 32 + 1) * 32; }
 __host__ __device__ __forceinline__ int bias_chunk_lo(int kv_len, int E) { return kv_len > E ? (kv_len - E) / 32 : 0; }
 template <>
@@ -628,16 +691,27 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 // Query rows of cursor x as the B operand of QK^T.  Rows past q_len * G read row 0 of the
 // sequence instead: their columns of S and O are never stored, and MFMA columns are independent.
 template <int MODE>
-__device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, int wv, bf16x8 q[4]) {
+// rst (fused step with a relative bias): components 4j .. 4j+3 of the row's rel_states, loaded
+// with its queries (once per row block).
+__device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, int wv, bf16x8 q[4],
+                                       uint32_t* rst = nullptr) {
   const bool live = x.nch > 0;
   int row = x.rb * ROW_BLOCK + n;
   if (!(live && row < x.q_len * p.G)) row = 0;
   const int tok = row / p.G;
   const int g = row - tok * p.G;
   const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)(x.h * p.HG + wv) * p.G : 0;
-  const uint16_t* qp = p.q + ((size_t)tok * p.Hq + base + g) * kD;
+  const size_t qrow = (size_t)tok * p.Hq + base + g;
+  const uint16_t* qp = p.q + qrow * kD;
 #pragma unroll
   for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + kdim<MODE>(j, s)));
+  if constexpr (MODE == KV_BF16_FUSED) {
+    if (rst && p.rel_states) {
+      const uint2 sv = *(const uint2*)(p.rel_states + qrow * kRelRows + 4 * j);
+      rst[0] = sv.x;
+      rst[1] = sv.y;
+    }
+  }
 }
 
 // bf16(float(x) * scale) for 8 packed bf16 values (the reference's k_scale formula, :124-129).
@@ -722,7 +796,7 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
   const int first_row_limit = x.kv_len - x.q_len + (x.rb * ROW_BLOCK) / p.G + 1;  // keys seen by row 0
   bool plain = !(p.soft_cap > 0.f) && p.sliding_window <= 0 &&
                x.key0() + KV_CHUNK <= (first_row_limit < x.kv_len ? first_row_limit : x.kv_len);
-  if (MODE != KV_BF16_BIAS && plain && p.scale_log2 > 0.f) {
+  if (!has_bias<MODE>() && plain && p.scale_log2 > 0.f) {
     // the raw scores' maximum, scaled once (a positive scale commutes with each score's rounding),
     // and each probability as exp2(fma(s, scale, -m))
     const float mr = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
@@ -756,7 +830,7 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
     for (int rr = 0; rr < 4; ++rr) {
       xs[0][rr] = s0[rr] * p.scale_log2;
       xs[1][rr] = s1[rr] * p.scale_log2;
-      if constexpr (MODE == KV_BF16_BIAS) {  // the table holds 0 for keys outside the window
+      if constexpr (has_bias<MODE>()) {  // the bias is 0 for keys outside the window
         xs[0][rr] += bias[0][rr] * kLog2e;
         xs[1][rr] += bias[1][rr] * kLog2e;
       }
@@ -776,7 +850,7 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
           xv = sv * p.scale_log2;
         }
         int kt = key0 + 16 * blk + rr;
-        if constexpr (MODE == KV_BF16_BIAS) xv += bias[blk][rr] * kLog2e;
+        if constexpr (has_bias<MODE>()) xv += bias[blk][rr] * kLog2e;
         bool masked = kt > st.pos || (p.sliding_window > 0 && kt <= st.pos - p.sliding_window);
         if (masked) xv += p.mask_log2;
         if (kt >= x.kv_len) xv = -INFINITY;
@@ -964,10 +1038,10 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   // Every buffer is redefined each step.
   Cursor ahead = nxt;
   if (u + 2 < u1)
-    advance(p, nseq, lane, win, ahead, err);
+    advance<MODE>(p, nseq, lane, win, ahead, err);
   else
     ahead.nch = 0;
-  const Pages pg_ahead = load_pages<UPG>(p, ahead, n);
+  const Pages pg_ahead = load_pages<MODE, UPG>(p, ahead, n);
   const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, wv, err);
   // keep the workgroup's waves (the kv heads of one group) in step, so the heads' slices of the
   // same keys reach the memory system together
@@ -1009,7 +1083,8 @@ constexpr int kWaveLds = kVtBytes_ + kKtBytes;
 
 template <int MODE, bool UPG>
 struct LinePath {
-  static constexpr bool on = UPG && (MODE == KV_BF16 || MODE == KV_BF16_SCALED || MODE == KV_BF16_BIAS);
+  static constexpr bool on =
+      UPG && (MODE == KV_BF16 || MODE == KV_BF16_SCALED || MODE == KV_BF16_BIAS || MODE == KV_BF16_FUSED);
 };
 
 struct LineRegs {
@@ -1020,10 +1095,13 @@ struct LineAddr {
   size_t e0;    // element index of this lane's dims of the unit's first key, K row
   int kmax;     // the unit's last key with data (keys past it read it instead)
   int bias_at;  // as UnitAddr
+  int knew;       // fused step: the unit's key (0..31) read from new_k / new_v instead, -1 = none
+  size_t newoff;  // fused step: element index of this lane's dims of that key's row in new_k / new_v
 };
 
 __device__ __forceinline__ int vt_swz(int row, int g) { return g ^ ((row >> 3) & 3); }
 
+template <int MODE>
 __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, const Pages& pages, int lane, int n,
                                               int j, int wv, int& err) {
   const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err);  // page checks, head, bias position
@@ -1033,26 +1111,115 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
   const int k = live ? x.kv_len - 1 - x.key0() : 0;
   a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
   a.bias_at = u.bias_at;
+  a.knew = -1;
+  a.newoff = 0;
+  if constexpr (MODE == KV_BF16_FUSED) {
+    // the step's new token (key kv_len-1) is not in the cache yet: its rows come from new_k/new_v
+    if (live && k < KV_CHUNK) {
+      a.knew = k;
+      a.newoff = ((size_t)x.i * p.Hkv + u.h) * kD + 8 * (lane & 15);
+    }
+  }
   return a;
 }
 
 // which = 0: K rows (combined head 2h), 1: V rows (2h+1).
+template <int MODE>
 __device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, int lane, int which, LineRegs& r) {
   const uint16_t* kv = (const uint16_t*)p.kv + a.e0 + (size_t)which * kD;
   const size_t row = (size_t)(2 * p.Hkv) * kD;
+  const uint16_t* nw = nullptr;
+  if constexpr (MODE == KV_BF16_FUSED) nw = (which ? p.new_v : p.new_k) + a.newoff;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     int key = 4 * i + (lane >> 4);
     key = key < a.kmax ? key : a.kmax;
-    r.w[i] = ld_stream((const u32x4*)(kv + (size_t)key * row));
+    const uint16_t* src = kv + (size_t)key * row;
+    if constexpr (MODE == KV_BF16_FUSED) src = key == a.knew ? nw : src;  // the step's new token
+    r.w[i] = ld_stream((const u32x4*)src);
   }
 }
 
+// The bias inputs of one unit, loaded with its K.  Table mode: the two f32x4 table entries of the
+// lane's keys (as bits).  Relative mode (rel_proj set): two 8-element groups of rel_proj rows over
+// the unit's distance window (row lane/4, groups lane%4 and 4); the row's rel_states come with its
+// queries (load_q).
+struct LineBias {
+  u32x4 w[2];
+};
+
+// Relative bias staging per wave (after the HG wave regions): 16 rel_proj rows x 40 distances
+// (bf16), row stride 80 bytes.  A unit's 32 keys have distances dlo .. dlo+31 (dlo = kv_len - 1 -
+// key0 - 31); the window holds the five aligned 8-element groups from dlo & ~7.
+constexpr int kRelRowBytes = 80;
+constexpr int kRelStage = kRelRows * kRelRowBytes;
+
+__device__ __forceinline__ int rel_dlo(const Cursor& x) { return x.kv_len - 1 - x.key0() - (KV_CHUNK - 1); }
+
 template <int MODE>
-__device__ __forceinline__ void load_line_bias(const Params& p, const LineAddr& a, f32x4 bias[2]) {
+__device__ __forceinline__ void load_line_bias(const Params& p, const Cursor& x, const LineAddr& a, int lane, int n,
+                                               int j, int wv, LineBias& b) {
+  if constexpr (MODE == KV_BF16_FUSED) {
+    {
+      // groups gbase + (lane & 3) and gbase + 4 of rel_proj row lane >> 2 (clamped into the table:
+      // groups outside [0, E/8) are zeroed when staged).  A unit with no key in the window reads
+      // one 16-byte group at one address (one cache line per instruction).
+      const int dlo = rel_dlo(x), gbase = dlo >> 3, ng = p.rel_extent >> 3;
+      const bool inw = x.nch > 0 && dlo < p.rel_extent && dlo + KV_CHUNK - 1 >= 0;
+      const int r = inw ? lane >> 2 : 0;
+      int g0 = gbase + (lane & 3), g1 = gbase + 4;
+      g0 = !inw || g0 < 0 ? 0 : (g0 >= ng ? ng - 1 : g0);
+      g1 = !inw || g1 < 0 ? 0 : (g1 >= ng ? ng - 1 : g1);
+      b.w[0] = *(const u32x4*)(p.rel_proj + (size_t)r * p.rel_extent + 8 * g0);
+      b.w[1] = *(const u32x4*)(p.rel_proj + (size_t)r * p.rel_extent + 8 * g1);
+    }
+  }
   if constexpr (MODE == KV_BF16_BIAS) {
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at + 16 * blk);  // aligned
+    for (int blk = 0; blk < 2; ++blk)
+      b.w[blk] = *(const u32x4*)(p.rel_bias + a.bias_at + 16 * blk);  // aligned
+  }
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// The bias of the lane's 8 scores (keys 16*blk + 4j + rr of row n) from the unit's LineBias.
+// Relative mode: the five groups are staged in the wave's rows, then bias[blk] = P_blk @ S with
+// P_blk[key][r] = rel_proj[r][distance of key] (16 x 16, zero outside [0, E)) and S[r][row] =
+// rel_states[q head of row][r]: one 16x16x16 bf16 MFMA per 16 keys, fp32 sums of exact products.
+template <int MODE>
+__device__ __forceinline__ void line_bias_values(const Params& p, const Cursor& x, const LineBias& b,
+                                                 const uint32_t rst[2], uint8_t* rs, int lane, int n, int j,
+                                                 f32x4 bias[2]) {
+  if constexpr (MODE == KV_BF16_FUSED) {
+    {
+      const int dlo = rel_dlo(x), gbase = dlo >> 3, ng = p.rel_extent >> 3;
+      bias[0] = bias[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (x.nch <= 0 || dlo >= p.rel_extent || dlo + KV_CHUNK - 1 < 0) return;  // no key in the window
+      const int r = lane >> 2, g0 = gbase + (lane & 3), g1 = gbase + 4;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      wave_lds_fence();  // the previous unit's fragments have been read
+      *(u32x4*)(rs + r * kRelRowBytes + 16 * (lane & 3)) = g0 >= 0 && g0 < ng ? b.w[0] : z;
+      if ((lane & 3) == 0) *(u32x4*)(rs + r * kRelRowBytes + 64) = g1 >= 0 && g1 < ng ? b.w[1] : z;
+      wave_lds_fence();
+      short4_t sb;
+      sb[0] = (short)(rst[0] & 0xffffu);
+      sb[1] = (short)(rst[0] >> 16);
+      sb[2] = (short)(rst[1] & 0xffffu);
+      sb[3] = (short)(rst[1] >> 16);
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        const int col = dlo + (KV_CHUNK - 1) - (16 * blk + n) - 8 * gbase;  // 0 .. 38
+        short4_t a;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[t] = *(const short*)(rs + (4 * j + t) * kRelRowBytes + 2 * col);
+        bias[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, sb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      }
+    }
+  }
+  if constexpr (MODE == KV_BF16_BIAS) {
+    bias[0] = __builtin_bit_cast(f32x4, b.w[0]);
+    bias[1] = __builtin_bit_cast(f32x4, b.w[1]);
   }
 }
 
@@ -1075,7 +1242,8 @@ __device__ __forceinline__ void store_k_tile(const Params& p, const LineRegs& k,
 // next unit's V loaded into v (after its V^T store).
 template <int MODE>
 __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor& x, LineRegs& v, const f32x4* bias,
-                                                  bf16x8 q[4], const Cursor& nx, const LineAddr& nx_addr,
+                                                  bf16x8 q[4], uint32_t rst[2], const Cursor& nx,
+                                                  const LineAddr& nx_addr,
                                                   RowState& st, uint8_t* vt, const uint8_t* kt, int lane, int n,
                                                   int j, int wv) {
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -1105,8 +1273,8 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
   // a new row block's queries (else q already holds its rows), issued after the wait for this
   // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
   // issued before it they would make that wait also retire the next unit's K
-  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);
-  load_lines(p, nx_addr, lane, 1, v);
+  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst);
+  load_lines<MODE>(p, nx_addr, lane, 1, v);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
 
@@ -1127,22 +1295,23 @@ template <int MODE, bool UPG>
 __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, int n, int j, int b, long long u,
                                           long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
                                           Pages& pg_nxt, LineRegs& k, LineRegs& v, f32x4 bias[2], bf16x8 q[4],
-                                          RowState& st, uint8_t* vt, uint8_t* kt, int& err, const Partition& pt,
-                                          int wv) {
+                                          uint32_t rst[2], RowState& st, uint8_t* vt, uint8_t* kt, uint8_t* rs,
+                                          int& err,
+                                          const Partition& pt, int wv) {
   Cursor ahead = nxt;
   if (u + 2 < u1)
-    advance(p, nseq, lane, win, ahead, err);
+    advance<MODE>(p, nseq, lane, win, ahead, err);
   else
     ahead.nch = 0;
-  const Pages pg_ahead = load_pages<UPG>(p, ahead, n);
-  const LineAddr nx_addr = line_addr(p, nxt, pg_nxt, lane, n, j, wv, err);
+  const Pages pg_ahead = load_pages<MODE, UPG>(p, ahead, n);
+  const LineAddr nx_addr = line_addr<MODE>(p, nxt, pg_nxt, lane, n, j, wv, err);
   __syncthreads();
-  load_lines(p, nx_addr, lane, 0, k);  // the next unit's K (this unit's K is in the tile)
-  f32x4 bias_nx[2];
-  load_line_bias<MODE>(p, nx_addr, bias_nx);
+  load_lines<MODE>(p, nx_addr, lane, 0, k);  // the next unit's K (this unit's K is in the tile)
+  LineBias bias_nx;
+  load_line_bias<MODE>(p, nxt, nx_addr, lane, n, j, wv, bias_nx);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit_line<MODE>(p, cur, v, bias, q, nxt, nx_addr, st, vt, kt, lane, n, j, wv);
+  compute_unit_line<MODE>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv);
   // The next unit's K goes to the tile before a row block's finish stores: its wait then counts
   // the same younger operations (the next unit's V) on every path.  Issued before it, the stores
   // made that wait also retire most of the V just loaded on the steps that end a row block.
@@ -1153,10 +1322,7 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
     finish_row_block(p, cur, st, b, complete, n, j, wv);
     if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
-  if constexpr (MODE == KV_BF16_BIAS) {
-    bias[0] = bias_nx[0];
-    bias[1] = bias_nx[1];
-  }
+  line_bias_values<MODE>(p, nxt, bias_nx, rst, rs, lane, n, j, bias);
 
   pg_nxt = pg_ahead;
   cur = nxt;
@@ -1645,15 +1811,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int nseq, tv, pf_min;
   {
     int kv[kWin], c0[kWin], c1[kWin];
-    const int ns_raw = p.num_seqs[0];
+    // fused decode step: q rows 0..B-1 one per sequence, cu_kv in place of the second q bound
+    constexpr bool fz = MODE == KV_BF16_FUSED;
+    const int ns_raw = fz ? p.fused_nseq : p.num_seqs[0];
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
       kv[w] = c0[w] = c1[w] = 0;
       const int i = 64 * w + lane;
       if (i < p.Nmax) {
         kv[w] = p.kv_lens[i];
-        c0[w] = p.cu_q_lens[i];
-        c1[w] = p.cu_q_lens[i + 1];
+        if (fz) {
+          c0[w] = i;
+          c1[w] = p.cu_kv[i];
+        } else {
+          c0[w] = p.cu_q_lens[i];
+          c1[w] = p.cu_q_lens[i + 1];
+        }
       }
     }
     nseq = uni(ns_raw);
@@ -1663,14 +1836,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int w = 0; w < kWin; ++w)
       if (nseq > 64 * w && nseq <= 64 * (w + 1)) tv = rl(c1[w], nseq - 1 - 64 * w);
-    if (nseq > 64 * kWin) tv = uni(p.cu_q_lens[nseq]);
+    if (nseq > 64 * kWin) tv = fz ? 0 : uni(p.cu_q_lens[nseq]);
+    if (fz) tv = nseq;
     // prefill tiles need the whole metadata in the four windows
     pf_min = (MODE == KV_BF16 && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
       wsi[w] = SeqInfo{0, 0, 0, 0};
-      if (nseq > 64 * w)  // windows past num_seqs hold no sequence (a uniform branch)
-        wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, pf_min, err);
+      if (nseq > 64 * w) {  // windows past num_seqs hold no sequence (a uniform branch)
+        if (fz)
+          wsi[w] = make_fused_seq(p, kv[w], c1[w], c0[w], 64 * w + lane < nseq, err);
+        else
+          wsi[w] = make_seq(p, kv[w], c0[w], c1[w], 64 * w + lane < nseq, pf_min, err);
+      }
     }
   }
   win.pf_min = pf_min;
@@ -1682,7 +1860,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       W += tile[w];
     }
   } else {
-    W = total_units(p, nseq, lane, err);
+    W = total_units<MODE>(p, nseq, lane, err);
   }
 
   // Work split: the first gpre workgroups take prefill tiles, the rest run stream-K over the
@@ -1756,37 +1934,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         seq_start = uni64(off_sel + rl64(incl - cnt, idx));
       }
     } else {
-      locate_seq(p, nseq, lane, u0, seq, seq_start, err);
-      load_window(p, nseq, seq, lane, win, err);
+      locate_seq<MODE>(p, nseq, lane, u0, seq, seq_start, err);
+      load_window<MODE>(p, nseq, seq, lane, win, err);
     }
     if (seq < nseq) {
-      Cursor cur = cursor_at(p, win, seq, u0 - seq_start);
+      Cursor cur = cursor_at<MODE>(p, win, seq, u0 - seq_start);
       Cursor nxt = cur;
       if (u0 + 1 < u1)
-        advance(p, nseq, lane, win, nxt, err);
+        advance<MODE>(p, nseq, lane, win, nxt, err);
       else
         nxt.nch = 0;
-      const Pages pg_cur = load_pages<UPG>(p, cur, n);
-      Pages pg_nxt = load_pages<UPG>(p, nxt, n);
+      const Pages pg_cur = load_pages<MODE, UPG>(p, cur, n);
+      Pages pg_nxt = load_pages<MODE, UPG>(p, nxt, n);
       if constexpr (LinePath<MODE, UPG>::on) {
         LineRegs k, v;
         f32x4 bias[2];
+        LineBias bias_in;
         bf16x8 q[4];
+        uint32_t rst[2] = {0u, 0u};
+        uint8_t* rs = smem + p.HG * kWaveLds + wv * kRelStage;  // relative-bias staging (fused step)
         // K, bias, queries, V: the loop's order (vmcnt retires in order, and the compiler
         // counts each wait for the least favourable path into it, this prologue included)
         {
-          const LineAddr a0 = line_addr(p, cur, pg_cur, lane, n, j, wv, err);
-          load_lines(p, a0, lane, 0, k);
-          load_line_bias<MODE>(p, a0, bias);
-          load_q<MODE>(p, cur, n, j, wv, q);
-          load_lines(p, a0, lane, 1, v);
+          const LineAddr a0 = line_addr<MODE>(p, cur, pg_cur, lane, n, j, wv, err);
+          load_lines<MODE>(p, a0, lane, 0, k);
+          load_line_bias<MODE>(p, cur, a0, lane, n, j, wv, bias_in);
+          load_q<MODE>(p, cur, n, j, wv, q, rst);
+          load_lines<MODE>(p, a0, lane, 1, v);
         }
         store_k_tile<MODE>(p, k, kt, lane);
+        line_bias_values<MODE>(p, cur, bias_in, rst, rs, lane, n, j, bias);
         RowState st;
         long long u = u0;
         for (;;) {
-          step_line<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, k, v, bias, q, st, vt, kt,
-                               err, pt, wv);
+          step_line<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, k, v, bias, q, rst, st, vt,
+                               kt, rs, err, pt, wv);
           if (++u >= u1) break;
         }
       } else {
@@ -2560,6 +2742,33 @@ __device__ __forceinline__ void combine_prefill(const Params& p, int idx, float 
 // the block is heavy (its slot's helper workgroups merge it).  After the (descriptor, head)
 // workgroups come the heavy-merge helpers, then (with the prefill kernel) 16 per prefill
 // workgroup for its split tiles.
+// Fused decode step: block s stores sequence s's new token (key kv_len-1, K of kv head h at combined
+// row 2h, V at 2h+1) into the cache, at slot (kv_len-1) % S of page page_indices[cu_kv[s] / S +
+// (kv_len-1) / S] (src/tpu_cake/workloads/inkling_rpa.py:518-534).  The attention kernel read
+// that key from new_k / new_v, so the store may follow it.  Anything out of range is skipped and
+// flagged.
+__device__ __forceinline__ void fused_store_token(const Params& p, int s) {
+  if (s >= p.fused_nseq) return;
+  const int len = p.kv_lens[s], cu = p.cu_kv[s];
+  const int pos = len - 1;
+  const long long entry = (long long)(cu >= 0 ? cu / p.S : 0) + (pos >= 0 ? pos / p.S : 0);
+  bool ok = len >= 1 && (long long)len <= (long long)p.PPS * p.S && cu >= 0 && cu % p.S == 0 &&
+            entry < p.fused_entries;
+  const int page = ok ? p.page_indices[entry] : 0;
+  ok = ok && page >= 0 && page < p.P;
+  if (!ok) {
+    if (threadIdx.x == 0) atomicOr(p.err, ERR_PAGE);
+    return;
+  }
+  uint16_t* rows = (uint16_t*)p.kv + ((size_t)page * p.S + pos % p.S) * (size_t)(2 * p.Hkv) * kD;
+  const int n = 2 * p.Hkv * kD;
+  for (int i = 8 * threadIdx.x; i < n; i += 8 * blockDim.x) {
+    const int r = i / kD, d = i - r * kD;
+    const uint16_t* src = ((r & 1) ? p.new_v : p.new_k) + ((size_t)s * p.Hkv + (r >> 1)) * kD + d;
+    *(u32x4*)(rows + i) = *(const u32x4*)src;
+  }
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
   __shared__ float red[3][64][33];    // waves 1..3's o (33: conflict-free row stride)
   __shared__ float redml[3][64][16];  // waves 1..3's (m, l) per row slot
@@ -2568,6 +2777,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     const int hb = blockIdx.x - p.grid * p.HG, nheavy = heavy_slots(p.grid) * p.HG * kHeavySlices;
     if (hb < nheavy)
       combine_heavy(p, hb, red, redml);
+    else if (p.fused)
+      fused_store_token(p, hb - nheavy);
     else
       combine_prefill(p, hb - nheavy, red, redml);
     return;
@@ -2648,8 +2859,12 @@ int fail(int code, const std::string& msg) {
 
 constexpr size_t kHeaderBytes = 256;
 
+// Zeros standing in for rel_proj ([16, 8]) when the fused step has no relative bias.
+__device__ uint16_t g_zero_proj[kRelRows * 8];
+
 struct DeviceInfo {
   int cus = 0;
+  const uint16_t* zero_proj = nullptr;  // this device's g_zero_proj
   int grid[kModes][9] = {};  // workgroups per launch, by kv mode and heads per workgroup (1..8)
 };
 
@@ -2670,8 +2885,10 @@ constexpr int kVtBytes = kWaveLds;  // LDS per wave: V^T chunk + K tile
 template <int MODE>
 int occupancy_grid(int cus, int hg) {
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE, false>, 64 * hg, hg * kVtBytes) !=
-          hipSuccess ||
+  // the fused step runs only on the full-line path, with its relative-bias staging
+  constexpr bool kFused = MODE == KV_BF16_FUSED;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE, kFused>, 64 * hg,
+                                                   hg * (kVtBytes + (kFused ? kRelStage : 0))) != hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
   int max_groups = kMaxWavesPerCU / hg;
@@ -2705,7 +2922,11 @@ int device_info(DeviceInfo& out) {
       d.grid[KV_BF16_SCALED][hg] = occupancy_grid<KV_BF16_SCALED>(cus, hg);
       d.grid[KV_FP8][hg] = occupancy_grid<KV_FP8>(cus, hg);
       d.grid[KV_BF16_BIAS][hg] = occupancy_grid<KV_BF16_BIAS>(cus, hg);
+      d.grid[KV_BF16_FUSED][hg] = occupancy_grid<KV_BF16_FUSED>(cus, hg);
     }
+    // 8 zero columns of a 16-wide relative projection: the fused step without a relative bias
+    if (hipGetSymbolAddress((void**)&d.zero_proj, HIP_SYMBOL(g_zero_proj)) != hipSuccess || !d.zero_proj)
+      return fail(RPA_E_HIP, "hipGetSymbolAddress(zero projection) failed");
     d.cus = cus;
   }
   out = d;
@@ -3170,15 +3391,26 @@ int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* 
   return RPA_OK;
 }
 
+// The fused decode step's own inputs when it runs in the attention launch (Params::fused).
+struct FusedInline {
+  int nseq, entries;
+  const int32_t* cu_kv;
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  const uint16_t* rel_states;  // nullptr: no relative bias
+  const uint16_t* rel_proj;
+  int rel_extent;
+};
+
 static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const void* q, const void* kv_pages,
                       const float* kv_scales, const int32_t* kv_lens, const int32_t* page_indices,
                       const int32_t* cu_q_lens, const int32_t* num_seqs, void* out, void* workspace,
                       size_t workspace_bytes, void* stream, void* ev_begin, void* ev_end,
-                      const float* rel_bias = nullptr, int rel_extent = 0) {
+                      const float* rel_bias = nullptr, int rel_extent = 0, const FusedInline* fz = nullptr) {
   int rc = check_shape(shape);
   if (rc) return rc;
   if (!opt) return fail(RPA_E_INVALID, "options is NULL");
-  if (!kv_lens || !page_indices || !cu_q_lens || !num_seqs || !kv_pages)
+  if (!kv_lens || !page_indices || (!fz && (!cu_q_lens || !num_seqs)) || !kv_pages)
     return fail(RPA_E_INVALID, "NULL metadata or kv_pages pointer");
   if (shape->num_tokens > 0 && (!q || !out)) return fail(RPA_E_INVALID, "NULL q or out pointer");
   if (q == out && q) return fail(RPA_E_INVALID, "out must not alias q");
@@ -3228,7 +3460,19 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   p.v_scale = opt->has_v_scale ? opt->v_scale : 1.f;
 
   int mode = KV_BF16;
-  if (rel_bias) {
+  if (fz) {  // the fused decode step in the attention launch (bias, if any, formed in the kernel)
+    if (p.S % KV_CHUNK) return fail(RPA_E_INVALID, "fused step in one launch needs a page size multiple of 32");
+    mode = KV_BF16_FUSED;
+    p.fused = 1;
+    p.fused_nseq = fz->nseq;
+    p.fused_entries = fz->entries;
+    p.cu_kv = fz->cu_kv;
+    p.new_k = fz->new_k;
+    p.new_v = fz->new_v;
+    p.rel_states = fz->rel_states;
+    p.rel_proj = fz->rel_states ? fz->rel_proj : d.zero_proj;
+    p.rel_extent = fz->rel_states ? fz->rel_extent : 8;
+  } else if (rel_bias) {
     if (shape->kv_dtype != RPA_KV_BF16 || kv_scales || opt->has_k_scale || opt->has_v_scale || rel_extent <= 0)
       return fail(RPA_E_INVALID, "a relative bias needs bf16 kv_pages without scales and a positive extent");
     mode = KV_BF16_BIAS;
@@ -3265,8 +3509,10 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");
   const bool upg = p.S % KV_CHUNK == 0;
   const dim3 grid(p.grid), block(64 * p.HG);
-  const size_t lds = (size_t)p.HG * kVtBytes;
-  if (mode == KV_BF16_BIAS) {
+  const size_t lds = (size_t)p.HG * (kVtBytes + (mode == KV_BF16_FUSED ? kRelStage : 0));
+  if (mode == KV_BF16_FUSED) {
+    hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_FUSED, true>), grid, block, lds, st, p);
+  } else if (mode == KV_BF16_BIAS) {
     if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, false>), grid, block, lds, st, p);
   } else if (mode == KV_FP8) {
@@ -3291,7 +3537,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot, then 16 per
   // prefill workgroup
   hipLaunchKernelGGL(rpa_combine_kernel,
-                     dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0)),
+                     dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0) +
+                          (p.fused ? p.fused_nseq : 0)),
                      dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
@@ -3458,6 +3705,30 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
     return fail(RPA_E_WORKSPACE, "fused workspace of " + std::to_string(workspace_bytes) + " bytes, need " +
                                      std::to_string(l.total));
   uint8_t* ws = (uint8_t*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  // One attention launch (metadata, new token and relative bias handled in the kernel, the token
+  // stored by the combine launch) for full 128-dim heads on the full-line path with aligned
+  // tensors and a 16-wide relative projection; the prep launch below otherwise.
+  const bool aligned = ((uintptr_t)queries | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)cache |
+                        (uintptr_t)relative_states | (uintptr_t)relative_projection) % 16 == 0;
+  if (f->head_dim == kD && f->page_size % KV_CHUNK == 0 && aligned &&
+      (f->relative_dim == 0 || (f->relative_dim == kRelRows && f->relative_extent % 8 == 0))) {
+    const rpa_shape_t rs = fused_rpa_shape(f);
+    rpa_options_t o;
+    memset(&o, 0, sizeof(o));
+    o.sm_scale = sm_scale;
+    FusedInline fi;
+    fi.nseq = f->num_seqs;
+    fi.entries = f->page_entries;
+    fi.cu_kv = cu_kv_lens;
+    fi.new_k = (const uint16_t*)keys;
+    fi.new_v = (const uint16_t*)values;
+    fi.rel_states = f->relative_dim > 0 ? (const uint16_t*)relative_states : nullptr;
+    fi.rel_proj = f->relative_dim > 0 ? (const uint16_t*)relative_projection : nullptr;
+    fi.rel_extent = f->relative_dim > 0 ? f->relative_extent : 0;
+    return launch_rpa(&rs, &o, queries, cache, nullptr, kv_lens, page_indices, nullptr, nullptr, out, workspace,
+                      workspace_bytes, stream, nullptr, nullptr, nullptr, 0, &fi);
+  }
   FusedArgs a;
   a.q = (const uint16_t*)queries;
   a.keys = (const uint16_t*)keys;
@@ -3485,7 +3756,6 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
   a.pps = f->pages_per_seq;
   a.R = f->relative_dim;
   a.E = f->relative_dim > 0 ? f->relative_extent : 0;
-  hipStream_t st = (hipStream_t)stream;
   a.vec = ((uintptr_t)cache | (uintptr_t)keys | (uintptr_t)values) % 16 == 0 && a.D % 8 == 0 && a.W % 8 == 0;
   const int write_blocks = a.B,
             bias_blocks = a.bias ? a.B * ((a.Hq + kBiasHeads - 1) / kBiasHeads) *
