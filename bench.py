@@ -257,7 +257,8 @@ def fused_bench(args, dev) -> int:
         "wall_s_timed_region": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": peak, "unit": "GB/s",
                      "frac": round(achieved / peak, 4), "traffic": measured_traffic("inkling"),
-                     "basis": "whole step (cache write, metadata and bias-table kernels, attention, combine)"},
+                     "basis": "whole step (every launch of the call: attention with the in-kernel bias, merge "
+                              "with the new-token store; a preparation launch first for shapes that need one)"},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline (fused oracle) ...")

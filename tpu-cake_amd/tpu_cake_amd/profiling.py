@@ -235,6 +235,8 @@ WRITE_SIZE = {copy_w:.0f} KiB (factor {wf:.3f}).
         cf, cw = _counters(raw / "fetch_inkling"), _counters(raw / "write_inkling")
         lines, tot = [], 0.0
         for k in ("rpa_fused_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel"):
+            if k not in cf or k not in cw:  # the one-launch form of the step has no prep launch
+                continue
             b = cf[k]["FETCH_SIZE"] * 1024 * ff + cw[k]["WRITE_SIZE"] * 1024 * wf
             tot += b
             lines.append(f"- {k}: FETCH_SIZE {cf[k]['FETCH_SIZE']:.0f} KiB x {ff:.3f}, WRITE_SIZE "
