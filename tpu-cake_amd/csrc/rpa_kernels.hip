@@ -346,11 +346,12 @@ __device__ __forceinline__ SeqInfo make_seq(const Params& p, int kv, int c0, int
   ql = bad_rows ? 0 : ql;
   e |= ql > kv ? ERR_QLEN : 0;
   const bool one_block = ql <= ROW_BLOCK && ql * p.G <= ROW_BLOCK;
+  const bool prefill = pf_min > 0 && ql >= pf_min;  // a prefill tile sequence: no units to count
+  const bool loop = !one_block && !prefill;
   int units = 0;
   if (ql > 0 && kv > 0) units = rb_units(kv, ql, p.G, 0, p.skip_masked, p.sliding_window);
-  if (__ballot(valid && !one_block) != 0 && !one_block)
-    units = seq_units_per_head(kv, ql, p.G, p.skip_masked, p.sliding_window);
-  if (pf_min > 0 && ql >= pf_min) units = 0;
+  if (__ballot(valid && loop) != 0 && loop) units = seq_units_per_head(kv, ql, p.G, p.skip_masked, p.sliding_window);
+  if (prefill) units = 0;
   err |= valid ? e : 0;
   SeqInfo s;
   s.kv_len = valid ? kv : 0;
