@@ -76,6 +76,8 @@ def test_decode_shapes(cuda, hq, hkv, d, page, lens):
     (32, 8, 64, [1, 31, 32, 33, 96, 700], 0, 512),
     (32, 8, 64, [1, 9, 40, 41, 300, 1025], 16, 40),
     (16, 2, 128, [2, 8, 129, 257], 16, 8),
+    (64, 16, 64, [3, 64, 128, 130, 900], 16, 512),   # two kv-head groups (Hkv 16): heads 8..15 in the second
+    (32, 8, 32, [32, 33, 64, 97], 16, 16),            # page 32: every unit its own page; window of 16
     # the prep launch: a window that is not a multiple of 8, a 32-wide projection
     (32, 8, 64, [5, 70, 200], 16, 20),
     (32, 8, 64, [5, 70, 200], 32, 64),
