@@ -541,7 +541,7 @@ struct Pages {
 // outstanding loads exactly (s_waitcnt vmcnt(N)) so the next unit's loads stay in flight.
 // UPG: page_size is a multiple of KV_CHUNK, so a chunk lies in one page and its page id is
 // wave-uniform: one scalar load instead of two vector loads per lane.
-template <int MODE, bool UPG>
+template <int MODE>
 __device__ __forceinline__ size_t page_row(const Params& p, const Cursor& x) {
   if (fused_on<MODE>(p)) return (size_t)x.pbase;
   return (size_t)x.i * p.PPS;
@@ -552,14 +552,14 @@ __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, in
   Pages r;
   if constexpr (UPG) {
     // one load at a wave-uniform address, kept per lane until it is used (a step later)
-    const size_t idx = x.nch > 0 ? page_row<MODE, UPG>(p, x) + page_of(x.key0(), p) : 0;
+    const size_t idx = x.nch > 0 ? page_row<MODE>(p, x) + page_of(x.key0(), p) : 0;
     const int pg = p.page_indices[idx + opaque_zero()];
     r.pg[0] = r.pg[1] = pg;
     return r;
   }
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
-  const size_t row = live ? page_row<MODE, UPG>(p, x) : 0;
+  const size_t row = live ? page_row<MODE>(p, x) : 0;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.key0() + 16 * blk + n;
@@ -691,9 +691,9 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 
 // Query rows of cursor x as the B operand of QK^T.  Rows past q_len * G read row 0 of the
 // sequence instead: their columns of S and O are never stored, and MFMA columns are independent.
-template <int MODE>
 // rst (fused step with a relative bias): components 4j .. 4j+3 of the row's rel_states, loaded
 // with its queries (once per row block).
+template <int MODE>
 __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, int wv, bf16x8 q[4],
                                        uint32_t* rst = nullptr) {
   const bool live = x.nch > 0;
@@ -1141,10 +1141,10 @@ __device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, i
   }
 }
 
-// The bias inputs of one unit, loaded with its K.  Table mode: the two f32x4 table entries of the
-// lane's keys (as bits).  Relative mode (rel_proj set): two 8-element groups of rel_proj rows over
-// the unit's distance window (row lane/4, groups lane%4 and 4); the row's rel_states come with its
-// queries (load_q).
+// The bias inputs of one unit, loaded with its K.  KV_BF16_BIAS: the two f32x4 table entries of
+// the lane's keys (as bits).  KV_BF16_FUSED: two 8-element groups of rel_proj rows over the unit's
+// distance window (row lane/4, groups lane%4 and 4); the row's rel_states come with its queries
+// (load_q).
 struct LineBias {
   u32x4 w[2];
 };
@@ -1161,19 +1161,17 @@ template <int MODE>
 __device__ __forceinline__ void load_line_bias(const Params& p, const Cursor& x, const LineAddr& a, int lane, int n,
                                                int j, int wv, LineBias& b) {
   if constexpr (MODE == KV_BF16_FUSED) {
-    {
-      // groups gbase + (lane & 3) and gbase + 4 of rel_proj row lane >> 2 (clamped into the table:
-      // groups outside [0, E/8) are zeroed when staged).  A unit with no key in the window reads
-      // one 16-byte group at one address (one cache line per instruction).
-      const int dlo = rel_dlo(x), gbase = dlo >> 3, ng = p.rel_extent >> 3;
-      const bool inw = x.nch > 0 && dlo < p.rel_extent && dlo + KV_CHUNK - 1 >= 0;
-      const int r = inw ? lane >> 2 : 0;
-      int g0 = gbase + (lane & 3), g1 = gbase + 4;
-      g0 = !inw || g0 < 0 ? 0 : (g0 >= ng ? ng - 1 : g0);
-      g1 = !inw || g1 < 0 ? 0 : (g1 >= ng ? ng - 1 : g1);
-      b.w[0] = *(const u32x4*)(p.rel_proj + (size_t)r * p.rel_extent + 8 * g0);
-      b.w[1] = *(const u32x4*)(p.rel_proj + (size_t)r * p.rel_extent + 8 * g1);
-    }
+    // groups gbase + (lane & 3) and gbase + 4 of rel_proj row lane >> 2 (clamped into the table:
+    // groups outside [0, E/8) are zeroed when staged).  A unit with no key in the window reads
+    // one 16-byte group at one address (one cache line per instruction).
+    const int dlo = rel_dlo(x), gbase = dlo >> 3, ng = p.rel_extent >> 3;
+    const bool inw = x.nch > 0 && dlo < p.rel_extent && dlo + KV_CHUNK - 1 >= 0;
+    const int r = inw ? lane >> 2 : 0;
+    int g0 = gbase + (lane & 3), g1 = gbase + 4;
+    g0 = !inw || g0 < 0 ? 0 : (g0 >= ng ? ng - 1 : g0);
+    g1 = !inw || g1 < 0 ? 0 : (g1 >= ng ? ng - 1 : g1);
+    b.w[0] = *(const u32x4*)(p.rel_proj + (size_t)r * p.rel_extent + 8 * g0);
+    b.w[1] = *(const u32x4*)(p.rel_proj + (size_t)r * p.rel_extent + 8 * g1);
   }
   if constexpr (MODE == KV_BF16_BIAS) {
 #pragma unroll
@@ -1185,7 +1183,7 @@ __device__ __forceinline__ void load_line_bias(const Params& p, const Cursor& x,
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // The bias of the lane's 8 scores (keys 16*blk + 4j + rr of row n) from the unit's LineBias.
-// Relative mode: the five groups are staged in the wave's rows, then bias[blk] = P_blk @ S with
+// KV_BF16_FUSED: the five groups are staged in the wave's rows, then bias[blk] = P_blk @ S with
 // P_blk[key][r] = rel_proj[r][distance of key] (16 x 16, zero outside [0, E)) and S[r][row] =
 // rel_states[q head of row][r]: one 16x16x16 bf16 MFMA per 16 keys, fp32 sums of exact products.
 template <int MODE>
@@ -1193,29 +1191,27 @@ __device__ __forceinline__ void line_bias_values(const Params& p, const Cursor& 
                                                  const uint32_t rst[2], uint8_t* rs, int lane, int n, int j,
                                                  f32x4 bias[2]) {
   if constexpr (MODE == KV_BF16_FUSED) {
-    {
-      const int dlo = rel_dlo(x), gbase = dlo >> 3, ng = p.rel_extent >> 3;
-      bias[0] = bias[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (x.nch <= 0 || dlo >= p.rel_extent || dlo + KV_CHUNK - 1 < 0) return;  // no key in the window
-      const int r = lane >> 2, g0 = gbase + (lane & 3), g1 = gbase + 4;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      wave_lds_fence();  // the previous unit's fragments have been read
-      *(u32x4*)(rs + r * kRelRowBytes + 16 * (lane & 3)) = g0 >= 0 && g0 < ng ? b.w[0] : z;
-      if ((lane & 3) == 0) *(u32x4*)(rs + r * kRelRowBytes + 64) = g1 >= 0 && g1 < ng ? b.w[1] : z;
-      wave_lds_fence();
-      short4_t sb;
-      sb[0] = (short)(rst[0] & 0xffffu);
-      sb[1] = (short)(rst[0] >> 16);
-      sb[2] = (short)(rst[1] & 0xffffu);
-      sb[3] = (short)(rst[1] >> 16);
+    const int dlo = rel_dlo(x), gbase = dlo >> 3, ng = p.rel_extent >> 3;
+    bias[0] = bias[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (x.nch <= 0 || dlo >= p.rel_extent || dlo + KV_CHUNK - 1 < 0) return;  // no key in the window
+    const int r = lane >> 2, g0 = gbase + (lane & 3), g1 = gbase + 4;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    wave_lds_fence();  // the previous unit's fragments have been read
+    *(u32x4*)(rs + r * kRelRowBytes + 16 * (lane & 3)) = g0 >= 0 && g0 < ng ? b.w[0] : z;
+    if ((lane & 3) == 0) *(u32x4*)(rs + r * kRelRowBytes + 64) = g1 >= 0 && g1 < ng ? b.w[1] : z;
+    wave_lds_fence();
+    short4_t sb;
+    sb[0] = (short)(rst[0] & 0xffffu);
+    sb[1] = (short)(rst[0] >> 16);
+    sb[2] = (short)(rst[1] & 0xffffu);
+    sb[3] = (short)(rst[1] >> 16);
 #pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        const int col = dlo + (KV_CHUNK - 1) - (16 * blk + n) - 8 * gbase;  // 0 .. 38
-        short4_t a;
+    for (int blk = 0; blk < 2; ++blk) {
+      const int col = dlo + (KV_CHUNK - 1) - (16 * blk + n) - 8 * gbase;  // 0 .. 38
+      short4_t af;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) a[t] = *(const short*)(rs + (4 * j + t) * kRelRowBytes + 2 * col);
-        bias[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, sb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      }
+      for (int t = 0; t < 4; ++t) af[t] = *(const short*)(rs + (4 * j + t) * kRelRowBytes + 2 * col);
+      bias[blk] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(af, sb, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
     }
   }
   if constexpr (MODE == KV_BF16_BIAS) {
