@@ -117,6 +117,42 @@ def test_rejected_metadata_never_reaches_the_kernel(cuda):
     assert np.array_equal(_bits(args[3]), before)
 
 
+@pytest.mark.parametrize("bad", [-64, 5])
+def test_one_launch_drops_a_sequence_with_bad_page_offset(cuda, bad):
+    """Metadata the preflight would reject, sent straight to the kernel (fused.invoke): a negative or
+    unaligned cu_kv_lens entry drops that sequence (page bit of the error word, its cache slot left
+    as it was) and leaves every other sequence's output and cache update as the oracle's."""
+    _say(f"fused one launch, cu_kv[1] = {bad}")
+    lens = [40, 100, 70, 300]
+    pool = int(sum(-(-x // 64) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(5, nseq=4, hq=32, hkv=8, d=128, page_size=64, pool_pages=pool, lengths=lens,
+                               rel_dim=16, extent=512)
+    expected = fo.inkling_fused_rpa_reference(inp)
+    bad_inp = dict(inp)
+    cu = inp["cu_kv_lens"].copy()
+    cu[1] = bad
+    bad_inp["cu_kv_lens"] = cu
+    args = _to_device(bad_inp)
+    before = _bits(args[3]).copy().reshape(inp["cache"].shape)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(torch.cuda.Stream()):  # a fresh workspace: its error word starts at 0
+        out, cache = fused.invoke(*args)
+        torch.cuda.current_stream().synchronize()
+        assert fused.read_error_word() == 1
+    torch.cuda.synchronize()
+    got_o = orc.bf16_to_f32(_bits(out))
+    exp_o = orc.bf16_to_f32(expected[0])
+    keep = [0, 2, 3]
+    assert np.allclose(got_o[keep], exp_o[keep], atol=0.02, rtol=0.02)
+    got_c = _bits(cache).reshape(inp["cache"].shape)
+    # sequence 1's slot: untouched; everything else: the oracle's updated cache
+    page = int(inp["page_indices"][int(inp["cu_kv_lens"][1]) // 64 + (lens[1] - 1) // 64])
+    slot = (lens[1] - 1) % 64
+    want = expected[1].copy()
+    want[page, slot] = before[page, slot]
+    assert np.array_equal(got_c, want)
+
+
 def test_repeat_is_idempotent(cuda):
     """Writing the same token twice leaves the same cache and output."""
     _say("fused repeat")
