@@ -1733,56 +1733,96 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
 
 // The prefill role of a workgroup: take tiles from the queue until it runs dry.  wsi: the four
 // metadata windows (nseq <= 256), total: the call's tile count.
+// Tile ti of the call's queue order (sequences in window order, each sequence's tiles last token
+// block first, kv heads innermost): its sequence, kv head, token block and chunk range.  seq < 0:
+// no tile (not reached for ti < total); c_hi <= c_lo: no key to visit.  Wave-collective.
+__device__ __forceinline__ PfTile pf_lookup(const Params& p, const SeqInfo wsi[4], int pf_min, int ti, int lane) {
+  PfTile tl;
+  tl.seq = -1;
+  tl.c_lo = tl.c_hi = 0;
+  int off = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int cnt = pf_tiles_of(p, wsi[w], pf_min) * p.Hkv;
+    int tot = cnt;
+    for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
+    tot = uni(tot);
+    if (tl.seq < 0 && ti < off + tot) {
+      int incl = cnt;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+      }
+      const int idx = __popcll(__ballot(off + incl <= ti));
+      const int li = ti - off - rl(incl - cnt, idx);  // tile index inside the sequence
+      tl.seq = 64 * w + idx;
+      tl.kv_len = rl(wsi[w].kv_len, idx);
+      tl.q_len = rl(wsi[w].q_len, idx);
+      tl.q_start = rl(wsi[w].q_start, idx);
+      const int nt = (tl.q_len + p.pf_tq - 1) / p.pf_tq;
+      tl.h = li % p.Hkv;
+      const int t = nt - 1 - li / p.Hkv;  // last tile of the sequence first
+      tl.tok0 = t * p.pf_tq;
+      tl.ntok = tl.q_len - tl.tok0 < p.pf_tq ? tl.q_len - tl.tok0 : p.pf_tq;
+    }
+    off += tot;
+  }
+  if (tl.seq < 0) return tl;
+  const int prior = tl.kv_len - tl.q_len;
+  const int pos_hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
+  if (pos_hi < 0) return tl;                          // q_len > kv_len: rows left unwritten
+  int lo = 0;
+  if (p.sliding_window > 0) {
+    lo = prior + tl.tok0 - p.sliding_window + 1;  // keys below are masked for every row
+    lo = lo < 0 ? 0 : lo;
+  }
+  tl.c_lo = lo / KV_CHUNK;
+  tl.c_hi = ((pos_hi < tl.kv_len - 1 ? pos_hi : tl.kv_len - 1) + KV_CHUNK) / KV_CHUNK;
+  return tl;
+}
+
+// The queue hands out tiles longest first (longest-processing-time order over the prefill
+// workgroups): every workgroup ranks the call's (sequence, token block) pairs by chunk count in
+// LDS (ties: queue order, so a sequence's last token block still comes first) and maps queue
+// position r to the pair of rank r / Hkv, kv head r % Hkv.  Calls with more pairs than
+// kPfOrderMax keep the queue order.
+constexpr int kPfOrderMax = 512;
+constexpr int kPfOrderBase = kPfQBase + 8 * kPfQWave;  // after the Q fragments
+static_assert(kPfOrderBase + 2 * kPfOrderMax * 4 <= 8 * kWaveLds, "prefill tile order exceeds the LDS allocation");
+
 template <int NP, bool UPG>
 __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], int pf_min, int total, uint8_t* lds,
                                         int* s_tile, int lane, int wv, int n, int j, int& err) {
+  const int npairs = total / p.Hkv;
+  const bool ranked = npairs <= kPfOrderMax;
+  int* psz = (int*)(lds + kPfOrderBase);  // chunk count of pair i
+  int* pord = psz + kPfOrderMax;          // pair of rank r
+  if (ranked) {
+    for (int i = wv; i < npairs; i += 8) {
+      const PfTile t = pf_lookup(p, wsi, pf_min, i * p.Hkv, lane);
+      if (lane == 0) psz[i] = t.c_hi > t.c_lo ? t.c_hi - t.c_lo : 0;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < npairs; i += blockDim.x) {
+      const int si = psz[i];
+      int r = 0;
+      for (int k = 0; k < npairs; ++k) {
+        const int sk = psz[k];
+        r += sk > si || (sk == si && k < i);
+      }
+      pord[r] = i;
+    }
+    __syncthreads();
+  }
   for (;;) {
     if (threadIdx.x == 0) *s_tile = atomicAdd(p.err + kQueueWord, 1);
     __syncthreads();
-    const int ti = uni(*s_tile);
+    const int tq = uni(*s_tile);
     __syncthreads();
-    if (ti >= total) break;
-    // the sequence holding tile ti: windows in order, then the lane inside
-    PfTile tl;
-    tl.seq = -1;
-    int off = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int cnt = pf_tiles_of(p, wsi[w], pf_min) * p.Hkv;
-      int tot = cnt;
-      for (int o = 32; o > 0; o >>= 1) tot += __shfl_xor(tot, o, 64);
-      tot = uni(tot);
-      if (tl.seq < 0 && ti < off + tot) {
-        int incl = cnt;
-        for (int o = 1; o < 64; o <<= 1) {
-          const int y = __shfl_up(incl, o, 64);
-          if (lane >= o) incl += y;
-        }
-        const int idx = __popcll(__ballot(off + incl <= ti));
-        const int li = ti - off - rl(incl - cnt, idx);  // tile index inside the sequence
-        tl.seq = 64 * w + idx;
-        tl.kv_len = rl(wsi[w].kv_len, idx);
-        tl.q_len = rl(wsi[w].q_len, idx);
-        tl.q_start = rl(wsi[w].q_start, idx);
-        const int nt = (tl.q_len + p.pf_tq - 1) / p.pf_tq;
-        tl.h = li % p.Hkv;
-        const int t = nt - 1 - li / p.Hkv;  // last tile of the sequence first
-        tl.tok0 = t * p.pf_tq;
-        tl.ntok = tl.q_len - tl.tok0 < p.pf_tq ? tl.q_len - tl.tok0 : p.pf_tq;
-      }
-      off += tot;
-    }
-    if (tl.seq < 0) continue;  // not reached: ti < total
-    const int prior = tl.kv_len - tl.q_len;
-    const int pos_hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
-    if (pos_hi < 0) continue;                           // q_len > kv_len: rows left unwritten
-    int lo = 0;
-    if (p.sliding_window > 0) {
-      lo = prior + tl.tok0 - p.sliding_window + 1;  // keys below are masked for every row
-      lo = lo < 0 ? 0 : lo;
-    }
-    tl.c_lo = lo / KV_CHUNK;
-    tl.c_hi = ((pos_hi < tl.kv_len - 1 ? pos_hi : tl.kv_len - 1) + KV_CHUNK) / KV_CHUNK;
+    if (tq >= total) break;
+    const int ti = ranked ? uni(pord[tq / p.Hkv]) * p.Hkv + tq % p.Hkv : tq;
+    const PfTile tl = pf_lookup(p, wsi, pf_min, ti, lane);
+    if (tl.seq < 0 || tl.c_hi <= tl.c_lo) continue;
     pf_tile<NP, UPG>(p, tl, lds, wv, n, j, err);
   }
 }
