@@ -92,6 +92,27 @@ def test_bias_windows_and_launch_forms(cuda, hq, hkv, page, lens, rel_dim, exten
     _run_and_check(inp)
 
 
+def test_random_one_launch_sweep(cuda):
+    """Seeded random shapes of the one-launch form (page 32/64/128, GQA 1-8, Hkv 1-16, R 0 or 16,
+    E a multiple of 8 from 8 to 600, lengths 1-3000 incl. page and chunk edges) against the oracle
+    at the reference's gate, cache bit-exact."""
+    rng = np.random.default_rng(2024)
+    for case in range(12):
+        hkv = int(rng.choice([1, 2, 4, 8, 16]))
+        g = int(rng.choice([1, 2, 4, 8]))
+        page = int(rng.choice([32, 64, 128]))
+        nseq = int(rng.integers(1, 24))
+        lens = [int(x) for x in rng.integers(1, 3000, size=nseq)]
+        lens[0] = int(rng.choice([1, 32, 33, page, page + 1]))
+        rel = int(rng.choice([0, 16]))
+        extent = 8 * int(rng.integers(1, 76))
+        _say(f"fused sweep {case}: hq={hkv * g} hkv={hkv} page={page} nseq={nseq} R={rel} E={extent}")
+        pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+        inp = fo.fused_inputs_like(100 + case, nseq=nseq, hq=hkv * g, hkv=hkv, d=128, page_size=page,
+                                   pool_pages=pool, lengths=lens, rel_dim=rel, extent=extent)
+        _run_and_check(inp)
+
+
 def test_more_than_256_sequences(cuda):
     """Metadata past the first four 64-sequence windows (loaded one window at a time)."""
     rng = np.random.default_rng(11)
