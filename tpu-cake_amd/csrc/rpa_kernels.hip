@@ -39,7 +39,8 @@
 //         B = P^T      [32 keys  x 16 rows]  lane%16 = row, slots straight from S's registers
 //         D = O^T      lane l holds dims 4j+r (+16 per block), row l%16
 //   with tau(j,e) = 16*(e/4) + 4j + e%4: the keys lane (row, j) already holds after QK^T, so
-//   P needs no cross-lane movement; V is transposed through LDS to match.
+//   P needs no cross-lane movement.  V is stored to LDS as key rows and its A fragments are read
+//   with gfx950's transposing LDS read (ds_read_b64_tr_b16), four keys of one dim per read.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -57,8 +58,10 @@ namespace rpa {
 namespace {
 
 constexpr int kD = 128;          // head_dim built
-constexpr int kVTRow = 80;       // bytes per LDS row (one dim) of the transposed V chunk: 64 + 16 pad
-constexpr int kVtBytes_ = 128 * kVTRow;  // one wave's transposed V chunk
+constexpr int kVTRow = 80;       // bytes per LDS row (one dim) of a prefill tile's transposed V chunk
+constexpr int kVtBytes_ = 128 * kVTRow;  // one wave's V region
+constexpr int kVRow = 2 * 128 + 16;      // decode: a unit's V chunk as 32 key rows of 272 bytes
+static_assert(32 * kVRow <= kVtBytes_, "V key rows exceed the wave's V region");
 constexpr int kMaxWavesPerCU = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.f;  // lazy softmax rescale threshold (log2 units)
@@ -70,6 +73,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // KV_BF16_BIAS: bf16 KV plus an additive relative-position bias table (the fused Inkling decode).
 // KV_BF16_FUSED: the fused Inkling decode step in one attention launch (Params::fused).
@@ -604,7 +608,7 @@ struct HalfRegs<KV_FP8> {
                   // applied); UPG: the K registers hold the unit's page's (K, V) scales, V's none
 };
 
-// The 8 dims lane group j holds in MFMA k-step s (QK^T; the same for K, Q and V^T rows).  bf16:
+// The 8 dims lane group j holds in MFMA k-step s (QK^T; the same for K, Q and V rows).  bf16:
 // 8j + 32s.  fp8: one 16-byte load covers two k-steps, so lane group j reads bytes 16j .. 16j+15 of
 // each 64-byte half of a row -- 64 bytes per row per load instruction, half the requests per byte
 // of 8-byte loads.
@@ -895,15 +899,31 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
   return pb;
 }
 
+// The eight A fragments of O^T += V^T P^T from a wave's V chunk stored as key rows (kVRow
+// stride): fragment d covers dims 16d .. 16d+15 in the PV key order (k = 8j + 4h + e <-> key
+// 16h + 4j + e, the order the QK^T output holds).  ds_read_b64_tr_b16 transposes within each
+// 16-lane group: lane n of group j reads dims 16d + 4(n%4) .. +3 of key 16h + 4j + n/4, and lane n
+// receives dim 16d + n of keys 16h + 4j .. +3.
+__device__ __forceinline__ void read_vt_fragments(const uint8_t* vt, int n, int j, bf16x8 va[8]) {
+  typedef __attribute__((address_space(3))) short4_t* lds_s4;
+  const uint8_t* vb = vt + (4 * j + (n >> 2)) * kVRow + 8 * (n & 3);
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(vb + 32 * d));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(vb + 16 * kVRow + 32 * d));
+    va[d] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+}
+
 template <int MODE>
 __device__ __forceinline__ const f32x4* bias_of(const HalfRegs<MODE>& r) {
   if constexpr (MODE == KV_BF16_BIAS) return r.bias;
   return nullptr;
 }
 
-// One unit.  S = K Q^T; V^T goes to LDS; then, if the next unit starts a new row block, its
-// queries are loaded into q (their registers are free once QK^T has issued), after which the next unit's V is loaded into the
-// registers just released; then softmax and O^T += V^T P^T.
+// One unit.  S = K Q^T; V goes to LDS as key rows; then, if the next unit starts a new row block,
+// its queries are loaded into q (their registers are free once QK^T has issued), after which the
+// next unit's V is loaded into the registers just released; then softmax and O^T += V^T P^T.
 template <int MODE, bool UPG>
 __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const HalfRegs<MODE>& kr,
                                              const HalfRegs<MODE>& vr, bf16x8 q[4], const Cursor& nx,
@@ -924,23 +944,14 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
   float vs = 1.f;
   if constexpr (MODE == KV_FP8 && UPG) vs = p.v_scale * kr.sc[1];  // the unit's V scale (one page)
 
-  // V^T into LDS: key t = 16*blk + n goes to slot pos = 8*(n/4) + 4*blk + n%4 of each dim row
+  // V into LDS as key rows (key 16*blk + n, kVRow stride), one 16-byte store per 8 dims; the PV
+  // A fragments are read back transposed (ds_read_b64_tr_b16)
   wave_lds_fence();
 #pragma unroll
-  for (int blk = 0; blk < 2; ++blk) {
-    const int slot_b = 2 * (8 * (n >> 2) + 4 * blk + (n & 3));
+  for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4 vw = to_bf16x8<MODE, UPG>(vr, p, blk, s, 1, vs);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        uint32_t w = vw[t];
-        int d = kdim<MODE>(j, s) + 2 * t;
-        *(uint16_t*)(vt + d * kVTRow + slot_b) = (uint16_t)(w & 0xffffu);
-        *(uint16_t*)(vt + (d + 1) * kVTRow + slot_b) = (uint16_t)(w >> 16);
-      }
-    }
-  }
+    for (int s = 0; s < 4; ++s)
+      *(u32x4*)(vt + (16 * blk + n) * kVRow + 2 * kdim<MODE>(j, s)) = to_bf16x8<MODE, UPG>(vr, p, blk, s, 1, vs);
   if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);  // a new row block's queries (as in compute_unit_line)
   load_half<MODE, UPG>(p, nx_addr, 1, v_next);
 
@@ -948,12 +959,10 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
 
   wave_lds_fence();
   bf16x8 va[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) va[d] = *(const bf16x8*)(vt + (16 * d + n) * kVTRow + 16 * j);
+  read_vt_fragments(vt, n, j, va);
 #pragma unroll
   for (int d = 0; d < 8; ++d) st.acc[d] = mfma(va[d], pb, st.acc[d]);
-  // the eight V^T fragment reads go out together, then the MFMAs (not read, wait, MFMA x 8)
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
   __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 }
 
@@ -1071,13 +1080,12 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
 // instruction, half of every 128-byte line.  Here a wave loads its kv head's K (then V) rows of a
 // unit as whole lines -- load i covers keys 4i .. 4i+3, lane L holding key 4i + L/16, dims
 // 8*(L%16) .. +7 -- with non-temporal loads, since every line is read once.  K goes to a
-// wave-private LDS tile (key rows, 272-byte stride: conflict-free A fragments), written at the end
-// of the step that loaded it and read by the next step's QK^T; V^T is written as before (key order
-// tau) with its 16-byte key groups XOR-swizzled by row bits 3-4, so the 16 dim rows one
-// transposing store touches fall in different banks.  Measured on C2's pool (a loads + LDS probe
-// of both patterns): 104 vs 111 us per 638 MB.  One K and one V register set suffice: K of the
-// next unit lands while this unit's K is read from the tile, V of the next unit is loaded once this
-// unit's V^T is stored.
+// wave-private LDS tile (key rows, 272-byte stride), written at the end of the step that loaded
+// it and read by the next step's QK^T; V goes to the wave's V region the same way (one 16-byte
+// store per load) and is read back transposed (read_vt_fragments).  Measured on C2's pool (a loads
+// + LDS probe of both patterns): 104 vs 111 us per 638 MB.  One K and one V register set suffice:
+// K of the next unit lands while this unit's K is read from the tile, V of the next unit is loaded
+// once this unit's V is stored.
 constexpr int kKtRow = kD * 2 + 16;
 constexpr int kKtBytes = KV_CHUNK * kKtRow;
 constexpr int kWaveLds = kVtBytes_ + kKtBytes;
@@ -1099,8 +1107,6 @@ struct LineAddr {
   int knew;       // fused step: the unit's key (0..31) read from new_k / new_v instead, -1 = none
   size_t newoff;  // fused step: element index of this lane's dims of that key's row in new_k / new_v
 };
-
-__device__ __forceinline__ int vt_swz(int row, int g) { return g ^ ((row >> 3) & 3); }
 
 template <int MODE>
 __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, const Pages& pages, int lane, int n,
@@ -1180,7 +1186,6 @@ __device__ __forceinline__ void load_line_bias(const Params& p, const Cursor& x,
   }
 }
 
-typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // The bias of the lane's 8 scores (keys 16*blk + 4j + rr of row n) from the unit's LineBias.
 // KV_BF16_FUSED: the five groups are staged in the wave's rows, then bias[blk] = P_blk @ S with
@@ -1235,8 +1240,8 @@ __device__ __forceinline__ void store_k_tile(const Params& p, const LineRegs& k,
     *(u32x4*)(kt + (4 * i + (lane >> 4)) * kKtRow + (lane & 15) * 16) = line_word<MODE>(k, i, p, 0);
 }
 
-// compute_unit with K read from the K tile, V^T stored from the line layout (swizzled) and the
-// next unit's V loaded into v (after its V^T store).
+// compute_unit with K read from the K tile, V stored as key rows from the line layout and the
+// next unit's V loaded into v (after that store).
 template <int MODE>
 __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor& x, LineRegs& v, const f32x4* bias,
                                                   bf16x8 q[4], uint32_t rst[2], const Cursor& nx,
@@ -1252,21 +1257,11 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
     s1 = mfma(a1, q[s], s1);
   }
 
-  // V^T: key t = 4i + lane/16 goes to position tau^-1(t) = 8*((t%16)/4) + 4*(t/16) + t%4 of each
-  // dim row, i.e. 16-byte group i%4 (swizzled), element 4*(i/4) + lane/16
+  // V as key rows (key 4i + lane/16, kVRow stride), as the K tile; read back transposed below
   wave_lds_fence();
-  const int e = lane >> 4, d0 = 8 * (lane & 15);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const u32x4 vw = line_word<MODE>(v, i, p, 1);
-    const int g = i & 3, off = 2 * (4 * (i >> 2) + e);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int d = d0 + 2 * t;
-      *(uint16_t*)(vt + d * kVTRow + 16 * vt_swz(d, g) + off) = (uint16_t)(vw[t] & 0xffffu);
-      *(uint16_t*)(vt + (d + 1) * kVTRow + 16 * vt_swz(d + 1, g) + off) = (uint16_t)(vw[t] >> 16);
-    }
-  }
+  for (int i = 0; i < 8; ++i)
+    *(u32x4*)(vt + (4 * i + (lane >> 4)) * kVRow + (lane & 15) * 16) = line_word<MODE>(v, i, p, 1);
   // a new row block's queries (else q already holds its rows), issued after the wait for this
   // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
   // issued before it they would make that wait also retire the next unit's K
@@ -1277,14 +1272,10 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
 
   wave_lds_fence();
   bf16x8 va[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    const int row = 16 * d + n;
-    va[d] = *(const bf16x8*)(vt + row * kVTRow + 16 * vt_swz(row, j));
-  }
+  read_vt_fragments(vt, n, j, va);
 #pragma unroll
   for (int d = 0; d < 8; ++d) st.acc[d] = mfma(va[d], pb, st.acc[d]);
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
   __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 }
 
@@ -1829,10 +1820,10 @@ __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], i
 
 template <int MODE, bool UPG>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x (transposed V chunk, K tile)
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x (V region, K tile)
   const int lane = threadIdx.x & 63;
   const int wv = uni(threadIdx.x >> 6);
-  uint8_t* vt = smem + wv * kWaveLds;  // this wave's V^T chunk, then its K tile (full-line path)
+  uint8_t* vt = smem + wv * kWaveLds;  // this wave's V region, then its K tile (full-line path)
   uint8_t* kt = vt + kVtBytes_;
   const int n = lane & 15, j = lane >> 4;
   const int b = blockIdx.x;
@@ -2915,7 +2906,7 @@ int heads_per_group(int hkv) {
   return 1;
 }
 
-constexpr int kVtBytes = kWaveLds;  // LDS per wave: V^T chunk + K tile
+constexpr int kVtBytes = kWaveLds;  // LDS per wave: V region + K tile
 
 // Workgroups for the persistent grid: the kernel's occupancy (2 waves per SIMD) in workgroups
 // of hg waves, capped so no CU holds more than kMaxWavesPerCU waves.
