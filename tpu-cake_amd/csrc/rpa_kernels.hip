@@ -58,8 +58,7 @@ namespace rpa {
 namespace {
 
 constexpr int kD = 128;          // head_dim built
-constexpr int kVTRow = 80;       // bytes per LDS row (one dim) of a prefill tile's transposed V chunk
-constexpr int kVtBytes_ = 128 * kVTRow;  // one wave's V region
+constexpr int kVtBytes_ = 10240;  // one wave's V region (the prefill tiles' buffers are laid over these)
 constexpr int kVRow = 2 * 128 + 16;      // decode: a unit's V chunk as 32 key rows of 272 bytes
 static_assert(32 * kVRow <= kVtBytes_, "V key rows exceed the wave's V region");
 constexpr int kMaxWavesPerCU = 8;
@@ -1324,14 +1323,14 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
 // h*G + g) over the 32*HG rows of a workgroup, wave w owning rows 32w .. 32w+31 as two 16-row
 // MFMA blocks.  Each 32-key chunk of kv head h is fetched from HBM once per tile by the whole
 // workgroup (a four-deep register ring, three chunks ahead) into double-buffered LDS: K as key
-// rows with a 272-byte stride (the 16 keys of an A fragment land in distinct banks), V
-// transposed as in compute_unit.  Every wave reads its A fragments from LDS and uses each for
+// rows with a 272-byte stride, V the same way (read back transposed, read_vt_fragments).  Every
+// wave reads its A fragments from LDS and uses each for
 // both of its row blocks; softmax as in compute_unit.  Tiles come from a queue (an atomic
 // counter in the workspace header, reset by the combine kernel), the last tile of each
 // sequence first.
 constexpr int kPfKRow = kD * 2 + 16;
 constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
-constexpr int kPfBufBytes = kPfKBytes + kD * kVTRow;
+constexpr int kPfBufBytes = kPfKBytes + KV_CHUNK * kVRow;
 constexpr int kPfQWave = 2 * 4 * 64 * 16;  // one wave's Q^T fragments: 2 row blocks x 4 k-steps x 64 lanes x 16 B
 constexpr int kPfQBase = 2 * kPfBufBytes;    // the tile's Q fragments follow the two chunk buffers
 // prefill tiles run in workgroups of eight waves, whose dynamic LDS is eight decode-wave regions
@@ -1364,11 +1363,9 @@ __device__ __forceinline__ int pf_tiles_of(const Params& p, const SeqInfo& si, i
   return (si.q_len + p.pf_tq - 1) / p.pf_tq;
 }
 
-// Which K/V piece of a chunk thread tid (of 512) carries: wave w, lane l; key group g = w/2
-// (keys tau(g, e) = 16*(e/4) + 4g + e%4, e = l/8: the eight keys one MFMA fragment lane of V^T
-// needs), dims 64*(w%2) + 8*(l%8) .. +8.  Eight lanes l%8 = const hold the same dims of the
-// group's eight keys, so an 8x8 transpose across them (three lane-exchange stages) turns their V
-// pieces into eight keys of one dim each: one 16-byte LDS write per lane.
+// Which K/V piece of a chunk thread tid (of 512) carries: wave w, lane l: key 16*(e/4) + 4*(w/2)
+// + e%4 with e = l/8, dims 64*(w%2) + 8*(l%8) .. +8 -- one 16-byte load and one 16-byte LDS store
+// each of K and V per thread and chunk.
 struct PfPiece {
   int key, d0;
 };
@@ -1430,44 +1427,11 @@ __device__ __forceinline__ void pf_load_chunk(const Params& p, const PfTile& tl,
   r.v[0] = *(const u32x4*)(kv + e + kD);
 }
 
-// Column group (16 bytes = 8 key slots) of V^T row `row` holding slot group g: XOR-swizzled by
-// row bits 4-5, so the 8 rows 8 apart that one transposed write touches, and the 8 consecutive rows
-// one fragment read touches, fall in distinct banks.
-__device__ __forceinline__ int pf_vt_group(int row, int g) { return g ^ ((row >> 4) & 3); }
-
 template <int NP>
 __device__ __forceinline__ void pf_store_chunk(uint8_t* buf, const PfRegs<NP>& r, int tid, int nthreads) {
   const PfPiece pc = pf_piece(tid);
-  const int l = tid & 63, g = (tid >> 6) >> 1;
   *(u32x4*)(buf + pc.key * kPfKRow + pc.d0 * 2) = r.k[0];
-  // 8x8 transpose of bf16 across lanes l%8 = const (row e = l/8 holds key e's 8 dims): exchange
-  // element bit i with lane-group bit i for i = 0 (lanes ^8), 1 (^16), 2 (^32)
-  uint32_t d[4] = {r.v[0][0], r.v[0][1], r.v[0][2], r.v[0][3]};
-  const uint32_t sel = (l & 8) ? 0x03020706u : 0x05040100u;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t pv = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[m], 0x128, 0xf, 0xf, false);  // lane ^ 8
-    d[m] = __builtin_amdgcn_perm(pv, d[m], sel);
-  }
-  {
-    const auto x = __builtin_amdgcn_permlane16_swap(d[0], d[1], false, false);
-    const auto y = __builtin_amdgcn_permlane16_swap(d[2], d[3], false, false);
-    d[0] = x[0];
-    d[1] = x[1];
-    d[2] = y[0];
-    d[3] = y[1];
-  }
-  {
-    const auto x = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
-    const auto y = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
-    d[0] = x[0];
-    d[2] = x[1];
-    d[1] = y[0];
-    d[3] = y[1];
-  }
-  // this lane now holds keys tau(g, 0..7) of dim d0 + l/8: slots 8g .. 8g+7 of that V^T row
-  const int row = pc.d0 + (l >> 3);
-  *(u32x4*)(buf + kPfKBytes + row * kVTRow + 16 * pf_vt_group(row, g)) = u32x4{d[0], d[1], d[2], d[3]};
+  *(u32x4*)(buf + kPfKBytes + pc.key * kVRow + pc.d0 * 2) = r.v[0];  // V as key rows (read_vt_fragments)
 }
 
 struct PfRow {
@@ -1600,18 +1564,14 @@ __device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, in
     pb1 = pf_softmax(p, tl, c, sc[1], st[1], j);
   }
   bf16x8 va[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    const int row = 16 * d + n;
-    va[d] = *(const bf16x8*)(vt + row * kVTRow + 16 * pf_vt_group(row, j));
-  }
+  read_vt_fragments(vt, n, j, va);
 #pragma unroll
   for (int d = 0; d < 8; ++d) {
     st[0].acc[d] = mfma(va[d], pb0, st[0].acc[d]);
     st[1].acc[d] = mfma(va[d], pb1, st[1].acc[d]);
   }
-  // the eight fragment reads go out together, then the sixteen MFMAs (not read, wait, MFMA x 8)
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  // the sixteen fragment reads go out together, then the sixteen MFMAs (not read, wait, MFMA x 8)
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
   __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
 }
 
