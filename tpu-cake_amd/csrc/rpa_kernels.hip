@@ -58,9 +58,8 @@ namespace rpa {
 namespace {
 
 constexpr int kD = 128;          // head_dim built
-constexpr int kVtBytes_ = 10240;  // one wave's V region (the prefill tiles' buffers are laid over these)
-constexpr int kVRow = 2 * 128 + 16;      // decode: a unit's V chunk as 32 key rows of 272 bytes
-static_assert(32 * kVRow <= kVtBytes_, "V key rows exceed the wave's V region");
+constexpr int kVRow = kD * 2 + 16;            // a 32-key V chunk as key rows of 272 bytes
+constexpr int kVtBytes_ = KV_CHUNK * kVRow;  // one wave's V region (prefill tiles lay their buffers over these)
 constexpr int kMaxWavesPerCU = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.f;  // lazy softmax rescale threshold (log2 units)
