@@ -1321,13 +1321,14 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
 // A tile is (sequence, kv head h, pf_tq consecutive query tokens): rows r = token*G + g (q head
 // h*G + g) over the 32*HG rows of a workgroup, wave w owning rows 32w .. 32w+31 as two 16-row
 // MFMA blocks.  Each 32-key chunk of kv head h is fetched from HBM once per tile by the whole
-// workgroup (a four-deep register ring, three chunks ahead) into double-buffered LDS: K as key
-// rows with a 272-byte stride, V the same way (read back transposed, read_vt_fragments).  Every
-// wave reads its A fragments from LDS and uses each for
-// both of its row blocks; softmax as in compute_unit.  Tiles come from a queue (an atomic
+// workgroup (a four-deep register ring, three chunks ahead) into double-buffered LDS: K as
+// 256-byte key rows whose 16-byte column groups are XOR-swizzled by key % 16 (the A fragment reads
+// measured conflict-free; a 272-byte stride reads at half that rate), V as 272-byte key rows read
+// back transposed (read_vt_fragments).  Every wave reads its A fragments from LDS and uses each
+// for both of its row blocks; softmax as in compute_unit.  Tiles come from a queue (an atomic
 // counter in the workspace header, reset by the combine kernel), the last tile of each
 // sequence first.
-constexpr int kPfKRow = kD * 2 + 16;
+constexpr int kPfKRow = kD * 2;  // K key rows, column groups swizzled (pf_store_chunk, pf_compute)
 constexpr int kPfKBytes = KV_CHUNK * kPfKRow;
 constexpr int kPfBufBytes = kPfKBytes + KV_CHUNK * kVRow;
 constexpr int kPfQWave = 2 * 4 * 64 * 16;  // one wave's Q^T fragments: 2 row blocks x 4 k-steps x 64 lanes x 16 B
@@ -1429,7 +1430,7 @@ __device__ __forceinline__ void pf_load_chunk(const Params& p, const PfTile& tl,
 template <int NP>
 __device__ __forceinline__ void pf_store_chunk(uint8_t* buf, const PfRegs<NP>& r, int tid, int nthreads) {
   const PfPiece pc = pf_piece(tid);
-  *(u32x4*)(buf + pc.key * kPfKRow + pc.d0 * 2) = r.k[0];
+  *(u32x4*)(buf + pc.key * kPfKRow + 16 * ((pc.d0 >> 3) ^ (pc.key & 15))) = r.k[0];
   *(u32x4*)(buf + kPfKBytes + pc.key * kVRow + pc.d0 * 2) = r.v[0];  // V as key rows (read_vt_fragments)
 }
 
@@ -1548,7 +1549,7 @@ __device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, in
     const bf16x8 q1 = *(const bf16x8*)(qs + ((1 * 4 + s) * 64 + lane) * 16);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      const bf16x8 a = *(const bf16x8*)(buf + (16 * kb + n) * kPfKRow + (32 * s + 8 * j) * 2);
+      const bf16x8 a = *(const bf16x8*)(buf + (16 * kb + n) * kPfKRow + 16 * ((4 * s + j) ^ n));
       sc[0][kb] = mfma(a, q0, sc[0][kb]);
       sc[1][kb] = mfma(a, q1, sc[1][kb]);
     }
