@@ -2006,55 +2006,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //
 // Workgroup = 4 waves, one per SIMD, wave w owning rows 64w .. 64w+63 as four 16-row MFMA blocks
 // (the whole register file of a SIMD: 64 rows of fp32 accumulators, the queries and a chunk's
-// scores stay in registers).  Per chunk the workgroup stages K (key rows, 272-byte stride) and V^T
-// (dim rows of 64 keys in the tau order of the QK output, 144-byte stride, 16-byte groups XOR-
-// swizzled by row bits 4-5: conflict-free transposing writes and fragment reads) in one of two LDS
-// buffers; the 8x8 transposes of V happen in registers across lanes.  Every K and V^T fragment
+// scores stay in registers).  Per chunk the workgroup stages K and V (key rows, 272-byte stride;
+// V read back transposed, read_vt_fragments) in one of two LDS buffers.  Every K and V^T fragment
 // feeds the wave's four row blocks: 64 + 64 MFMAs per chunk per wave.  Loads run two chunk steps
 // ahead (page ids three), stores of the next chunk follow the compute, one barrier per step.
 constexpr int kPkRows = 256;
 constexpr int kPkChunk = 64;
 constexpr int kPkKRow = kD * 2 + 16;            // 272 B per K row
 constexpr int kPkKTile = kPkChunk * kPkKRow;    // 17408 B
-constexpr int kPkVtRow = kPkChunk * 2 + 16;     // 144 B per V^T dim row (64 keys + pad)
-constexpr int kPkVtTile = kD * kPkVtRow;        // 18432 B
+constexpr int kPkVtTile = kPkChunk * kVRow;     // 17408 B: V as key rows (read_vt_fragments per 32 keys)
 constexpr int kPkStage = kPkKTile + kPkVtTile;  // 35840 B
 constexpr int kPkLds = 2 * kPkStage;
-
-// Position of 16-byte key group q (= 4 * half + g) in V^T row `row`.
-__device__ __forceinline__ int pk_vt_pos(int row, int q) {
-  return q ^ (((row >> 4) & 1) << 1) ^ (((row >> 5) & 1) << 2);
-}
-
-// 8x8 bf16 transpose across the lanes l % 8 == const: before, lane l holds 8 dims of key row
-// l / 8; after, 8 keys (rows 0..7) of dim l / 8 -- exchanging element bit i with lane-group bit i
-// for i = 0 (lanes ^8), 1 (^16), 2 (^32).
-__device__ __forceinline__ u32x4 transpose8x8_bf16(u32x4 v, int l) {
-  uint32_t d[4] = {v[0], v[1], v[2], v[3]};
-  const uint32_t sel = (l & 8) ? 0x03020706u : 0x05040100u;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t pv = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[m], 0x128, 0xf, 0xf, false);  // lane ^ 8
-    d[m] = __builtin_amdgcn_perm(pv, d[m], sel);
-  }
-  {
-    const auto x = __builtin_amdgcn_permlane16_swap(d[0], d[1], false, false);
-    const auto y = __builtin_amdgcn_permlane16_swap(d[2], d[3], false, false);
-    d[0] = x[0];
-    d[1] = x[1];
-    d[2] = y[0];
-    d[3] = y[1];
-  }
-  {
-    const auto x = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
-    const auto y = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
-    d[0] = x[0];
-    d[2] = x[1];
-    d[1] = y[0];
-    d[3] = y[1];
-  }
-  return u32x4{d[0], d[1], d[2], d[3]};
-}
 
 struct PkTile {
   int seq, h, t, nt;       // sequence, kv head, token block, token blocks of the sequence
@@ -2162,10 +2124,10 @@ struct PkRegs {
   u32x4 k[4], v[4];
 };
 
-// Issue the loads of chunk step x (page id pg, read a step earlier).  K piece i: key
-// (tid / 16) + 16 i, dims 8 (tid % 16) ..; V piece i: key 32 (i & 1) + tau(w, lane / 8), dims
-// 8 ((lane % 8) + 8 (i >> 1)) ..  Keys past kv_len read key kv_len - 1 (masked by their scores).
-// The chunk's base address is wave-uniform; each piece is a 32-bit byte offset from it.
+// Issue the loads of chunk step x (page id pg, read a step earlier).  K and V piece i: key
+// (tid / 16) + 16 i, dims 8 (tid % 16) .. (whole 128-byte lines, non-temporal).  Keys past kv_len
+// read key kv_len - 1 (masked by their scores).  The chunk's base address is wave-uniform; each
+// piece is a 32-bit byte offset from it.
 __device__ __forceinline__ void pk_load(const Params& p, const PkCur& x, int pg, int tid, PkRegs& r, int& err) {
   pg = uni(pg);
   if (pg < 0 || pg >= p.P) {  // out-of-range page id: never dereferenced
@@ -2176,8 +2138,7 @@ __device__ __forceinline__ void pk_load(const Params& p, const PkCur& x, int pg,
   const int kmax = x.live ? x.tl.kv_len - 1 - key0 : 0;
   const uint8_t* base = p.kv + 2 * kv_elem(p, pg, key0, 2 * (x.live ? x.tl.h : 0));
   const uint32_t row = (uint32_t)(2 * p.Hkv) * kD * 2;  // bytes between consecutive keys of a page
-  const int w = tid >> 6, l = tid & 63, e = l >> 3;
-  const uint32_t kcol = 16u * (tid & 15), vcol = 2u * kD + 16u * (l & 7);
+  const uint32_t kcol = 16u * (tid & 15);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     int kk = (tid >> 4) + 16 * i;
@@ -2186,9 +2147,9 @@ __device__ __forceinline__ void pk_load(const Params& p, const PkCur& x, int pg,
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    int kk = 32 * (i & 1) + 16 * (e >> 2) + 4 * w + (e & 3);
+    int kk = (tid >> 4) + 16 * i;
     kk = kk < kmax ? kk : kmax;
-    r.v[i] = *(const u32x4*)(base + ((uint32_t)kk * row + vcol + 128u * (i >> 1)));
+    r.v[i] = ld_stream((const u32x4*)(base + ((uint32_t)kk * row + 2u * kD + kcol)));
   }
 }
 
@@ -2198,17 +2159,12 @@ __device__ __forceinline__ int pk_page_id(const Params& p, const PkCur& x) {
 }
 
 __device__ __forceinline__ void pk_store(uint8_t* stage, const PkRegs& r, int tid) {
-  const int w = tid >> 6, l = tid & 63;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     *(u32x4*)(stage + ((tid >> 4) + 16 * i) * kPkKRow + 16 * (tid & 15)) = r.k[i];
   uint8_t* vt = stage + kPkKTile;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u32x4 t = transpose8x8_bf16(r.v[i], l);  // keys tau(w, 0..7) of dim d
-    const int d = 8 * ((l & 7) + 8 * (i >> 1)) + (l >> 3);
-    *(u32x4*)(vt + d * kPkVtRow + 16 * pk_vt_pos(d, 4 * (i & 1) + w)) = t;
-  }
+  for (int i = 0; i < 4; ++i) *(u32x4*)(vt + ((tid >> 4) + 16 * i) * kVRow + 16 * (tid & 15)) = r.v[i];
 }
 
 struct PkRow {
@@ -2346,11 +2302,7 @@ __device__ __forceinline__ void pk_compute(const Params& p, const PkTile& tl, in
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) pb[rb] = pk_softmax(p, tl, k0, plain, sc[rb], st[rb], j);
     bf16x8 va[8];  // the half's V^T fragments
-#pragma unroll
-    for (int db = 0; db < 8; ++db) {
-      const int row = 16 * db + n;
-      va[db] = *(const bf16x8*)(vt + row * kPkVtRow + 16 * pk_vt_pos(row, 4 * hf + j));
-    }
+    read_vt_fragments(vt + 32 * hf * kVRow, n, j, va);
 #pragma unroll
     for (int db = 0; db < 8; ++db)
 #pragma unroll
