@@ -126,12 +126,11 @@ def test_plan_lds_matches_kernel_constants():
     # the per-wave LDS the host requests, restated from the kernel's own constants
     const = {k: int(v) for k, v in re.findall(r"constexpr int (kD|KV_CHUNK) = (\d+);",
                                                KERNEL_SRC + (ROOT / "tpu-cake_amd" / "csrc" / "rpa_schedule.h").read_text())}
-    row = const["kD"] * 2 + 16
     assert re.search(r"constexpr int kKtRow = kD \* 2 \+ 16;", KERNEL_SRC)
-    assert re.search(r"constexpr int kVRow = kD \* 2 \+ 16;", KERNEL_SRC)
+    assert re.search(r"constexpr int kVRow = kD \* 2 \+ 32;", KERNEL_SRC)
     assert re.search(r"constexpr int kVtBytes_ = KV_CHUNK \* kVRow;", KERNEL_SRC)
     assert re.search(r"constexpr int kKtBytes = KV_CHUNK \* kKtRow;", KERNEL_SRC)
-    per_wave = 2 * const["KV_CHUNK"] * row
+    per_wave = const["KV_CHUNK"] * (const["kD"] * 2 + 32) + const["KV_CHUNK"] * (const["kD"] * 2 + 16)
     assert contracts.WAVE_LDS_BYTES == per_wave
     assert f"LDS {8 * per_wave} B" in contracts.render_workload("mi355x-rpa-c2")
     assert "whole 128-byte K/V lines" in contracts.render_workload("mi355x-rpa-c2")

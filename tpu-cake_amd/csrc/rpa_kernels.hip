@@ -58,7 +58,7 @@ namespace rpa {
 namespace {
 
 constexpr int kD = 128;          // head_dim built
-constexpr int kVRow = kD * 2 + 16;            // a 32-key V chunk as key rows of 272 bytes
+constexpr int kVRow = kD * 2 + 32;            // a 32-key V chunk as key rows of 288 bytes (conflict-free transposing reads)
 constexpr int kVtBytes_ = KV_CHUNK * kVRow;  // one wave's V region (prefill tiles lay their buffers over these)
 constexpr int kMaxWavesPerCU = 8;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -1079,7 +1079,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
 // unit as whole lines -- load i covers keys 4i .. 4i+3, lane L holding key 4i + L/16, dims
 // 8*(L%16) .. +7 -- with non-temporal loads, since every line is read once.  K goes to a
 // wave-private LDS tile (key rows, 272-byte stride), written at the end of the step that loaded
-// it and read by the next step's QK^T; V goes to the wave's V region the same way (one 16-byte
+// it and read by the next step's QK^T; V goes to the wave's V region (288-byte key rows, one 16-byte
 // store per load) and is read back transposed (read_vt_fragments).  Measured on C2's pool (a loads
 // + LDS probe of both patterns): 104 vs 111 us per 638 MB.  One K and one V register set suffice:
 // K of the next unit lands while this unit's K is read from the tile, V of the next unit is loaded
@@ -1323,7 +1323,7 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
 // MFMA blocks.  Each 32-key chunk of kv head h is fetched from HBM once per tile by the whole
 // workgroup (a four-deep register ring, three chunks ahead) into double-buffered LDS: K as
 // 256-byte key rows whose 16-byte column groups are XOR-swizzled by key % 16 (the A fragment reads
-// measured conflict-free; a 272-byte stride reads at half that rate), V as 272-byte key rows read
+// measured conflict-free; a 272-byte stride reads at half that rate), V as 288-byte key rows read
 // back transposed (read_vt_fragments).  Every wave reads its A fragments from LDS and uses each
 // for both of its row blocks; softmax as in compute_unit.  Tiles come from a queue (an atomic
 // counter in the workspace header, reset by the combine kernel), the last tile of each
@@ -2006,15 +2006,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 //
 // Workgroup = 4 waves, one per SIMD, wave w owning rows 64w .. 64w+63 as four 16-row MFMA blocks
 // (the whole register file of a SIMD: 64 rows of fp32 accumulators, the queries and a chunk's
-// scores stay in registers).  Per chunk the workgroup stages K and V (key rows, 272-byte stride;
-// V read back transposed, read_vt_fragments) in one of two LDS buffers.  Every K and V^T fragment
+// scores stay in registers).  Per chunk the workgroup stages K and V (key rows, 272 and 288-byte
+// strides; V read back transposed, read_vt_fragments) in one of two LDS buffers.  Every K and V^T fragment
 // feeds the wave's four row blocks: 64 + 64 MFMAs per chunk per wave.  Loads run two chunk steps
 // ahead (page ids three), stores of the next chunk follow the compute, one barrier per step.
 constexpr int kPkRows = 256;
 constexpr int kPkChunk = 64;
 constexpr int kPkKRow = kD * 2 + 16;            // 272 B per K row
 constexpr int kPkKTile = kPkChunk * kPkKRow;    // 17408 B
-constexpr int kPkVtTile = kPkChunk * kVRow;     // 17408 B: V as key rows (read_vt_fragments per 32 keys)
+constexpr int kPkVtTile = kPkChunk * kVRow;     // 18432 B: V as key rows (read_vt_fragments per 32 keys)
 constexpr int kPkStage = kPkKTile + kPkVtTile;  // 35840 B
 constexpr int kPkLds = 2 * kPkStage;
 

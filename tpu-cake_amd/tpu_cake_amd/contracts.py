@@ -211,9 +211,9 @@ MI355X_BF16_FLOPS = _RATES.compute_flops_per_second
 WAVES_PER_CU = 8                            # the attention kernel: 2 waves per SIMD
 KV_CHUNK = 32                               # keys per stream-K unit (csrc/rpa_schedule.h)
 ROW_BLOCK = 16
-# LDS per wave of the attention kernel: the unit's V chunk and the K tile of the full-line path, each
-# 32 key rows x 272 B (csrc/rpa_kernels.hip, kVRow / kKtRow)
-WAVE_LDS_BYTES = 2 * KV_CHUNK * (128 * 2 + 16)
+# LDS per wave of the attention kernel: the unit's V chunk (32 key rows x 288 B) and the K tile of the
+# full-line path (32 key rows x 272 B) (csrc/rpa_kernels.hip, kVRow / kKtRow)
+WAVE_LDS_BYTES = KV_CHUNK * (128 * 2 + 32) + KV_CHUNK * (128 * 2 + 16)
 # split row blocks with this many contributors are merged by HEAVY_SLICES dim-slice workgroups per
 # kv head, one helper slot per (HEAVY_CONTRIB - 1) workgroups (csrc/rpa_kernels.hip, kHeavyContrib)
 HEAVY_CONTRIB = 32
