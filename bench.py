@@ -362,9 +362,9 @@ def main() -> int:
                     help="KV pool copies rotated so that at least this many bytes separate reuses")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--waves-per-cu", type=int, default=None, help="schedule knob (default: the tuned table)")
-    ap.add_argument("--prefill-tiles", type=int, default=None, choices=[-1, 0, 1, 2],
-                    help="1: prefill kernel, 2: the attention kernel's own prefill tiles, -1: stream-K rows "
-                         "(default: the tuned table)")
+    ap.add_argument("--prefill-tiles", type=int, default=None, choices=[-1, 0, 1, 2, 3],
+                    help="1: prefill kernel, 2: the attention kernel's own prefill tiles, 3: those tiles in "
+                         "one 8-wave workgroup per CU, -1: stream-K rows (default: the tuned table)")
     ap.add_argument("--prefill-cost", type=float, default=None, help="schedule knob (default: the tuned table)")
     ap.add_argument("--host-submit", action="store_true",
                     help="instead of the benchmark, measure the host time to submit one call (C1 shapes, "

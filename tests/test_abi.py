@@ -95,7 +95,7 @@ def test_invalid_shapes_rejected(lib, bad, msg):
 
 
 @pytest.mark.parametrize("knob,msg", [(dict(waves_per_cu=9), b"waves_per_cu"), (dict(waves_per_cu=-1), b"waves_per_cu"),
-                                      (dict(prefill_tiles=3), b"prefill_tiles"),
+                                      (dict(prefill_tiles=4), b"prefill_tiles"),
                                       (dict(prefill_cost=-0.5), b"prefill_cost")])
 def test_invalid_tuning_knobs_rejected(lib, knob, msg):
     opts = _lib.RpaOptions(sm_scale=1.0, **knob)

@@ -146,6 +146,10 @@ struct Params {
   // query tokens are its tiles of pf_tq tokens (256 rows), the attention kernel skips them and
   // runs no prefill role of its own
   bool pf_kernel;
+  // co-resident layout (mixed batches): 4-wave workgroups, two per CU (workgroups b and b + grid/2
+  // share a CU); the prefill tiles are 128 rows, one prefill workgroup beside one stream-K
+  // workgroup on a CU, and stream-K workgroups join the tile queue when their range is done
+  int co;
   int pk_grid;                 // prefill-kernel workgroups
   float* pk_acc;               // [2 * pk_grid][256][kD] split-tile partials
   float* pk_ml;                // [2 * pk_grid][256][2]
@@ -1684,6 +1688,23 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
 
 // The prefill role of a workgroup: take tiles from the queue until it runs dry.  wsi: the four
 // metadata windows (nseq <= 256), total: the call's tile count.
+// The chunks a tile visits, from its sequence's kv_len / q_len and its tokens tok0 .. tok0+ntok-1:
+// up to the causal limit of its last row, from the sliding-window start of its first row.
+// c_hi <= c_lo: no key to visit (q_len > kv_len: rows left unwritten).
+__device__ __forceinline__ void pf_tile_chunks(const Params& p, PfTile& tl) {
+  tl.c_lo = tl.c_hi = 0;
+  const int prior = tl.kv_len - tl.q_len;
+  const int pos_hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
+  if (pos_hi < 0) return;
+  int lo = 0;
+  if (p.sliding_window > 0) {
+    lo = prior + tl.tok0 - p.sliding_window + 1;  // keys below are masked for every row
+    lo = lo < 0 ? 0 : lo;
+  }
+  tl.c_lo = lo / KV_CHUNK;
+  tl.c_hi = ((pos_hi < tl.kv_len - 1 ? pos_hi : tl.kv_len - 1) + KV_CHUNK) / KV_CHUNK;
+}
+
 // Tile ti of the call's queue order (sequences in window order, each sequence's tiles last token
 // block first, kv heads innermost): its sequence, kv head, token block and chunk range.  seq < 0:
 // no tile (not reached for ti < total); c_hi <= c_lo: no key to visit.  Wave-collective.
@@ -1719,16 +1740,7 @@ __device__ __forceinline__ PfTile pf_lookup(const Params& p, const SeqInfo wsi[4
     off += tot;
   }
   if (tl.seq < 0) return tl;
-  const int prior = tl.kv_len - tl.q_len;
-  const int pos_hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
-  if (pos_hi < 0) return tl;                          // q_len > kv_len: rows left unwritten
-  int lo = 0;
-  if (p.sliding_window > 0) {
-    lo = prior + tl.tok0 - p.sliding_window + 1;  // keys below are masked for every row
-    lo = lo < 0 ? 0 : lo;
-  }
-  tl.c_lo = lo / KV_CHUNK;
-  tl.c_hi = ((pos_hi < tl.kv_len - 1 ? pos_hi : tl.kv_len - 1) + KV_CHUNK) / KV_CHUNK;
+  pf_tile_chunks(p, tl);
   return tl;
 }
 
@@ -1775,6 +1787,371 @@ __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], i
     const PfTile tl = pf_lookup(p, wsi, pf_min, ti, lane);
     if (tl.seq < 0 || tl.c_hi <= tl.c_lo) continue;
     pf_tile<NP, UPG>(p, tl, lds, wv, n, j, err);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// prefill tiles of the co-resident layout (Params::co): 4-wave workgroups, 128-row tiles
+// ---------------------------------------------------------------------------------------------
+// A tile is (sequence, kv head, 128 / G tokens); wave w owns rows 32w .. 32w+31 as two 16-row MFMA
+// blocks, its queries in registers.  K/V chunks (32 keys) go from HBM straight into LDS with
+// gfx950's global_load_lds_dwordx4 (no registers held for data in flight), into a ring of four
+// 16 KiB slots, three chunks ahead of the compute.  Slot layout: K as 256-byte key rows whose
+// 16-byte column groups sit at group ^ (key % 16) (conflict-free A fragment reads), then V as
+// 256-byte key rows whose 32-byte dim blocks sit at block ^ (key % 8) (conflict-free transposing
+// reads, read_vt_fragments_x).  Each DMA instruction writes one contiguous KiB (64 lanes x 16 B);
+// the lane's source address picks which piece lands where.  The chunks' page ids come from a
+// table the workgroup copies into LDS per segment of up to kCoPages pages.
+//
+// Waits: the DMA is issued from inline asm, so the compiler neither sees nor counts it, and the
+// only loads in the step loop are those DMAs (kCoDmas per wave per chunk).  The step's barrier
+// (co_barrier) therefore waits with an exact vmcnt for this wave's share of the chunk it is about
+// to read, and the barrier makes every wave's share visible.  (Issued as the compiler's builtin,
+// the DMA makes it wait for every DMA in flight before each LDS read it cannot tell apart,
+// draining the ring every step.)  No load in asm writes a register: a register the compiler
+// believed loaded could be reused before the load lands.
+constexpr int kCoWaves = 4;
+constexpr int kCoSlot = 16384;                    // one chunk: K (8 KiB) + V (8 KiB)
+constexpr int kCoSlots = 4;
+constexpr int kCoOrderBase = kCoSlots * kCoSlot;  // tile order tables (2 x kPfOrderMax ints)
+constexpr int kCoPages = 256;                     // page-id table entries
+constexpr int kCoPageBase = kCoOrderBase + 2 * kPfOrderMax * 4;
+static_assert(kCoPageBase + kCoPages * 4 <= kCoWaves * kWaveLds,
+              "co-resident prefill LDS exceeds the workgroup's allocation");
+constexpr int kCoDmas = 4;  // per wave and chunk: two K and two V DMAs
+
+// The step's barrier: this wave's DMAs of the chunk about to be read have landed (the two younger
+// chunks' may still be in flight), its LDS reads are done, then s_barrier.  A workgroup-scope
+// release fence (__syncthreads) would wait for every DMA in flight.
+__device__ __forceinline__ void co_barrier() {
+  static_assert(2 * kCoDmas == 8, "co_barrier's vmcnt");
+  asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Every DMA of this wave has landed.
+__device__ __forceinline__ void co_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Byte address in LDS of a pointer into the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr_of(const void* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
+
+// One 16-byte-per-lane DMA into the 1 KiB of LDS at lds_addr (wave-uniform); m0 is saved and
+// restored around it, so the compiler's use of m0 is untouched.
+__device__ __forceinline__ void co_dma(const void* src, uint32_t lds_addr) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(src), "s"(lds_addr)
+      : "memory");
+}
+
+// Per-lane parts of the DMA addresses, the same for every chunk: lane l of wave wv carries, for
+// t = 0, 1, key 4i + l/16 of block i = wv + 4t, and 16-byte LDS position l % 16 of that key's K row
+// (column group pos ^ (key % 16)) and V row (dims of 32-byte block (pos/2) ^ (key % 8), half pos % 2).
+struct CoLane {
+  int key[2];   // key within the chunk
+  int colk[2];  // element offset of the K piece within the key's row of kv head h
+  int colv[2];  // element offset of the V piece
+};
+
+__device__ __forceinline__ CoLane co_lane(int wv, int lane) {
+  CoLane c;
+  const int pos = lane & 15;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int k = 4 * (wv + kCoWaves * t) + (lane >> 4);
+    c.key[t] = k;
+    c.colk[t] = 8 * (pos ^ (k & 15));
+    c.colv[t] = kD + 16 * ((pos >> 1) ^ (k & 7)) + 8 * (pos & 1);
+  }
+  return c;
+}
+
+// A segment of a tile's chunks whose pages fit the page-id table.
+struct CoSeg {
+  int c_lo, c_hi;  // chunks
+  int p_lo;        // page of chunk c_lo (table entry 0)
+  int cps;         // chunks per page (page_size / 32)
+};
+
+// This wave's share of chunk c into LDS slot dst (wave-uniform LDS address): K blocks wv and
+// wv + 4 (keys 4i .. 4i+3 each, 1 KiB per DMA) and the same V blocks.  Keys past kv_len read key
+// kv_len - 1 (scores -inf; V meets P = 0).
+__device__ __forceinline__ void co_issue(const Params& p, const PfTile& tl, const CoLane& cl, const CoSeg& sg,
+                                         const int* ptab, int c, uint32_t dst, int wv, int& err) {
+  int pg = uni(ptab[c / sg.cps - sg.p_lo]);
+  if (pg < 0 || pg >= p.P) {  // out-of-range page id: never dereferenced
+    err |= ERR_PAGE;
+    pg = 0;
+  }
+  const uint16_t* base = (const uint16_t*)p.kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h);
+  const int kmax = tl.kv_len - 1 - c * KV_CHUNK, stride = 2 * p.Hkv * kD;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t i = (uint32_t)(wv + kCoWaves * t);
+    const uint16_t* row = base + (unsigned)((cl.key[t] < kmax ? cl.key[t] : kmax) * stride);
+    co_dma(row + cl.colk[t], dst + 1024u * i);
+    co_dma(row + cl.colv[t], dst + 8192u + 1024u * i);
+  }
+}
+
+// read_vt_fragments for a slot's V rows (256 bytes at slot + 8192, 32-byte blocks at block ^
+// (key % 8)).
+__device__ __forceinline__ void read_vt_fragments_x(const uint8_t* slot, int n, int j, bf16x8 va[8]) {
+  typedef __attribute__((address_space(3))) short4_t* lds_s4;
+  const int k = 4 * j + (n >> 2), x = k & 7;  // key of the low half; the high half (k + 16) has the same k % 8
+  const uint8_t* vb = slot + 8192 + k * 256 + 8 * (n & 3);
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    const int off = 32 * (d ^ x);
+    const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(vb + off));
+    const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(vb + 16 * 256 + off));
+    va[d] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+}
+
+// S = K Q^T of chunk slot buf for the wave's two row blocks: the eight K fragment reads go out
+// together, then the sixteen MFMAs.
+__device__ __forceinline__ void co_qk(const uint8_t* buf, const bf16x8 q[2][4], f32x4 sc[2][2], int n, int j) {
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) sc[rb][0] = sc[rb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 a[4][2];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) a[s][kb] = *(const bf16x8*)(buf + (16 * kb + n) * 256 + 16 * ((4 * s + j) ^ n));
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc[0][kb] = mfma(a[s][kb], q[0][s], sc[0][kb]);
+      sc[1][kb] = mfma(a[s][kb], q[1][s], sc[1][kb]);
+    }
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+}
+
+// Softmax and O += P V of chunk slot buf, the V^T fragments read before the softmax.
+template <bool PLAIN>
+__device__ __forceinline__ void co_pv(const Params& p, const PfTile& tl, int c, const uint8_t* buf, const f32x4 sc[2][2],
+                                      PfRow st[2], int n, int j) {
+  bf16x8 va[8];
+  read_vt_fragments_x(buf, n, j, va);
+  bf16x8 pb0, pb1;
+  if constexpr (PLAIN) {
+    pb0 = pf_softmax_plain(p, sc[0], st[0]);
+    pb1 = pf_softmax_plain(p, sc[1], st[1]);
+  } else {
+    pb0 = pf_softmax(p, tl, c, sc[0], st[0], j);
+    pb1 = pf_softmax(p, tl, c, sc[1], st[1], j);
+  }
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    st[0].acc[d] = mfma(va[d], pb0, st[0].acc[d]);
+    st[1].acc[d] = mfma(va[d], pb1, st[1].acc[d]);
+  }
+}
+
+// Step on chunk c of segment sg.  In flight on entry: the DMAs of c, c + 1, c + 2.  Wait for this
+// wave's DMAs of c, barrier (every wave's share of c is in LDS, and every wave is done with chunk
+// c - 1's slot); S = K Q^T of c; the DMAs of c + 3 into the freed slot (issued while the MFMAs
+// run); the softmax and P V of c.
+template <bool PLAIN>
+__device__ __forceinline__ void co_step(const Params& p, const PfTile& tl, const CoLane& cl, const CoSeg& sg,
+                                        const int* ptab, int c, uint8_t* lds, const bf16x8 q[2][4], PfRow st[2],
+                                        int wv, int n, int j, int& err) {
+  const int last = sg.c_hi - 1;
+  co_barrier();
+  const uint8_t* buf = lds + (c & (kCoSlots - 1)) * kCoSlot;
+  f32x4 sc[2][2];
+  co_qk(buf, q, sc, n, j);
+  const int cn = c + 3 < last ? c + 3 : last;
+  co_issue(p, tl, cl, sg, ptab, cn, lds_addr_of(lds + ((c + 3) & (kCoSlots - 1)) * kCoSlot), wv, err);
+  co_pv<PLAIN>(p, tl, c, buf, sc, st, n, j);
+}
+
+__device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const CoLane& cln, uint8_t* lds, int wv,
+                                        int lane, int n, int j, int& err) {
+  PfRow st[2];
+  bf16x8 q[2][4];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int r = 32 * wv + 16 * rb + n;
+    const int tok = r / p.G, g = r - tok * p.G;
+    st[rb].ok = tok < tl.ntok;
+    st[rb].pos = tl.kv_len - tl.q_len + tl.tok0 + tok;
+    st[rb].ok = st[rb].ok && st[rb].pos >= 0;
+    const int qtok = st[rb].ok ? tl.q_start + tl.tok0 + tok : tl.q_start;
+    const uint16_t* qp = p.q + ((size_t)qtok * p.Hq + tl.h * p.G + (st[rb].ok ? g : 0)) * kD + 8 * j;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) q[rb][s] = *(const bf16x8*)(qp + 32 * s);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) st[rb].acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st[rb].m = -INFINITY;
+    st[rb].l = 0.f;
+  }
+  // chunks below cp are seen in full by every row (the plain softmax); the rest (the diagonal, a
+  // window, a soft cap) take the general one
+  int cp = tl.c_lo;
+  if (!(p.soft_cap > 0.f) && p.sliding_window <= 0 && p.scale_log2 > 0.f) {
+    const int pos_min = tl.kv_len - tl.q_len + tl.tok0;
+    cp = (pos_min + 1) / KV_CHUNK;
+    cp = cp < tl.kv_len / KV_CHUNK ? cp : tl.kv_len / KV_CHUNK;
+  }
+  int* ptab = (int*)(lds + kCoPageBase);
+  CoSeg sg;
+  sg.cps = p.S / KV_CHUNK;
+  for (sg.c_lo = tl.c_lo; sg.c_lo < tl.c_hi; sg.c_lo = sg.c_hi) {
+    sg.p_lo = sg.c_lo / sg.cps;
+    sg.c_hi = (sg.p_lo + kCoPages) * sg.cps;
+    sg.c_hi = sg.c_hi < tl.c_hi ? sg.c_hi : tl.c_hi;
+    const int npg = (sg.c_hi - 1) / sg.cps - sg.p_lo + 1;
+    __syncthreads();  // the previous segment's or tile's table and slots are no longer read
+    for (int t = threadIdx.x; t < npg; t += kCoWaves * 64) ptab[t] = p.page_indices[(size_t)tl.seq * p.PPS + sg.p_lo + t];
+    // the table and (first segment) the queries have landed, on every path: the compiler then has
+    // no load of its own left to wait for inside the step loop
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+    const int c0 = sg.c_lo, last = sg.c_hi - 1;
+    auto cl = [&](int c) { return c < last ? c : last; };
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      co_issue(p, tl, cln, sg, ptab, cl(c0 + k), lds_addr_of(lds + ((c0 + k) & (kCoSlots - 1)) * kCoSlot), wv, err);
+    int c = c0;
+    const int cpe = cp < sg.c_hi ? cp : sg.c_hi;
+    for (; c < cpe; ++c) co_step<true>(p, tl, cln, sg, ptab, c, lds, q, st, wv, n, j, err);
+    for (; c < sg.c_hi; ++c) co_step<false>(p, tl, cln, sg, ptab, c, lds, q, st, wv, n, j, err);
+    co_drain();  // the clamped DMAs past the segment land before the slots are reused
+  }
+
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const float lt = rows4_sum(st[rb].l);
+    if (!st[rb].ok) continue;
+    const int r = 32 * wv + 16 * rb + n;
+    const int tok = r / p.G, g = r - tok * p.G;
+    const float inv = 1.f / lt;
+    uint16_t* op = p.out + ((size_t)(tl.q_start + tl.tok0 + tok) * p.Hq + tl.h * p.G + g) * kD + 4 * j;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      u32x2 w;
+      w[0] = pack_bf16x2(st[rb].acc[d][0] * inv, st[rb].acc[d][1] * inv);
+      w[1] = pack_bf16x2(st[rb].acc[d][2] * inv, st[rb].acc[d][3] * inv);
+      *(u32x2*)(op + 16 * d) = w;
+    }
+  }
+}
+
+// The (sequence, token block) pairs of the call's prefill tiles in queue order (sequences in window
+// order, each sequence's token blocks last first), held per lane: lane l's sequence of window w
+// owns pairs base[w] + off[w] .. + nt[w] - 1.  One DPP scan per window; a pair's tile then costs
+// a ballot and a few readlanes (co_tile_of), not a scan.
+struct CoPairs {
+  int off[4], nt[4];  // per lane
+  int base[5];        // uniform; base[4] = pairs in all
+};
+
+__device__ __forceinline__ CoPairs co_pairs(const Params& p, const SeqInfo wsi[4], int pf_min, int lane) {
+  CoPairs cp;
+  int base = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int nt = pf_tiles_of(p, wsi[w], pf_min);
+    const int incl = wave_incl_scan32(nt, lane);
+    cp.nt[w] = nt;
+    cp.off[w] = incl - nt;
+    cp.base[w] = base;
+    base += rl(incl, 63);
+  }
+  cp.base[4] = base;
+  return cp;
+}
+
+// The tile of pair pi (< base[4]) and kv head h.  Wave-collective.
+__device__ __forceinline__ PfTile co_tile_of(const Params& p, const SeqInfo wsi[4], const CoPairs& cp, int pi, int h) {
+  PfTile tl;
+  tl.seq = -1;
+  tl.c_lo = tl.c_hi = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    if (pi >= cp.base[w] && pi < cp.base[w + 1]) {
+      const int r = pi - cp.base[w];
+      // the last lane whose first pair is <= r holds pair r (offsets never decrease, and a later lane
+      // with no pairs has an offset above r)
+      const int idx = __popcll(__ballot(cp.off[w] <= r)) - 1;
+      const int k = r - rl(cp.off[w], idx), nt = rl(cp.nt[w], idx);
+      tl.seq = 64 * w + idx;
+      tl.kv_len = rl(wsi[w].kv_len, idx);
+      tl.q_len = rl(wsi[w].q_len, idx);
+      tl.q_start = rl(wsi[w].q_start, idx);
+      tl.h = h;
+      tl.tok0 = (nt - 1 - k) * p.pf_tq;  // last token block first
+      tl.ntok = tl.q_len - tl.tok0 < p.pf_tq ? tl.q_len - tl.tok0 : p.pf_tq;
+    }
+  }
+  if (tl.seq >= 0) pf_tile_chunks(p, tl);
+  return tl;
+}
+
+// The co-resident layout's prefill role: take tiles from the queue until it runs dry.  The queue
+// hands out tiles longest first (as pf_role): the workgroup writes the chunk count of every pair
+// (one lane per sequence), ranks the pairs in LDS and maps queue position r to the pair of rank
+// r / Hkv, kv head r % Hkv.  Calls with more pairs than kPfOrderMax keep the queue order.
+__device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, int total, uint8_t* lds,
+                                        int* s_tile, int lane, int wv, int n, int j, int& err) {
+  const CoPairs cp = co_pairs(p, wsi, pf_min, lane);
+  const int npairs = cp.base[4];
+  const bool ranked = npairs <= kPfOrderMax;
+  int* psz = (int*)(lds + kCoOrderBase);
+  int* pord = psz + kPfOrderMax;
+  const CoLane cln = co_lane(wv, lane);
+  if (ranked) {
+    if (wv == 0) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        PfTile t;
+        t.kv_len = wsi[w].kv_len;
+        t.q_len = wsi[w].q_len;
+        for (int k = 0; k < cp.nt[w]; ++k) {
+          t.tok0 = (cp.nt[w] - 1 - k) * p.pf_tq;
+          t.ntok = t.q_len - t.tok0 < p.pf_tq ? t.q_len - t.tok0 : p.pf_tq;
+          pf_tile_chunks(p, t);
+          psz[cp.base[w] + cp.off[w] + k] = t.c_hi > t.c_lo ? t.c_hi - t.c_lo : 0;
+        }
+      }
+      for (int i = npairs + lane; i < (npairs + 3) / 4 * 4; i += 64) psz[i] = -1;  // pad to whole int4s
+    }
+    __syncthreads();
+    const int n4 = (npairs + 3) / 4;
+    for (int i = threadIdx.x; i < npairs; i += blockDim.x) {
+      const int si = psz[i];
+      int r = 0;
+      for (int k4 = 0; k4 < n4; ++k4) {
+        const int4 v = ((const int4*)psz)[k4];
+        const int k = 4 * k4;
+        r += (v.x > si || (v.x == si && k < i)) + (v.y > si || (v.y == si && k + 1 < i)) +
+             (v.z > si || (v.z == si && k + 2 < i)) + (v.w > si || (v.w == si && k + 3 < i));
+      }
+      pord[r] = i;
+    }
+    __syncthreads();
+  }
+  for (;;) {
+    if (threadIdx.x == 0) *s_tile = atomicAdd(p.err + kQueueWord, 1);
+    __syncthreads();
+    const int tq = uni(*s_tile);
+    __syncthreads();
+    if (tq >= total) break;
+    const int pi = ranked ? uni(pord[tq / p.Hkv]) : tq / p.Hkv;
+    const PfTile tl = co_tile_of(p, wsi, cp, pi, tq % p.Hkv);
+    if (tl.seq < 0 || tl.c_hi <= tl.c_lo) continue;
+    co_tile(p, tl, cln, lds, wv, lane, n, j, err);
   }
 }
 
@@ -1882,14 +2259,32 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       gpre = (int)((float)p.grid * pw / (pw + dw) + 0.5f);
       gpre = gpre < 1 ? 1 : gpre;
       if (W > 0 && gpre > p.grid - 1) gpre = p.grid - 1;
+      if (p.co && gpre > p.grid / 2) gpre = p.grid / 2;  // at most one prefill workgroup per CU
       if (gpre > pf_total) gpre = pf_total;
     }
   }
-  if (MODE == KV_BF16 && b < gpre) {  // (HG == 8: one K and one V piece per thread per chunk)
-    __shared__ int s_tile;
-    pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+  // Roles.  One workgroup per CU (8 waves): workgroups 0 .. gpre-1 take prefill tiles, the rest
+  // run stream-K.  Co-resident layout (two 4-wave workgroups per CU, b and b + grid/2 on one CU):
+  // workgroups grid/2 .. grid/2 + gpre - 1 take prefill tiles, so each sits beside a stream-K
+  // workgroup, and every stream-K workgroup takes tiles too once its range is done.
+  __shared__ int s_tile;
+  bool pf_first;
+  int bd;
+  if (MODE == KV_BF16 && p.co) {
+    const int half = p.grid >> 1;
+    pf_first = b >= half && b < half + gpre;
+    bd = pf_first ? -1 : (b < half ? b : b - gpre);
+  } else {
+    pf_first = b < gpre;
+    bd = b - gpre;
   }
-  const int bd = b - gpre, gd = p.grid - gpre;  // stream-K workgroup index and count
+  const int gd = p.grid - gpre;  // stream-K workgroup count
+  if (MODE == KV_BF16 && pf_first) {
+    if (UPG && p.co)
+      co_role(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+    else  // (HG == 8: one K and one V piece per thread per chunk)
+      pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+  }
   const Partition pt = make_partition_fast(W, gd > 0 ? gd : 1);
   const long long u0 = uni64(range_start(bd, pt)), u1 = uni64(range_start(bd + 1, pt));
   if (bd >= 0 && W > 0 && u0 < u1) {
@@ -1981,6 +2376,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+  }
+  if (MODE == KV_BF16 && UPG && p.co && !pf_first && pf_total > 0) {
+    __syncthreads();  // every wave is done with its stream-K LDS regions
+    co_role(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
 
   {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
@@ -2837,15 +3236,23 @@ int occupancy_grid(int cus, int hg) {
   return cus * per_cu;
 }
 
-// waves_per_cu (rpa_options_t, 1..kMaxWavesPerCU - 1) lowers the waves per CU of the grid -- a
-// per-call tuning knob, like the reference's block-size parameters.
-int grid_for_call(const DeviceInfo& d, int mode, int hg, int waves_per_cu) {
-  int grid = d.grid[mode][hg];
+// The attention grid: the occupancy grid (occ workgroups of hg waves on `cus` CUs), and with
+// waves_per_cu in 1 .. kMaxWavesPerCU - 1 (rpa_options_t, a per-call tuning knob like the
+// reference's block-size parameters) at most cus * waves_per_cu waves in all: floor(cus *
+// waves_per_cu / hg) workgroups, at least one.  With 8 waves per workgroup, waves_per_cu = 4 is
+// one workgroup per two CUs.
+int grid_rule(int occ, int cus, int hg, int waves_per_cu) {
+  int grid = occ;
   if (waves_per_cu >= 1 && waves_per_cu < kMaxWavesPerCU) {
-    const int per_cu = waves_per_cu / hg > 0 ? waves_per_cu / hg : 1;
-    if (grid > d.cus * per_cu) grid = d.cus * per_cu;
+    long long cap = (long long)cus * waves_per_cu / hg;
+    cap = cap < 1 ? 1 : cap;
+    if (grid > cap) grid = (int)cap;
   }
   return grid;
+}
+
+int grid_for_call(const DeviceInfo& d, int mode, int hg, int waves_per_cu) {
+  return grid_rule(d.grid[mode][hg], d.cus, hg, waves_per_cu);
 }
 
 int device_info(DeviceInfo& out) {
@@ -3342,6 +3749,43 @@ struct FusedInline {
   int rel_extent;
 };
 
+// Where the rows of sequences with >= 16 query tokens go (bf16 KV without scales, masked keys at
+// weight 0), and the workgroup shape that follows:
+//   prefill_tiles 2 or 0, page size a multiple of 32, Hkv a multiple of 4, and num_tokens >=
+//     max_num_seqs + 15 (the batch can hold such a sequence; a batch of one token per sequence
+//     keeps the decode layout): the attention kernel's tiles in the co-resident layout (4-wave
+//     workgroups, two per CU, one prefill and one stream-K workgroup side by side);
+//   prefill_tiles 3, or 2 / 0 otherwise with eight kv heads per workgroup: the attention
+//     kernel's tiles in 8-wave workgroups, one per CU, roles split by CU;
+//   prefill_tiles 1, or 0 when neither applies: the prefill kernel, when chunks lie in one page
+//     (page size a multiple of 64);
+//   otherwise, and with -1: causal row blocks of the stream-K role.
+void resolve_layout(Params& p, int mode, const rpa_shape_t* shape, const rpa_options_t* opt) {
+  const int pt = opt->prefill_tiles;
+  const bool bf = mode == KV_BF16 && p.skip_masked;
+  const bool co_ok = bf && (pt == 0 || pt == 2) && p.S % KV_CHUNK == 0 && p.Hkv % kCoWaves == 0 &&
+                     p.G <= 32 * kCoWaves && (long long)shape->num_tokens >= (long long)shape->max_num_seqs + 15;
+  const bool tiles_ok = bf && p.HG == 8 && p.G <= 32 * p.HG;
+  const bool pk_ok = bf && p.G <= kPkRows && p.S % kPkChunk == 0;
+  const float cost = opt->prefill_cost > 0.f ? opt->prefill_cost : kPfCost;
+  if (co_ok) {
+    p.co = 1;
+    p.HG = kCoWaves;
+    p.NG = p.Hkv / kCoWaves;
+    p.pf_tq = 32 * kCoWaves / p.G;
+    p.pf_min = 16;
+    p.pf_cost = cost;
+  } else if (pk_ok && (pt == 1 || (pt == 0 && !tiles_ok))) {
+    p.pf_kernel = true;
+    p.pf_tq = kPkRows / p.G;
+    p.pf_min = 16;
+  } else if (tiles_ok && pt >= 0) {
+    p.pf_tq = 32 * p.HG / p.G;
+    p.pf_min = 16;
+    p.pf_cost = cost;
+  }
+}
+
 static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const void* q, const void* kv_pages,
                       const float* kv_scales, const int32_t* kv_lens, const int32_t* page_indices,
                       const int32_t* cu_q_lens, const int32_t* num_seqs, void* out, void* workspace,
@@ -3357,8 +3801,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (opt->sliding_window < 0) return fail(RPA_E_INVALID, "sliding_window must be positive");
   if (opt->waves_per_cu < 0 || opt->waves_per_cu > kMaxWavesPerCU)
     return fail(RPA_E_INVALID, "waves_per_cu must be in [0, 8]");
-  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 2)
-    return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0, 1 or 2");
+  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 3)
+    return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0, 1, 2 or 3");
   if (!(opt->prefill_cost >= 0.f && opt->prefill_cost <= 64.f))
     return fail(RPA_E_INVALID, "prefill_cost must be in [0, 64]");
   if (shape->num_tokens == 0 || shape->max_num_seqs == 0) return RPA_OK;
@@ -3425,25 +3869,9 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (kv_scales) return fail(RPA_E_INVALID, "kv_scales is only used with fp8 kv_pages");
     if (opt->has_k_scale || opt->has_v_scale) mode = KV_BF16_SCALED;
   }
+  resolve_layout(p, mode, shape, opt);
   p.grid = grid_for_call(d, mode, p.HG, opt->waves_per_cu);
-  // Sequences with >= 16 query tokens (bf16 KV without scales, masked keys at weight 0):
-  //   prefill_tiles 2, or 0 with eight kv heads per workgroup: the attention kernel's own prefill
-  //     tiles (measured faster on C3 than the prefill kernel: 187 us against 272 us for the call);
-  //   prefill_tiles 1, or 0 otherwise: the prefill kernel, when chunks lie in one page (page size a
-  //     multiple of 64);
-  //   otherwise, and with -1: causal row blocks of the stream-K role.
-  const bool tiles_ok = mode == KV_BF16 && p.skip_masked && p.HG == 8 && p.G <= 32 * p.HG;
-  const bool pk_ok = mode == KV_BF16 && p.skip_masked && p.G <= kPkRows && p.S % kPkChunk == 0;
-  if (pk_ok && (opt->prefill_tiles == 1 || (opt->prefill_tiles == 0 && !tiles_ok))) {
-    p.pf_kernel = true;
-    p.pf_tq = kPkRows / p.G;
-    p.pf_min = 16;
-    p.pk_grid = d.cus;
-  } else if (tiles_ok && opt->prefill_tiles >= 0) {
-    p.pf_tq = 32 * p.HG / p.G;
-    p.pf_min = 16;
-    p.pf_cost = opt->prefill_cost > 0.f ? opt->prefill_cost : kPfCost;
-  }
+  if (p.pf_kernel) p.pk_grid = d.cus;
   hipStream_t st = (hipStream_t)stream;
   if (ev_begin && hipEventRecord((hipEvent_t)ev_begin, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");

@@ -212,10 +212,11 @@ def _static_plan(q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, kv_sca
     if not (isinstance(wpc, int) and 0 <= wpc <= 8):
         raise ValueError(f"waves_per_cu={wpc!r} must be an int in [0, 8]")
     # True / 0: the library's choice; 1: the prefill kernel; 2: the attention kernel's own prefill
-    # tiles; False / -1: causal row blocks of the stream-K role
+    # tiles (two 4-wave workgroups per CU where they apply); 3: the attention kernel's tiles in one
+    # 8-wave workgroup per CU; False / -1: causal row blocks of the stream-K role
     tiles = {True: 0, False: -1}.get(tiles, tiles) if isinstance(tiles, bool) else tiles
-    if tiles not in (-1, 0, 1, 2):
-        raise ValueError(f"prefill_tiles={tiles!r} must be a bool or one of -1, 0, 1, 2")
+    if tiles not in (-1, 0, 1, 2, 3):
+        raise ValueError(f"prefill_tiles={tiles!r} must be a bool or one of -1, 0, 1, 2, 3")
     if not (0.0 <= float(cost) <= 64.0):
         raise ValueError(f"prefill_cost={cost!r} must be in [0, 64]")
     mask_value = knobs["mask_value"]
@@ -259,7 +260,7 @@ def ragged_paged_attention(
     kernel_events: tuple | None = None,      # (begin, end) events around the attention kernel: torch.cuda.Event
                                              # or timing.KernelEvent (anything with a .cuda_event handle)
     waves_per_cu: int | None = None,         # tuning knobs (rpa_options_t); None = the tuned table's entry
-    prefill_tiles: bool | int | None = None, # 1 prefill kernel, 2 in-kernel tiles, True/0 either, False/-1 rows
+    prefill_tiles: bool | int | None = None, # 1 prefill kernel, 2/3 in-kernel tiles, True/0 auto, False/-1 rows
     prefill_cost: float | None = None,
 ) -> torch.Tensor:
     """Ragged paged attention (mixed prefill and decode) on MI355X.

@@ -49,8 +49,8 @@ def validate_entry(entry: dict) -> dict:
         raise ValueError(f"waves_per_cu={e['waves_per_cu']!r} must be an int in [0, 8]")
     if isinstance(e["prefill_tiles"], bool):  # True: the library's choice; False: stream-K rows
         e["prefill_tiles"] = 0 if e["prefill_tiles"] else -1
-    if e["prefill_tiles"] not in (-1, 0, 1, 2):
-        raise ValueError(f"prefill_tiles={e['prefill_tiles']!r} must be -1, 0, 1 or 2 (or a bool)")
+    if e["prefill_tiles"] not in (-1, 0, 1, 2, 3):
+        raise ValueError(f"prefill_tiles={e['prefill_tiles']!r} must be -1, 0, 1, 2 or 3 (or a bool)")
     if not (isinstance(e["prefill_cost"], (int, float)) and 0.0 <= float(e["prefill_cost"]) <= 64.0):
         raise ValueError(f"prefill_cost={e['prefill_cost']!r} must be in [0, 64]")
     e["prefill_cost"] = float(e["prefill_cost"])
