@@ -63,14 +63,21 @@ typedef struct rpa_shape {
  * schedule, never the result beyond fp32 summation order.  They take the place
  * of the reference's per-call block sizes num_kv_pages_per_block /
  * num_queries_per_block (ragged_paged_attention.py:726-728, :801-816):
- *   waves_per_cu   1..7 caps the persistent attention grid at that many waves
- *                  per compute unit (0 or 8: the kernel's occupancy, 8);
+ *   waves_per_cu   1..7 caps the persistent attention grid at cus * waves_per_cu
+ *                  waves: floor(cus * waves_per_cu / waves_per_workgroup)
+ *                  workgroups, at least one (with 8-wave workgroups, 4 is one
+ *                  workgroup per two CUs); 0 or 8: the kernel's occupancy, 8
+ *                  waves per CU (rpa_attention_grid reports the result);
  *   prefill_tiles  sequences with at least 16 query tokens (bf16 KV without
  *                  scales, the default mask value): 2 = the attention kernel's
- *                  own MFMA prefill tiles (8 kv heads per workgroup); 1 = the
- *                  standalone prefill kernel (page size a multiple of 64);
- *                  0 = the first of those two that applies; -1 = causal row
- *                  blocks of the stream-K role (also whenever neither applies);
+ *                  own MFMA prefill tiles, in two 4-wave workgroups per CU (one
+ *                  prefill, one stream-K) when the page size is a multiple of
+ *                  32, Hkv a multiple of 4 and num_tokens >= max_num_seqs + 15,
+ *                  else in one 8-wave workgroup per CU (8 kv heads per
+ *                  workgroup); 3 = those tiles in one 8-wave workgroup per CU;
+ *                  1 = the standalone prefill kernel (page size a multiple of
+ *                  64); 0 = 2, else 1, whichever applies first; -1 = causal row
+ *                  blocks of the stream-K role (also whenever none applies);
  *   prefill_cost   > 0: the cost of one prefill-tile chunk step in stream-K
  *                  units, which sets the work split between the two roles
  *                  (0 = 0.45). */
@@ -88,6 +95,15 @@ typedef struct rpa_options {
   int32_t prefill_tiles;
   float prefill_cost;
 } rpa_options_t;
+
+/* The attention launch a call of this shape and these options makes: *grid workgroups of
+ * *waves_per_workgroup waves, on a device of `cus` compute units at the kernel's nominal
+ * occupancy (8 waves per CU within 160 KiB of LDS; no device is touched), or on the current
+ * device when cus is 0.  No counterpart in the reference (its grid is (Hq/Hq_blk, cdiv(T,
+ * q_per_blk)), ragged_paged_attention.py:822-823); it lets a tuner tell the waves_per_cu knob's
+ * values apart. */
+int rpa_attention_grid(const rpa_shape_t* shape, const rpa_options_t* options, int32_t cus, int32_t* grid,
+                       int32_t* waves_per_workgroup);
 
 /* ABI version of the loaded library (RPA_ABI_VERSION). */
 int rpa_abi_version(void);

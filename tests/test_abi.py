@@ -153,3 +153,51 @@ def test_v1_invalid_shapes_rejected_before_launch(lib, bad, msg):
 def test_v1_null_pointers_rejected(lib):
     rc = lib.rpa_inkling_decode(ctypes.byref(_v1_shape()), 1.0, *([None] * 8), 0, None)
     assert rc == -1 and b"NULL" in lib.rpa_last_error()
+
+
+class _ShapeCase:
+    """A host case with the shapes of a configuration and no data (zero-stride arrays): all that
+    rpa_attention_grid reads."""
+
+    def __init__(self, T, hq, hkv, n, pps=128, page=64, pages=4000, kv_dtype="bf16"):
+        import numpy as np
+        self.q = np.broadcast_to(np.zeros((1, 1, 1), np.uint16), (T, hq, 128))
+        self.kv_pages = np.broadcast_to(np.zeros((1, 1, 1, 1), np.uint16), (pages, page, 2 * hkv, 128))
+        self.page_indices = np.broadcast_to(np.zeros((1, 1), np.int32), (n, pps))
+        self.sm_scale = 128 ** -0.5
+        self.kv_dtype = kv_dtype
+
+
+@pytest.mark.parametrize("case,knobs,expect", [
+    # decode batch (C2 shapes): 8-wave workgroups, one per CU; waves_per_cu caps the waves in all
+    (dict(T=64, hq=32, hkv=8, n=64), {}, (256, 8)),
+    (dict(T=64, hq=32, hkv=8, n=64), {"waves_per_cu": 8}, (256, 8)),
+    (dict(T=64, hq=32, hkv=8, n=64), {"waves_per_cu": 7}, (224, 8)),
+    (dict(T=64, hq=32, hkv=8, n=64), {"waves_per_cu": 4}, (128, 8)),
+    (dict(T=64, hq=32, hkv=8, n=64), {"waves_per_cu": 1}, (32, 8)),
+    (dict(T=64, hq=32, hkv=8, n=64, kv_dtype="fp8"), {"waves_per_cu": 6}, (192, 8)),
+    # mixed batch (C3 shapes): the co-resident layout, two 4-wave workgroups per CU
+    (dict(T=2072, hq=32, hkv=8, n=28), {}, (512, 4)),
+    (dict(T=2072, hq=32, hkv=8, n=28), {"waves_per_cu": 4}, (256, 4)),
+    (dict(T=2072, hq=32, hkv=8, n=28), {"prefill_tiles": 3}, (256, 8)),
+    (dict(T=2072, hq=32, hkv=8, n=28), {"prefill_tiles": -1}, (256, 8)),
+    (dict(T=2072, hq=32, hkv=8, n=28, page=16), {}, (256, 8)),  # page 16: no co-resident layout
+    # two kv heads (C1 shapes): 2-wave workgroups, four per CU
+    (dict(T=4, hq=8, hkv=2, n=4, page=16), {}, (1024, 2)),
+    (dict(T=4, hq=8, hkv=2, n=4, page=16), {"waves_per_cu": 4}, (512, 2)),
+    (dict(T=4, hq=8, hkv=2, n=4, page=16), {"waves_per_cu": 1}, (128, 2)),
+])
+def test_attention_grid_rule(lib, case, knobs, expect):
+    from tpu_cake_amd import ops
+    assert ops.attention_grid(_ShapeCase(**case), knobs, cus=256) == expect
+
+
+def test_search_refuses_noop_waves_per_cu_candidate():
+    from tpu_cake_amd import ops, search
+    case = _ShapeCase(T=64, hq=32, hkv=8, n=64)
+    grid = lambda c, k: ops.attention_grid(c, k, cus=256)  # noqa: E731
+    c = search.SearchContract(config="c2", baseline="base", candidates=(("base", {}), ("w8", {"waves_per_cu": 8})), rounds=4)
+    with pytest.raises(ValueError, match="RPA_SEARCH_NOOP_CANDIDATE"):
+        search.refuse_noop_candidates(c, case, grid)
+    ok = search.SearchContract(config="c2", baseline="base", candidates=(("base", {}), ("w4", {"waves_per_cu": 4})), rounds=4)
+    search.refuse_noop_candidates(ok, case, grid)

@@ -49,6 +49,10 @@ def test_artifacts_are_deterministic_and_self_consistent(name):
 REF_SCHEDULE_SHA256 = "b97d16b523329ed57890184ad9d6b0ed893d3c666874e919ccf857aa6591f4cc"
 REF_EXPERIMENT_ID = "b288837a2a06fc716e66c3508f761d0d4d01e110df248dadb9fa542b31296932"
 REF_EXPERIMENT_FILE_SHA256 = "9e098004545330efb41513a9b436a8c5f651e46768467f086638f41e3c351717"
+# The reference's id formula (src/tpu_cake/contracts.py:214-224) hashes the profile's
+# minimum_counter_device_planes (default 0, :105), which the checked-in artifact predates: the
+# id its current code gives the same experiment.
+REF_FORMULA_EXPERIMENT_ID = "6f641a51af96c717cbe33ade0300c1736395ceed59824536603e72e5f074180f"
 
 
 def test_reference_inkling_rpa_row_reproduces_the_reference_artifacts(tmp_path, capsys):
@@ -57,11 +61,17 @@ def test_reference_inkling_rpa_row_reproduces_the_reference_artifacts(tmp_path, 
     text = contracts.render_workload("inkling-rpa")
     assert hashlib.sha256(text.encode()).hexdigest() == REF_SCHEDULE_SHA256
     exp = contracts.experiment("inkling-rpa")
-    assert exp.experiment_id == REF_EXPERIMENT_ID and exp.schedule_sha256 == REF_SCHEDULE_SHA256
+    assert exp.schedule_sha256 == REF_SCHEDULE_SHA256
+    assert exp.experiment_id == REF_FORMULA_EXPERIMENT_ID
+    assert contracts.artifact_id(exp, checked_in_form=True) == REF_EXPERIMENT_ID
     out = tmp_path / "exp.json"
-    assert contracts.main(["experiment", "inkling-rpa", "--output", str(out)]) == 0
+    assert contracts.main(["experiment", "inkling-rpa", "--checked-in-form", "--output", str(out)]) == 0
     assert f"EXPERIMENT_WRITTEN workload=inkling-rpa id={REF_EXPERIMENT_ID}" in capsys.readouterr().out
     assert hashlib.sha256(out.read_bytes()).hexdigest() == REF_EXPERIMENT_FILE_SHA256
+    # the default form carries the field and the reference formula's id
+    assert contracts.main(["experiment", "inkling-rpa", "--output", str(out)]) == 0
+    assert f"EXPERIMENT_WRITTEN workload=inkling-rpa id={REF_FORMULA_EXPERIMENT_ID}" in capsys.readouterr().out
+    assert json.loads(out.read_text())["profile"]["minimum_counter_device_planes"] == 0
     assert exp.target.accelerator == "TPU7x" and exp.workload.execution is None
     # a change to the schedule changes both hashes
     assert hashlib.sha256(text.replace("kv_block_size = #builtin.int<8>", "kv_block_size = #builtin.int<16>")

@@ -50,6 +50,7 @@
 
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "rpa.h"
 #include "rpa_schedule.h"
@@ -3738,6 +3739,29 @@ int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* 
   return RPA_OK;
 }
 
+// Workspaces whose last call could not launch its combine kernel (descriptors, flags and the tile
+// counter left set): cleared by the next call on them before it launches.
+std::mutex g_dirty_mu;
+std::vector<const void*> g_dirty_ws;
+
+void mark_workspace_dirty(const void* ws) {
+  std::lock_guard<std::mutex> lock(g_dirty_mu);
+  for (const void* w : g_dirty_ws)
+    if (w == ws) return;
+  g_dirty_ws.push_back(ws);
+}
+
+bool take_workspace_dirty(const void* ws) {
+  std::lock_guard<std::mutex> lock(g_dirty_mu);
+  if (g_dirty_ws.empty()) return false;
+  for (size_t i = 0; i < g_dirty_ws.size(); ++i)
+    if (g_dirty_ws[i] == ws) {
+      g_dirty_ws.erase(g_dirty_ws.begin() + i);
+      return true;
+    }
+  return false;
+}
+
 // The fused decode step's own inputs when it runs in the attention launch (Params::fused).
 struct FusedInline {
   int nseq, entries;
@@ -3748,6 +3772,28 @@ struct FusedInline {
   const uint16_t* rel_proj;
   int rel_extent;
 };
+
+int check_options(const rpa_options_t* opt) {
+  if (opt->sliding_window < 0) return fail(RPA_E_INVALID, "sliding_window must be positive");
+  if (opt->waves_per_cu < 0 || opt->waves_per_cu > kMaxWavesPerCU)
+    return fail(RPA_E_INVALID, "waves_per_cu must be in [0, 8]");
+  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 3)
+    return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0, 1, 2 or 3");
+  if (!(opt->prefill_cost >= 0.f && opt->prefill_cost <= 64.f))
+    return fail(RPA_E_INVALID, "prefill_cost must be in [0, 64]");
+  return RPA_OK;
+}
+
+// Workgroups per CU of the attention kernel at its occupancy (2 waves per SIMD, kMaxWavesPerCU
+// waves) within the CU's LDS, for hg waves per workgroup and lds bytes of dynamic LDS each: what
+// hipOccupancyMaxActiveBlocksPerMultiprocessor reports on gfx950.
+constexpr int kLdsPerCu = 160 * 1024;
+int nominal_per_cu(int hg, size_t lds) {
+  int per_cu = kMaxWavesPerCU / hg;
+  const int by_lds = (int)(kLdsPerCu / (lds + 256));  // 256: the kernel's static LDS, rounded up
+  per_cu = per_cu < by_lds ? per_cu : by_lds;
+  return per_cu < 1 ? 1 : per_cu;
+}
 
 // Where the rows of sequences with >= 16 query tokens go (bf16 KV without scales, masked keys at
 // weight 0), and the workgroup shape that follows:
@@ -3798,13 +3844,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     return fail(RPA_E_INVALID, "NULL metadata or kv_pages pointer");
   if (shape->num_tokens > 0 && (!q || !out)) return fail(RPA_E_INVALID, "NULL q or out pointer");
   if (q == out && q) return fail(RPA_E_INVALID, "out must not alias q");
-  if (opt->sliding_window < 0) return fail(RPA_E_INVALID, "sliding_window must be positive");
-  if (opt->waves_per_cu < 0 || opt->waves_per_cu > kMaxWavesPerCU)
-    return fail(RPA_E_INVALID, "waves_per_cu must be in [0, 8]");
-  if (opt->prefill_tiles < -1 || opt->prefill_tiles > 3)
-    return fail(RPA_E_INVALID, "prefill_tiles must be -1, 0, 1, 2 or 3");
-  if (!(opt->prefill_cost >= 0.f && opt->prefill_cost <= 64.f))
-    return fail(RPA_E_INVALID, "prefill_cost must be in [0, 64]");
+  rc = check_options(opt);
+  if (rc) return rc;
   if (shape->num_tokens == 0 || shape->max_num_seqs == 0) return RPA_OK;
   DeviceInfo d;
   rc = device_info(d);
@@ -3815,6 +3856,16 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
                                      std::to_string(need));
 
   clear_stale_error();
+  if (take_workspace_dirty(workspace)) {  // a previous call on it could not launch its combine
+    const size_t n16 = ws_layout(d).ml / 16;
+    hipLaunchKernelGGL(rpa_scratch_clear_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (u32x4*)workspace, n16);
+    const hipError_t ce = hipGetLastError();
+    if (ce != hipSuccess) {
+      mark_workspace_dirty(workspace);
+      return fail(RPA_E_HIP, std::string("workspace clear failed: ") + hipGetErrorString(ce));
+    }
+  }
   Params p = base_params(shape);
   p.q = (const uint16_t*)q;
   p.kv = (const uint8_t*)kv_pages;
@@ -3895,13 +3946,17 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(RPA_E_HIP, std::string("attention launch failed: ") + hipGetErrorString(e));
+  // From here the attention kernel has run, and its descriptors and tile counter wait in the
+  // workspace for the combine kernel, which returns them to zero: the combine is launched whatever
+  // else fails, and if it cannot be, the workspace is cleared before its next use.
+  int err_rc = RPA_OK;
   if (p.pf_kernel) {
     hipLaunchKernelGGL(rpa_prefill_kernel, dim3(p.pk_grid), dim3(256), kPkLds, st, p);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(RPA_E_HIP, std::string("prefill launch failed: ") + hipGetErrorString(e));
+    if (e != hipSuccess) err_rc = fail(RPA_E_HIP, std::string("prefill launch failed: ") + hipGetErrorString(e));
   }
-  if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess)
-    return fail(RPA_E_HIP, "hipEventRecord(end) failed");
+  if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess && err_rc == RPA_OK)
+    err_rc = fail(RPA_E_HIP, "hipEventRecord(end) failed");
   // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot, then 16 per
   // prefill workgroup
   hipLaunchKernelGGL(rpa_combine_kernel,
@@ -3909,7 +3964,42 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
                           (p.fused ? p.fused_nseq : 0)),
                      dim3(256), 0, st, p);
   e = hipGetLastError();
-  if (e != hipSuccess) return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
+  if (e != hipSuccess) {
+    mark_workspace_dirty(workspace);
+    return fail(RPA_E_HIP, std::string("combine launch failed: ") + hipGetErrorString(e));
+  }
+  return err_rc;
+}
+
+int rpa_attention_grid(const rpa_shape_t* shape, const rpa_options_t* opt, int32_t cus, int32_t* grid,
+                       int32_t* waves_per_workgroup) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  if (!opt || !grid || !waves_per_workgroup) return fail(RPA_E_INVALID, "NULL options or output pointer");
+  rc = check_options(opt);
+  if (rc) return rc;
+  if (cus < 0) return fail(RPA_E_INVALID, "cus must be >= 0");
+  Params p = base_params(shape);
+  const float mask = opt->has_mask_value ? opt->mask_value : kDefaultMask;
+  p.skip_masked = mask <= -1e30f;
+  int mode = KV_BF16;
+  if (shape->kv_dtype == RPA_KV_FP8_E4M3)
+    mode = KV_FP8;
+  else if (opt->has_k_scale || opt->has_v_scale)
+    mode = KV_BF16_SCALED;
+  resolve_layout(p, mode, shape, opt);
+  int occ;
+  if (cus > 0) {
+    occ = cus * nominal_per_cu(p.HG, (size_t)p.HG * kVtBytes);
+  } else {
+    DeviceInfo d;
+    rc = device_info(d);
+    if (rc) return rc;
+    cus = d.cus;
+    occ = d.grid[mode][p.HG];
+  }
+  *grid = grid_rule(occ, cus, p.HG, opt->waves_per_cu);
+  *waves_per_workgroup = p.HG;
   return RPA_OK;
 }
 

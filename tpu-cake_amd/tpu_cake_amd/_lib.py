@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "rpa_inkling_fused_decode",
     "rpa_inkling_workspace_size",
     "rpa_inkling_decode",
+    "rpa_attention_grid",
 )
 
 
@@ -162,6 +163,9 @@ def load() -> ctypes.CDLL:
         lib.rpa_inkling_fused_decode.argtypes = [ctypes.POINTER(RpaFusedShape), ctypes.c_float] + [vp] * 13 + [sz, vp]
         lib.rpa_inkling_workspace_size.restype = sz
         lib.rpa_inkling_workspace_size.argtypes = [ctypes.POINTER(RpaInklingShape)]
+        lib.rpa_attention_grid.restype = ctypes.c_int
+        lib.rpa_attention_grid.argtypes = [ctypes.POINTER(RpaShape), ctypes.POINTER(RpaOptions), ctypes.c_int32,
+                                           i32p, i32p]
         lib.rpa_inkling_decode.restype = ctypes.c_int
         lib.rpa_inkling_decode.argtypes = [ctypes.POINTER(RpaInklingShape), ctypes.c_float] + [vp] * 8 + [sz, vp]
         version = lib.rpa_abi_version()

@@ -178,27 +178,39 @@ class KernelExperiment(BaseModel):
     @computed_field
     @property
     def experiment_id(self) -> str:
-        """sha256 of the experiment's JSON without this field (sorted keys, compact)."""
-        encoded = json.dumps(_artifact_payload(self), sort_keys=True, separators=(",", ":")).encode()
-        return hashlib.sha256(encoded).hexdigest()
+        """sha256 of the experiment's JSON without this field (sorted keys, compact): the
+        reference's id (src/tpu_cake/contracts.py:214-224)."""
+        return _payload_id(_artifact_payload(self))
 
 
-def _artifact_payload(experiment: KernelExperiment) -> dict:
-    """The fields an artifact carries: a workload without an execution contract omits it, and a
-    profile expectation omits ``minimum_counter_device_planes`` while it holds its default 0 -- the
-    form of the reference's checked-in artifact (``contracts/inkling-rpa-experiment.json``), which
-    predates that field, so the ``inkling-rpa`` artifact and its id reproduce it exactly."""
+def _payload_id(payload: dict) -> str:
+    return hashlib.sha256(json.dumps(payload, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
+
+
+def _artifact_payload(experiment: KernelExperiment, *, checked_in_form: bool = False) -> dict:
+    """The fields an artifact carries: a workload without an execution contract omits it (the
+    reference's rule, src/tpu_cake/contracts.py:219-222).  ``checked_in_form``: also omit the
+    profile's ``minimum_counter_device_planes`` while it holds its default 0 -- the form of the
+    reference's checked-in ``contracts/inkling-rpa-experiment.json``, written before that field
+    existed (the reference's current code hashes the field, so its id for that row differs from
+    the one the checked-in file carries)."""
     payload = experiment.model_dump(mode="json", exclude={"experiment_id"})
     if payload["workload"]["execution"] is None:
         del payload["workload"]["execution"]
-    if payload["profile"].get("minimum_counter_device_planes") == 0:
+    if checked_in_form and payload["profile"].get("minimum_counter_device_planes") == 0:
         del payload["profile"]["minimum_counter_device_planes"]
     return payload
 
 
-def experiment_artifact_json(experiment: KernelExperiment, *, indent: int = 2) -> str:
-    """The artifact: the experiment's fields and its id, indented."""
-    return json.dumps(dict(_artifact_payload(experiment), experiment_id=experiment.experiment_id), indent=indent)
+def experiment_artifact_json(experiment: KernelExperiment, *, indent: int = 2, checked_in_form: bool = False) -> str:
+    """The artifact: the experiment's fields and its id, indented.  ``checked_in_form``: the form of
+    the reference's checked-in artifact, with the id computed over that form (see _artifact_payload)."""
+    payload = _artifact_payload(experiment, checked_in_form=checked_in_form)
+    return json.dumps(dict(payload, experiment_id=_payload_id(payload)), indent=indent)
+
+
+def artifact_id(experiment: KernelExperiment, *, checked_in_form: bool = False) -> str:
+    return _payload_id(_artifact_payload(experiment, checked_in_form=checked_in_form))
 
 
 # ----------------------------------------------------------------------------------- target
@@ -552,6 +564,10 @@ def main(argv=None) -> int:
         sp = sub.add_parser(cmd)
         sp.add_argument("workload", choices=sorted(ALL_WORKLOADS))
         sp.add_argument("--output", type=pathlib.Path)
+        if cmd == "experiment":
+            sp.add_argument("--checked-in-form", action="store_true",
+                            help="write the form of the reference's checked-in artifacts (no "
+                                 "minimum_counter_device_planes while it is 0), id over that form")
     args = ap.parse_args(argv)
     if args.cmd == "list-workloads":
         for name in ALL_WORKLOADS:
@@ -567,11 +583,12 @@ def main(argv=None) -> int:
             print(f"WORKLOAD_RENDERED workload={args.workload} path={args.output}")
         return 0
     exp = experiment(args.workload)
-    rendered = experiment_artifact_json(exp) + "\n"
+    rendered = experiment_artifact_json(exp, checked_in_form=args.checked_in_form) + "\n"
     if args.output is None:
         print(rendered, end="")
     else:
         args.output.parent.mkdir(parents=True, exist_ok=True)
         args.output.write_text(rendered)
-        print(f"EXPERIMENT_WRITTEN workload={args.workload} id={exp.experiment_id} path={args.output}")
+        print(f"EXPERIMENT_WRITTEN workload={args.workload} id={artifact_id(exp, checked_in_form=args.checked_in_form)} "
+              f"path={args.output}")
     return 0

@@ -483,5 +483,25 @@ def run_case(case, device="cuda", **kwargs) -> torch.Tensor:
                                   d["num_seqs"], sm_scale=case.sm_scale, kv_scales=kv_scales, **kwargs)
 
 
+def attention_grid(case, knobs: dict | None = None, cus: int = 0) -> tuple[int, int]:
+    """(workgroups, waves per workgroup) of the attention launch the library makes for a host
+    ``RpaCase`` with the schedule knobs ``knobs`` (``waves_per_cu`` / ``prefill_tiles`` /
+    ``prefill_cost``), on a device of ``cus`` compute units at the kernel's nominal occupancy, or
+    on the current GPU when ``cus`` is 0 (``rpa_attention_grid``)."""
+    k = tuned.validate_entry(dict(knobs or {}))
+    T, Hq, D = case.q.shape
+    P, S, C, _ = case.kv_pages.shape
+    n_max, pps = case.page_indices.shape
+    shape = _lib.RpaShape(T, Hq, C // 2, D, P, S, n_max, pps,
+                          _lib.RPA_KV_FP8_E4M3 if case.kv_dtype == "fp8" else _lib.RPA_KV_BF16)
+    opts = _lib.RpaOptions(sm_scale=float(case.sm_scale), waves_per_cu=int(k["waves_per_cu"]),
+                           prefill_tiles=int(k["prefill_tiles"]), prefill_cost=float(k["prefill_cost"]))
+    grid, waves = ctypes.c_int32(0), ctypes.c_int32(0)
+    lib = _lib.load()
+    _lib.check(lib.rpa_attention_grid(ctypes.byref(shape), ctypes.byref(opts), int(cus), ctypes.byref(grid),
+                                      ctypes.byref(waves)))
+    return grid.value, waves.value
+
+
 def default_sm_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)

@@ -325,11 +325,38 @@ def load_output(run_root: pathlib.Path) -> np.ndarray:
 
 
 # --------------------------------------------------------------------------- the search
-def run_search(root, contract: SearchContract, *, runner, checker, case=None, keep_outputs: bool = False) -> dict:
+def refuse_noop_candidates(contract: SearchContract, case, grid_of) -> None:
+    """Refuse a candidate that differs from the baseline only in ``waves_per_cu`` and resolves to
+    the baseline's launch (``grid_of(case, knobs) -> (workgroups, waves per workgroup)``, the
+    library's ``rpa_attention_grid``): timing it against the baseline would compare identical
+    launches."""
+    base = contract.knobs(contract.baseline)
+    base_grid = None
+    for name in contract.names:
+        k = contract.knobs(name)
+        if name == contract.baseline or {**k, "waves_per_cu": base["waves_per_cu"]} != base:
+            continue
+        base_grid = base_grid or grid_of(case, base)
+        g = grid_of(case, k)
+        if g == base_grid:
+            raise ValueError(f"RPA_SEARCH_NOOP_CANDIDATE candidate={name}: waves_per_cu={k['waves_per_cu']} "
+                             f"resolves to the baseline's launch ({g[0]} workgroups of {g[1]} waves)")
+
+
+def _device_grid(case, knobs) -> tuple:
+    from . import ops
+
+    return ops.attention_grid(case, knobs, cus=0)
+
+
+def run_search(root, contract: SearchContract, *, runner, checker, case=None, keep_outputs: bool = False,
+               grid_of=_device_grid) -> dict:
     """Run (or resume) a search; ``checker(case, output_f32) -> {"passed": bool, ...}`` is the
     correctness gate (``case`` defaults to the configuration's workload, built once here).  A gate
     run's output is deleted once its verdict is written (its sha256 stays in ``steps.json``) unless
-    ``keep_outputs``.  Writes ``result.json`` under ``root`` and returns it."""
+    ``keep_outputs``.  Candidates that resolve to the baseline's launch are refused first
+    (``refuse_noop_candidates``; ``grid_of`` None skips that).  Writes ``result.json`` under
+    ``root`` and returns it."""
     root = pathlib.Path(root).resolve()
     root.mkdir(parents=True, exist_ok=True)
     cpath = root / "contract.json"
@@ -389,6 +416,8 @@ def run_search(root, contract: SearchContract, *, runner, checker, case=None, ke
         from .workloads import make_config
 
         case = make_config(contract.config, seed=contract.seed)
+    if grid_of is not None:
+        refuse_noop_candidates(contract, case, grid_of)
     case_sha = hashlib.sha256(case.q.tobytes() + case.kv_pages.tobytes() + case.kv_lens.tobytes()
                               + case.page_indices.tobytes()).hexdigest()
     for pos, name in enumerate(contract.names):
