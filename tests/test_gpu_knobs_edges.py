@@ -251,3 +251,27 @@ def test_metadata_on_the_host_is_rejected_after_a_cached_call(cuda):
     with pytest.raises(ValueError, match="kv_lens must be on a GPU"):
         _run(bad, case)
     _assert_close(_run(d, case), _ref(case), "after the refusal")
+
+
+# ------------------------------------------------------------------------------------- layouts
+def test_split_co_tiles_then_prefill_kernel_then_co(cuda):
+    """The co-resident layout splitting long tiles (a 17-token chunk over 4000 prior keys, priors
+    that make 30-chunk tiles), then the prefill kernel on the same workspace, then the co layout
+    again: each layout's merge descriptors stay apart (fields one leaves behind never read as the
+    other's flags), every call within 2e-2 of the oracle."""
+    case = make_custom(kv_lens=[1000, 1300, 45, 4017, 2200], q_lens=[1, 300, 1, 17, 64], num_q_heads=32,
+                       num_kv_heads=8, page_size=64, seed=808)
+    d = ops.case_to_device(case, "cuda")
+    ref = _ref(case)
+    _say("co-resident layout, split tiles")
+    _assert_close(_run(d, case), ref, "co")
+    _say("prefill kernel on the same workspace")
+    _assert_close(_run(d, case, prefill_tiles=1), ref, "prefill kernel")
+    _say("one 8-wave workgroup per CU")
+    _assert_close(_run(d, case, prefill_tiles=3), ref, "8-wave tiles")
+    _say("co-resident layout again")
+    _assert_close(_run(d, case), ref, "co again")
+    g3 = make_custom(kv_lens=[1000, 300, 45, 2500], q_lens=[1, 300, 1, 17], num_q_heads=21, num_kv_heads=3,
+                     page_size=64, seed=213)
+    _say("G=7 (prefill kernel) after the co layout's splits")
+    _assert_close(_run(ops.case_to_device(g3, "cuda"), g3), _ref(g3), "G=7 after co")

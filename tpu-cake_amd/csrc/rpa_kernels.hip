@@ -151,10 +151,22 @@ struct Params {
   // share a CU); the prefill tiles are 128 rows, one prefill workgroup beside one stream-K
   // workgroup on a CU, and stream-K workgroups join the tile queue when their range is done
   int co;
+  int co_split_max;            // split co tiles the workspace holds
+  struct CoDesc* co_desc;      // [co_split_max]
   int pk_grid;                 // prefill-kernel workgroups
   float* pk_acc;               // [2 * pk_grid][256][kD] split-tile partials
   float* pk_ml;                // [2 * pk_grid][256][2]
   struct PkDesc* pk_desc;      // [pk_grid] split tile ending in prefill workgroup b
+};
+
+// A co-resident prefill tile split into nparts chunk ranges: its partials are in slots slot0 ..
+// slot0 + nparts - 1 of [slot][128 rows][kD] (acc) and [slot][128 rows][2] (m, l) over the
+// prefill-kernel partial areas (unused in that layout); the combine merges them.  Descriptors live
+// in an area of their own: fields left by one layout must never read as another's flags.
+struct CoDesc {
+  int valid[4];  // one per 32-row group; the combine workgroup of that group clears it
+  int q_row0;    // first query token of the tile
+  int ntok, h, nparts, slot0, pad[3];
 };
 
 // A prefill tile split across prefill-kernel workgroups b0..b (b = the owner of its last chunk).
@@ -1977,8 +1989,9 @@ __device__ __forceinline__ void co_step(const Params& p, const PfTile& tl, const
   co_pv<PLAIN>(p, tl, c, buf, sc, st, n, j);
 }
 
+// slot >= 0: the tile is one part of a split tile, its (m, l, acc) go to that partial slot
 __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const CoLane& cln, uint8_t* lds, int wv,
-                                        int lane, int n, int j, int& err) {
+                                        int lane, int n, int j, int& err, int slot) {
   PfRow st[2];
   bf16x8 q[2][4];
 #pragma unroll
@@ -2031,6 +2044,20 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
     co_drain();  // the clamped DMAs past the segment land before the slots are reused
   }
 
+  if (slot >= 0) {  // a part of a split tile: its unnormalised state, (m, l) in log2 units
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const float lt = rows4_sum(st[rb].l);
+      if (!st[rb].ok) continue;
+      const int r = 32 * wv + 16 * rb + n;
+      float* ml = p.pk_ml + ((size_t)slot * 128 + r) * 2;
+      if (j == 0) *(f32x2*)ml = f32x2{st[rb].m, lt};
+      float* acc = p.pk_acc + ((size_t)slot * 128 + r) * kD + 4 * j;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) *(f32x4*)(acc + 16 * d) = st[rb].acc[d];
+    }
+    return;
+  }
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const float lt = rows4_sum(st[rb].l);
@@ -2100,59 +2127,147 @@ __device__ __forceinline__ PfTile co_tile_of(const Params& p, const SeqInfo wsi[
   return tl;
 }
 
-// The co-resident layout's prefill role: take tiles from the queue until it runs dry.  The queue
-// hands out tiles longest first (as pf_role): the workgroup writes the chunk count of every pair
-// (one lane per sequence), ranks the pairs in LDS and maps queue position r to the pair of rank
-// r / Hkv, kv head r % Hkv.  Calls with more pairs than kPfOrderMax keep the queue order.
-__device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, int total, uint8_t* lds,
-                                        int* s_tile, int lane, int wv, int n, int j, int& err) {
+// Splitting: a call whose tiles are fewer than the grid's workgroups (the queue cannot keep them
+// all busy) cuts every tile longer than kCoMinSplit chunks into up to np equal chunk ranges
+// (units), np = min(kCoMaxParts, grid / tiles), each unit's partial merged by the combine kernel.
+// Unit u = pair * np + part; parts past a short tile's own count are empty.  Units are ranked
+// longest first by a 32-bit key: chunk count (15 bits) over the unit index (16 bits).
+constexpr int kCoMaxParts = 4;
+constexpr int kCoMinSplit = 16;  // tiles of up to this many chunks (512 keys) are never split
+
+// Chunk count of pair k (0 = the last token block) of a sequence with nt token blocks.
+__device__ __forceinline__ int co_pair_size(const Params& p, int kv_len, int q_len, int nt, int k) {
+  PfTile t;
+  t.kv_len = kv_len;
+  t.q_len = q_len;
+  t.tok0 = (nt - 1 - k) * p.pf_tq;
+  t.ntok = q_len - t.tok0 < p.pf_tq ? q_len - t.tok0 : p.pf_tq;
+  pf_tile_chunks(p, t);
+  return t.c_hi > t.c_lo ? t.c_hi - t.c_lo : 0;
+}
+
+// Parts of a tile of sz chunks when the call splits into np.
+__device__ __forceinline__ int co_tile_parts(int sz, int np) {
+  if (np <= 1 || sz <= kCoMinSplit) return 1;
+  const int k = (sz + kCoMinSplit - 1) / kCoMinSplit;  // parts of at least kCoMinSplit chunks
+  return k < np ? k : np;
+}
+
+// The co-resident layout's prefill role: take units from the queue until it runs dry.  The
+// workgroup writes every unit's key (one thread per unit: a binary search over the sequences'
+// first pairs finds its sequence), ranks them in LDS and maps queue position r to the unit of rank
+// r / Hkv, kv head r % Hkv.  Calls with more units than kPfOrderMax keep the pair order unsplit.
+__device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, uint8_t* lds, int* s_tile,
+                                        int lane, int wv, int n, int j, int& err) {
   const CoPairs cp = co_pairs(p, wsi, pf_min, lane);
   const int npairs = cp.base[4];
-  const bool ranked = npairs <= kPfOrderMax;
-  int* psz = (int*)(lds + kCoOrderBase);
-  int* pord = psz + kPfOrderMax;
+  int np = 1;
+  if (npairs * p.Hkv < p.grid && npairs * p.Hkv <= p.co_split_max) {
+    np = p.grid / (npairs * p.Hkv);
+    np = np < kCoMaxParts ? np : kCoMaxParts;
+    if (npairs * np > kPfOrderMax) np = kPfOrderMax / npairs;
+    np = np < 1 ? 1 : np;
+  }
+  const int nunits = npairs * np;
+  const bool ranked = nunits <= kPfOrderMax;
+  int nvalid = nunits;
+  int* pkey = (int*)(lds + kCoOrderBase);
+  int* pord = pkey + kPfOrderMax;
   const CoLane cln = co_lane(wv, lane);
   if (ranked) {
+    // per sequence (256 entries each, over pord's area and the page table until they are
+    // written): its first pair (the exclusive scan of the pair counts: never decreasing, and a
+    // sequence with no pairs shares its successor's), kv_len, q_len
+    int* sq_off = pord;
+    int* sq_kv = pord + 256;
+    int* sq_ql = (int*)(lds + kCoPageBase);
+    static_assert(kCoPages >= 256, "sequence table");
     if (wv == 0) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        PfTile t;
-        t.kv_len = wsi[w].kv_len;
-        t.q_len = wsi[w].q_len;
-        for (int k = 0; k < cp.nt[w]; ++k) {
-          t.tok0 = (cp.nt[w] - 1 - k) * p.pf_tq;
-          t.ntok = t.q_len - t.tok0 < p.pf_tq ? t.q_len - t.tok0 : p.pf_tq;
-          pf_tile_chunks(p, t);
-          psz[cp.base[w] + cp.off[w] + k] = t.c_hi > t.c_lo ? t.c_hi - t.c_lo : 0;
-        }
+        const int i = 64 * w + lane;
+        sq_off[i] = cp.base[w] + cp.off[w];
+        sq_kv[i] = wsi[w].kv_len;
+        sq_ql[i] = wsi[w].q_len;
       }
-      for (int i = npairs + lane; i < (npairs + 3) / 4 * 4; i += 64) psz[i] = -1;  // pad to whole int4s
     }
     __syncthreads();
-    const int n4 = (npairs + 3) / 4;
-    for (int i = threadIdx.x; i < npairs; i += blockDim.x) {
-      const int si = psz[i];
+    for (int u = threadIdx.x; u < nunits; u += blockDim.x) {
+      const int pair = u / np, part = u - pair * np;
+      int seq = 0;  // the last sequence whose first pair is <= pair (sq_off[0] = 0)
+#pragma unroll
+      for (int step = 128; step > 0; step >>= 1)
+        if (sq_off[seq + step] <= pair) seq += step;
+      const int k = pair - sq_off[seq], q_len = sq_ql[seq];
+      const int nt = (q_len + p.pf_tq - 1) / p.pf_tq;
+      const int sz = co_pair_size(p, sq_kv[seq], q_len, nt, k);
+      const int parts = co_tile_parts(sz, np);
+      int psz = part < parts ? (sz * (part + 1)) / parts - (sz * part) / parts : -1;
+      psz = psz < 0x7fff ? psz : 0x7fff;  // keys stay positive
+      pkey[u] = psz < 0 ? -1 : (psz << 16) | u;
+    }
+    __syncthreads();
+    const int n4 = (nunits + 3) / 4;
+    if (wv == 0) {
+      for (int i = nunits + lane; i < n4 * 4; i += 64) pkey[i] = -1;  // pad to whole int4s
+      int cnt = 0;  // units with a key (empty parts have none)
+      for (int i = lane; i < nunits; i += 64) cnt += pkey[i] >= 0;
+      cnt = wave_sum32(cnt);
+      if (lane == 0) *s_tile = cnt;
+    }
+    __syncthreads();
+    nvalid = uni(*s_tile);
+    // the ranks of the units with a key are 0 .. nvalid-1 (keys are distinct)
+    for (int i = threadIdx.x; i < nunits; i += blockDim.x) {
+      const int ki = pkey[i];
+      if (ki < 0) continue;
       int r = 0;
       for (int k4 = 0; k4 < n4; ++k4) {
-        const int4 v = ((const int4*)psz)[k4];
-        const int k = 4 * k4;
-        r += (v.x > si || (v.x == si && k < i)) + (v.y > si || (v.y == si && k + 1 < i)) +
-             (v.z > si || (v.z == si && k + 2 < i)) + (v.w > si || (v.w == si && k + 3 < i));
+        const int4 v = ((const int4*)pkey)[k4];
+        r += (v.x > ki) + (v.y > ki) + (v.z > ki) + (v.w > ki);
       }
       pord[r] = i;
     }
     __syncthreads();
   }
+  const int total = (ranked ? nvalid : npairs) * p.Hkv;
   for (;;) {
     if (threadIdx.x == 0) *s_tile = atomicAdd(p.err + kQueueWord, 1);
     __syncthreads();
     const int tq = uni(*s_tile);
     __syncthreads();
     if (tq >= total) break;
-    const int pi = ranked ? uni(pord[tq / p.Hkv]) : tq / p.Hkv;
-    const PfTile tl = co_tile_of(p, wsi, cp, pi, tq % p.Hkv);
+    const int h = tq % p.Hkv;
+    int pair = tq / p.Hkv, part = 0, unit_np = 1;
+    if (ranked) {
+      const int u = uni(pord[tq / p.Hkv]);
+      pair = u / np;
+      part = u - pair * np;
+      unit_np = np;
+    }
+    PfTile tl = co_tile_of(p, wsi, cp, pair, h);
     if (tl.seq < 0 || tl.c_hi <= tl.c_lo) continue;
-    co_tile(p, tl, cln, lds, wv, lane, n, j, err);
+    int slot = -1;
+    const int parts = co_tile_parts(tl.c_hi - tl.c_lo, unit_np);
+    if (parts > 1) {
+      const int sz = tl.c_hi - tl.c_lo, c0 = tl.c_lo;
+      tl.c_lo = c0 + (sz * part) / parts;
+      tl.c_hi = c0 + (sz * (part + 1)) / parts;
+      const int st = pair * p.Hkv + h;  // split tile (npairs * Hkv <= co_split_max)
+      slot = st * kCoMaxParts + part;
+      if (part == 0 && threadIdx.x < 4) {  // its merge descriptor (read by the combine launch)
+        CoDesc* d = p.co_desc + st;
+        if (threadIdx.x == 0) {
+          d->q_row0 = tl.q_start + tl.tok0;
+          d->ntok = tl.ntok;
+          d->h = h;
+          d->nparts = parts;
+          d->slot0 = st * kCoMaxParts;
+        }
+        d->valid[threadIdx.x] = 1;
+      }
+    }
+    co_tile(p, tl, cln, lds, wv, lane, n, j, err, slot);
   }
 }
 
@@ -2282,7 +2397,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int gd = p.grid - gpre;  // stream-K workgroup count
   if (MODE == KV_BF16 && pf_first) {
     if (UPG && p.co)
-      co_role(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+      co_role(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
     else  // (HG == 8: one K and one V piece per thread per chunk)
       pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
@@ -2380,7 +2495,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   if (MODE == KV_BF16 && UPG && p.co && !pf_first && pf_total > 0) {
     __syncthreads();  // every wave is done with its stream-K LDS regions
-    co_role(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
+    co_role(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
   }
 
   {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
@@ -3109,6 +3224,53 @@ __device__ __forceinline__ void fused_store_token(const Params& p, int s) {
   }
 }
 
+// Co-resident split tile merge: workgroup idx merges rows 32 g .. 32 g + 31 (g = idx % 4) of split
+// tile idx / 4 from its nparts partial slots: thread t takes row 32 g + t / 8, dims 16 (t % 8) ..
+// +15, folds the parts in order with the online log-sum-exp update and writes bf16.
+__device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
+  const int st = idx >> 2, g = idx & 3;
+  if (st >= p.co_split_max) return;
+  CoDesc* dp = p.co_desc + st;
+  int valid = dp->valid[g];
+  CoDesc d = *dp;
+  asm volatile("" : "+v"(valid), "+v"(d.q_row0), "+v"(d.ntok), "+v"(d.h), "+v"(d.nparts), "+v"(d.slot0));
+  if (!__builtin_amdgcn_readfirstlane(valid)) return;
+  const int t = threadIdx.x, row = 32 * g + (t >> 3), c16 = 16 * (t & 7);
+  const int nparts = __builtin_amdgcn_readfirstlane(d.nparts);
+  if (row < d.ntok * p.G) {
+    f32x4 o[4];
+    float m = -INFINITY, l = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nparts && k < kCoMaxParts; ++k) {
+      const size_t slot = (size_t)d.slot0 + k;
+      const f32x2 ml = *(const f32x2*)(p.pk_ml + (slot * 128 + row) * 2);
+      const float* acc = p.pk_acc + (slot * 128 + row) * kD + c16;
+      const float mn = fmaxf(m, ml[0]), mu = mn == -INFINITY ? 0.f : mn;
+      const float sa = __builtin_amdgcn_exp2f(m - mu), sb = __builtin_amdgcn_exp2f(ml[0] - mu);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = o[e] * sa + *(const f32x4*)(acc + 4 * e) * sb;
+      l = l * sa + ml[1] * sb;
+      m = mn;
+    }
+    const float inv = 1.f / l;
+    const int tok = row / p.G, head = d.h * p.G + (row - tok * p.G);
+    uint16_t* op = p.out + ((size_t)(d.q_row0 + tok) * p.Hq + head) * kD + c16;
+    u32x4 w0, w1;
+    w0[0] = pack_bf16x2(o[0][0] * inv, o[0][1] * inv);
+    w0[1] = pack_bf16x2(o[0][2] * inv, o[0][3] * inv);
+    w0[2] = pack_bf16x2(o[1][0] * inv, o[1][1] * inv);
+    w0[3] = pack_bf16x2(o[1][2] * inv, o[1][3] * inv);
+    w1[0] = pack_bf16x2(o[2][0] * inv, o[2][1] * inv);
+    w1[1] = pack_bf16x2(o[2][2] * inv, o[2][3] * inv);
+    w1[2] = pack_bf16x2(o[3][0] * inv, o[3][1] * inv);
+    w1[3] = pack_bf16x2(o[3][2] * inv, o[3][3] * inv);
+    *(u32x4*)op = w0;
+    *(u32x4*)(op + 8) = w1;
+  }
+  if (t == 0) dp->valid[g] = 0;
+}
+
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
   __shared__ float red[3][64][33];    // waves 1..3's o (33: conflict-free row stride)
   __shared__ float redml[3][64][16];  // waves 1..3's (m, l) per row slot
@@ -3119,6 +3281,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
       combine_heavy(p, hb, red, redml);
     else if (p.fused)
       fused_store_token(p, hb - nheavy);
+    else if (p.co)
+      combine_co_split(p, hb - nheavy);
     else
       combine_prefill(p, hb - nheavy, red, redml);
     return;
@@ -3282,11 +3446,12 @@ int device_info(DeviceInfo& out) {
 }
 
 // Workspace: [error word | pad to 256] [split descriptors, one per workgroup] [heavy-merge helper
-// flags and descriptors] [prefill split descriptors] [partial m,l] [partial acc] [prefill partial
-// m,l] [prefill partial acc].  Header, descriptors and flags are zeroed once (rpa_workspace_init);
+// flags and descriptors] [prefill split descriptors] [split co tile descriptors] [partial m,l]
+// [partial acc] [prefill partial m,l] [prefill partial acc] (the last two also hold the partials of
+// split co tiles, whose layout never runs the prefill kernel).  Header, descriptors and flags are zeroed once (rpa_workspace_init);
 // every call leaves each descriptor invalid and each flag clear again when its combine has run.
 struct WsLayout {
-  size_t desc, heavy, heavy_desc, pk_desc, ml, acc, pk_ml, pk_acc, total;
+  size_t desc, heavy, heavy_desc, pk_desc, co_desc, ml, acc, pk_ml, pk_acc, total;
 };
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
@@ -3299,7 +3464,8 @@ WsLayout ws_layout(const DeviceInfo& d) {
   w.heavy_desc = w.heavy + round256((size_t)heavy_slots((int)gmax) * 8 * kHeavySlices * sizeof(int32_t));
   w.pk_desc = w.heavy_desc + round256((size_t)heavy_slots((int)gmax) * sizeof(SplitDesc));
   const size_t pk = (size_t)d.cus;  // prefill-kernel workgroups: one per CU
-  w.ml = w.pk_desc + round256(pk * sizeof(PkDesc));
+  w.co_desc = w.pk_desc + round256(pk * sizeof(PkDesc));  // split co tiles: one per CU
+  w.ml = w.co_desc + round256((size_t)d.cus * sizeof(CoDesc));
   w.acc = w.ml + round256(2 * gmax * ROW_BLOCK * 2 * sizeof(float));
   w.pk_ml = w.acc + round256(2 * gmax * ROW_BLOCK * kD * sizeof(float));
   w.pk_acc = w.pk_ml + round256(2 * pk * kPkRows * 2 * sizeof(float));
@@ -3923,6 +4089,13 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   resolve_layout(p, mode, shape, opt);
   p.grid = grid_for_call(d, mode, p.HG, opt->waves_per_cu);
   if (p.pf_kernel) p.pk_grid = d.cus;
+  // split co tiles: descriptors over the prefill-kernel descriptor area (one PkDesc per CU), partial
+  // slots of 128 rows over its partial areas (2 x 256 rows per CU)
+  static_assert(kCoMaxParts * 128 <= 2 * kPkRows, "co split tiles exceed the prefill-kernel partial areas");
+  if (p.co) {
+    p.co_split_max = d.cus;
+    p.co_desc = (CoDesc*)((uint8_t*)workspace + w.co_desc);
+  }
   hipStream_t st = (hipStream_t)stream;
   if (ev_begin && hipEventRecord((hipEvent_t)ev_begin, st) != hipSuccess)
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");
@@ -3961,7 +4134,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   // prefill workgroup
   hipLaunchKernelGGL(rpa_combine_kernel,
                      dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0) +
-                          (p.fused ? p.fused_nseq : 0)),
+                          (p.fused ? p.fused_nseq : 0) + (p.co ? 4 * p.co_split_max : 0)),
                      dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) {
