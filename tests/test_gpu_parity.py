@@ -124,15 +124,21 @@ def test_chunked_prefill_and_decode_mixed(cuda):
     _check(case)
 
 
-@pytest.mark.parametrize("mode", ["fp8", "scaled"])
-def test_chunked_prefill_without_tiles(cuda, mode):
-    # fp8 KV and scalar K/V scales take no prefill tiles: their long query chunks run as causal
-    # 16-row blocks through the stream-K role
-    _say(f"chunked prefill through stream-K, {mode}")
-    case = make_custom(kv_lens=[700, 45, 1030, 9], q_lens=[1, 45, 130, 1], num_q_heads=32, num_kv_heads=8,
-                       page_size=64, seed=53, kv_dtype="fp8" if mode == "fp8" else "bf16")
-    kw = dict(k_scale=0.75, v_scale=1.25) if mode == "scaled" else {}
-    _check(case, gpu_kw=kw, oracle_kw=kw)
+@pytest.mark.parametrize("mode", ["fp8", "scaled", "fp8-scalar", "mask"])
+@pytest.mark.parametrize("tiles", [0, -1])
+def test_chunked_prefill_fp8_scaled_mask(cuda, mode, tiles):
+    # fp8 KV (per-(page, head) scales, or scalar k_scale / v_scale instead), scalar K/V scales on
+    # bf16 KV and a finite mask value: the long query chunks run as co-resident MFMA tiles (the
+    # chunk converted one step ahead; a finite mask visits every key) or, prefill_tiles=-1, as
+    # causal 16-row blocks through the stream-K role
+    _say(f"chunked prefill, {mode}, prefill_tiles={tiles}")
+    case = make_custom(kv_lens=[700, 45, 1030, 9, 2100], q_lens=[1, 45, 130, 1, 300], num_q_heads=32,
+                       num_kv_heads=8, page_size=64, seed=53, kv_dtype="fp8" if mode.startswith("fp8") else "bf16")
+    if mode == "fp8-scalar":  # the codes span +-448; scalars of that size bring K and V back to unit scale
+        case.kv_scales = None
+    kw = {"scaled": dict(k_scale=0.75, v_scale=1.25), "fp8-scalar": dict(k_scale=1.0 / 128, v_scale=1.0 / 112),
+          "mask": dict(mask_value=-2.5)}.get(mode, {})
+    _check(case, gpu_kw=dict(kw, prefill_tiles=tiles), oracle_kw=kw)
 
 
 def test_padding_rows_and_seqs(cuda):

@@ -1702,13 +1702,18 @@ __device__ __forceinline__ void pf_tile(const Params& p, const PfTile& tl, uint8
 // The prefill role of a workgroup: take tiles from the queue until it runs dry.  wsi: the four
 // metadata windows (nseq <= 256), total: the call's tile count.
 // The chunks a tile visits, from its sequence's kv_len / q_len and its tokens tok0 .. tok0+ntok-1:
-// up to the causal limit of its last row, from the sliding-window start of its first row.
+// up to the causal limit of its last row, from the sliding-window start of its first row (with a
+// finite mask value, where masked keys keep a weight: all of them).
 // c_hi <= c_lo: no key to visit (q_len > kv_len: rows left unwritten).
 __device__ __forceinline__ void pf_tile_chunks(const Params& p, PfTile& tl) {
   tl.c_lo = tl.c_hi = 0;
   const int prior = tl.kv_len - tl.q_len;
   const int pos_hi = prior + tl.tok0 + tl.ntok - 1;  // last key any row of the tile sees
   if (pos_hi < 0) return;
+  if (!p.skip_masked) {  // a finite mask value: masked keys keep a weight, so every key is visited
+    tl.c_hi = (tl.kv_len + KV_CHUNK - 1) / KV_CHUNK;
+    return;
+  }
   int lo = 0;
   if (p.sliding_window > 0) {
     lo = prior + tl.tok0 - p.sliding_window + 1;  // keys below are masked for every row
@@ -1823,22 +1828,47 @@ __device__ __forceinline__ void pf_role(const Params& p, const SeqInfo wsi[4], i
 // the DMA makes it wait for every DMA in flight before each LDS read it cannot tell apart,
 // draining the ring every step.)  No load in asm writes a register: a register the compiler
 // believed loaded could be reused before the load lands.
+//
+// Scaled bf16 and fp8 pools (the reference dequantises K and V as bf16(float(x) * scale),
+// ragged_paged_attention.py:124-129) add one pass per chunk, one step ahead of its compute, so the
+// step keeps one barrier: scaled bf16 chunks are scaled in place in their ring slot; fp8 chunks
+// (half the bytes) land in a ring of four 8 KiB code slots and are converted into a double buffer
+// of bf16 slots of the layout above, with the page's K and V scales (per (page, kv head), from a
+// table loaded with the page ids).
 constexpr int kCoWaves = 4;
 constexpr int kCoSlot = 16384;                    // one chunk: K (8 KiB) + V (8 KiB)
 constexpr int kCoSlots = 4;
+constexpr int kCoCodeSlot = 8192;                 // one fp8 chunk: K codes (4 KiB) + V codes (4 KiB)
 constexpr int kCoOrderBase = kCoSlots * kCoSlot;  // tile order tables (2 x kPfOrderMax ints)
-constexpr int kCoPages = 256;                     // page-id table entries
+constexpr int kCoPages = 128;                     // page-id table entries (and fp8 scale pairs)
 constexpr int kCoPageBase = kCoOrderBase + 2 * kPfOrderMax * 4;
-static_assert(kCoPageBase + kCoPages * 4 <= kCoWaves * kWaveLds,
+constexpr int kCoScaleBase = kCoPageBase + kCoPages * 4;
+static_assert(kCoScaleBase + kCoPages * 8 <= kCoWaves * kWaveLds,
               "co-resident prefill LDS exceeds the workgroup's allocation");
-constexpr int kCoDmas = 4;  // per wave and chunk: two K and two V DMAs
+static_assert(kCoSlots * kCoCodeSlot + 2 * kCoSlot <= kCoOrderBase, "fp8 code ring and bf16 buffers");
 
-// The step's barrier: this wave's DMAs of the chunk about to be read have landed (the two younger
-// chunks' may still be in flight), its LDS reads are done, then s_barrier.  A workgroup-scope
-// release fence (__syncthreads) would wait for every DMA in flight.
+// Modes with co-resident prefill tiles.
+template <int MODE>
+constexpr bool co_tiles() {
+  return MODE == KV_BF16 || MODE == KV_BF16_SCALED || MODE == KV_FP8;
+}
+template <int MODE>
+constexpr int co_dmas() {  // DMA instructions per wave and chunk
+  return MODE == KV_FP8 ? 2 : 4;
+}
+template <int MODE>
+constexpr bool co_converts() {  // a pass per chunk one step ahead (scaled or fp8)
+  return MODE != KV_BF16;
+}
+
+// The step's barrier: this wave's DMAs of the chunk the step reads first (chunk c, or c + 1 for the
+// modes that convert one step ahead) have landed -- N younger DMAs may still be in flight -- and
+// its LDS reads are done, then s_barrier.  A workgroup-scope release fence (__syncthreads) would
+// wait for every DMA in flight.
+template <int N>
 __device__ __forceinline__ void co_barrier() {
-  static_assert(2 * kCoDmas == 8, "co_barrier's vmcnt");
-  asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  static_assert(N >= 0 && N < 16, "co_barrier's vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
 // Every DMA of this wave has landed.
@@ -1864,17 +1894,25 @@ __device__ __forceinline__ void co_dma(const void* src, uint32_t lds_addr) {
       : "memory");
 }
 
-// Per-lane parts of the DMA addresses, the same for every chunk: lane l of wave wv carries, for
-// t = 0, 1, key 4i + l/16 of block i = wv + 4t, and 16-byte LDS position l % 16 of that key's K row
-// (column group pos ^ (key % 16)) and V row (dims of 32-byte block (pos/2) ^ (key % 8), half pos % 2).
+// Per-lane parts of the DMA addresses, the same for every chunk.  bf16: lane l of wave wv carries,
+// for t = 0, 1, key 4i + l/16 of block i = wv + 4t, and 16-byte LDS position l % 16 of that key's K
+// row (column group pos ^ (key % 16)) and V row (dims of 32-byte block (pos/2) ^ (key % 8), half
+// pos % 2).  fp8 (key[0], colk[0]): key 8 wv + l/8, bytes 16 (l % 8) .. +15 of its 128-byte row.
 struct CoLane {
   int key[2];   // key within the chunk
   int colk[2];  // element offset of the K piece within the key's row of kv head h
   int colv[2];  // element offset of the V piece
 };
 
+template <int MODE>
 __device__ __forceinline__ CoLane co_lane(int wv, int lane) {
   CoLane c;
+  if constexpr (MODE == KV_FP8) {
+    c.key[0] = c.key[1] = 8 * wv + (lane >> 3);
+    c.colk[0] = c.colk[1] = 16 * (lane & 7);
+    c.colv[0] = c.colv[1] = kD + 16 * (lane & 7);
+    return c;
+  }
   const int pos = lane & 15;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -1893,9 +1931,11 @@ struct CoSeg {
   int cps;         // chunks per page (page_size / 32)
 };
 
-// This wave's share of chunk c into LDS slot dst (wave-uniform LDS address): K blocks wv and
-// wv + 4 (keys 4i .. 4i+3 each, 1 KiB per DMA) and the same V blocks.  Keys past kv_len read key
-// kv_len - 1 (scores -inf; V meets P = 0).
+// This wave's share of chunk c into LDS at dst (wave-uniform LDS address).  bf16: K blocks wv and
+// wv + 4 (keys 4i .. 4i+3 each, 1 KiB per DMA) and the same V blocks into a 16 KiB slot; fp8: K
+// codes of keys 8 wv .. 8 wv + 7 (1 KiB) and their V codes into an 8 KiB code slot.  Keys past
+// kv_len read key kv_len - 1 (scores -inf; V meets P = 0).
+template <int MODE>
 __device__ __forceinline__ void co_issue(const Params& p, const PfTile& tl, const CoLane& cl, const CoSeg& sg,
                                          const int* ptab, int c, uint32_t dst, int wv, int& err) {
   int pg = uni(ptab[c / sg.cps - sg.p_lo]);
@@ -1903,8 +1943,15 @@ __device__ __forceinline__ void co_issue(const Params& p, const PfTile& tl, cons
     err |= ERR_PAGE;
     pg = 0;
   }
-  const uint16_t* base = (const uint16_t*)p.kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h);
   const int kmax = tl.kv_len - 1 - c * KV_CHUNK, stride = 2 * p.Hkv * kD;
+  if constexpr (MODE == KV_FP8) {
+    const uint8_t* base = p.kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h);
+    const uint8_t* row = base + (unsigned)((cl.key[0] < kmax ? cl.key[0] : kmax) * stride);
+    co_dma(row + cl.colk[0], dst + 1024u * wv);
+    co_dma(row + cl.colv[0], dst + 4096u + 1024u * wv);
+    return;
+  }
+  const uint16_t* base = (const uint16_t*)p.kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const uint32_t i = (uint32_t)(wv + kCoWaves * t);
@@ -1912,6 +1959,47 @@ __device__ __forceinline__ void co_issue(const Params& p, const PfTile& tl, cons
     co_dma(row + cl.colk[t], dst + 1024u * i);
     co_dma(row + cl.colv[t], dst + 8192u + 1024u * i);
   }
+}
+
+// The pass one step ahead: chunk c's data at src becomes the bf16 slot dst.  Scaled bf16: in place
+// (src == dst), every element times its scale, rounded to bf16 (the layout does not matter);
+// fp8: thread t converts key t / 8, dims 16 (t % 8) .. +15 of K and V with the page's scales into
+// the slot layout (K groups at group ^ (key % 16), V blocks at block ^ (key % 8)).
+template <int MODE>
+__device__ __forceinline__ void co_convert(const Params& p, const CoSeg& sg, const float* scl, int c, const uint8_t* src,
+                                           uint8_t* dst) {
+  const int t = threadIdx.x;
+  if constexpr (MODE == KV_BF16_SCALED) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      u32x4* w = (u32x4*)(dst + 8192 * h + 32 * t);
+      const float sc = h ? p.v_scale : p.k_scale;
+      const u32x4 a = w[0], b = w[1];
+      w[0] = scale_bf16x8(a, sc);
+      w[1] = scale_bf16x8(b, sc);
+    }
+  } else if constexpr (MODE == KV_FP8) {
+    const int key = t >> 3, g = t & 7, e = 2 * (c / sg.cps - sg.p_lo);
+    const float ks = scl[e], vs = scl[e + 1];
+    const u32x4 kc = *(const u32x4*)(src + key * 128 + 16 * g);
+    const u32x4 vc = *(const u32x4*)(src + 4096 + key * 128 + 16 * g);
+    uint8_t* krow = dst + key * 256;
+    *(u32x4*)(krow + 16 * ((2 * g) ^ (key & 15))) = fp8x8_to_bf16x8(u32x2{kc[0], kc[1]}, ks);
+    *(u32x4*)(krow + 16 * ((2 * g + 1) ^ (key & 15))) = fp8x8_to_bf16x8(u32x2{kc[2], kc[3]}, ks);
+    uint8_t* vblk = dst + 8192 + key * 256 + 32 * (g ^ (key & 7));
+    *(u32x4*)vblk = fp8x8_to_bf16x8(u32x2{vc[0], vc[1]}, vs);
+    *(u32x4*)(vblk + 16) = fp8x8_to_bf16x8(u32x2{vc[2], vc[3]}, vs);
+  }
+}
+
+// Where chunk x's data lands (DMA) and where its bf16 slot is read from (compute).
+template <int MODE>
+__device__ __forceinline__ uint8_t* co_land(uint8_t* lds, int x) {
+  return MODE == KV_FP8 ? lds + (x & (kCoSlots - 1)) * kCoCodeSlot : lds + (x & (kCoSlots - 1)) * kCoSlot;
+}
+template <int MODE>
+__device__ __forceinline__ uint8_t* co_slot(uint8_t* lds, int x) {
+  return MODE == KV_FP8 ? lds + kCoSlots * kCoCodeSlot + (x & 1) * kCoSlot : lds + (x & (kCoSlots - 1)) * kCoSlot;
 }
 
 // read_vt_fragments for a slot's V rows (256 bytes at slot + 8192, 32-byte blocks at block ^
@@ -1971,25 +2059,31 @@ __device__ __forceinline__ void co_pv(const Params& p, const PfTile& tl, int c, 
   }
 }
 
-// Step on chunk c of segment sg.  In flight on entry: the DMAs of c, c + 1, c + 2.  Wait for this
-// wave's DMAs of c, barrier (every wave's share of c is in LDS, and every wave is done with chunk
-// c - 1's slot); S = K Q^T of c; the DMAs of c + 3 into the freed slot (issued while the MFMAs
-// run); the softmax and P V of c.
-template <bool PLAIN>
+// Step on chunk c of segment sg.  In flight on entry: the DMAs of c, c + 1, c + 2.  Wait (bf16: for
+// this wave's DMAs of c; converting modes: of c + 1, c having been converted by the previous step),
+// barrier (every wave's share is in LDS, the previous step's conversion visible, and every wave done
+// with chunk c - 1's slot); converting modes: chunk c + 1's pass; S = K Q^T of c; the DMAs of c + 3
+// into the freed ring slot (issued while the MFMAs run); the softmax and P V of c.
+template <int MODE, bool PLAIN>
 __device__ __forceinline__ void co_step(const Params& p, const PfTile& tl, const CoLane& cl, const CoSeg& sg,
-                                        const int* ptab, int c, uint8_t* lds, const bf16x8 q[2][4], PfRow st[2],
-                                        int wv, int n, int j, int& err) {
+                                        const int* ptab, const float* scl, int c, uint8_t* lds, const bf16x8 q[2][4],
+                                        PfRow st[2], int wv, int n, int j, int& err) {
   const int last = sg.c_hi - 1;
-  co_barrier();
-  const uint8_t* buf = lds + (c & (kCoSlots - 1)) * kCoSlot;
+  co_barrier<(co_converts<MODE>() ? 1 : 2) * co_dmas<MODE>()>();
+  if constexpr (co_converts<MODE>()) {
+    const int cn = c + 1 < last ? c + 1 : last;
+    co_convert<MODE>(p, sg, scl, cn, co_land<MODE>(lds, c + 1), co_slot<MODE>(lds, c + 1));
+  }
+  const uint8_t* buf = co_slot<MODE>(lds, c);
   f32x4 sc[2][2];
   co_qk(buf, q, sc, n, j);
   const int cn = c + 3 < last ? c + 3 : last;
-  co_issue(p, tl, cl, sg, ptab, cn, lds_addr_of(lds + ((c + 3) & (kCoSlots - 1)) * kCoSlot), wv, err);
+  co_issue<MODE>(p, tl, cl, sg, ptab, cn, lds_addr_of(co_land<MODE>(lds, c + 3)), wv, err);
   co_pv<PLAIN>(p, tl, c, buf, sc, st, n, j);
 }
 
 // slot >= 0: the tile is one part of a split tile, its (m, l, acc) go to that partial slot
+template <int MODE>
 __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const CoLane& cln, uint8_t* lds, int wv,
                                         int lane, int n, int j, int& err, int slot) {
   PfRow st[2];
@@ -2011,7 +2105,7 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
     st[rb].l = 0.f;
   }
   // chunks below cp are seen in full by every row (the plain softmax); the rest (the diagonal, a
-  // window, a soft cap) take the general one
+  // window, a soft cap, masked keys of a finite mask value) take the general one
   int cp = tl.c_lo;
   if (!(p.soft_cap > 0.f) && p.sliding_window <= 0 && p.scale_log2 > 0.f) {
     const int pos_min = tl.kv_len - tl.q_len + tl.tok0;
@@ -2019,6 +2113,7 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
     cp = cp < tl.kv_len / KV_CHUNK ? cp : tl.kv_len / KV_CHUNK;
   }
   int* ptab = (int*)(lds + kCoPageBase);
+  float* scl = (float*)(lds + kCoScaleBase);
   CoSeg sg;
   sg.cps = p.S / KV_CHUNK;
   for (sg.c_lo = tl.c_lo; sg.c_lo < tl.c_hi; sg.c_lo = sg.c_hi) {
@@ -2026,9 +2121,17 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
     sg.c_hi = (sg.p_lo + kCoPages) * sg.cps;
     sg.c_hi = sg.c_hi < tl.c_hi ? sg.c_hi : tl.c_hi;
     const int npg = (sg.c_hi - 1) / sg.cps - sg.p_lo + 1;
-    __syncthreads();  // the previous segment's or tile's table and slots are no longer read
-    for (int t = threadIdx.x; t < npg; t += kCoWaves * 64) ptab[t] = p.page_indices[(size_t)tl.seq * p.PPS + sg.p_lo + t];
-    // the table and (first segment) the queries have landed, on every path: the compiler then has
+    __syncthreads();  // the previous segment's or tile's tables and slots are no longer read
+    for (int t = threadIdx.x; t < npg; t += kCoWaves * 64) {
+      const int pg = p.page_indices[(size_t)tl.seq * p.PPS + sg.p_lo + t];
+      ptab[t] = pg;
+      if constexpr (MODE == KV_FP8) {  // the page's K and V scales of kv head h (page 0's for a bad id)
+        f32x2 sv = f32x2{1.f, 1.f};  // times the scalar k_scale / v_scale, as the decode role applies them
+        if (p.kv_scales) sv = *(const f32x2*)(p.kv_scales + ((size_t)(pg >= 0 && pg < p.P ? pg : 0) * p.Hkv + tl.h) * 2);
+        *(f32x2*)(scl + 2 * t) = f32x2{sv[0] * p.k_scale, sv[1] * p.v_scale};
+      }
+    }
+    // the tables and (first segment) the queries have landed, on every path: the compiler then has
     // no load of its own left to wait for inside the step loop
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     __syncthreads();
@@ -2036,11 +2139,15 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
     auto cl = [&](int c) { return c < last ? c : last; };
 #pragma unroll
     for (int k = 0; k < 3; ++k)
-      co_issue(p, tl, cln, sg, ptab, cl(c0 + k), lds_addr_of(lds + ((c0 + k) & (kCoSlots - 1)) * kCoSlot), wv, err);
+      co_issue<MODE>(p, tl, cln, sg, ptab, cl(c0 + k), lds_addr_of(co_land<MODE>(lds, c0 + k)), wv, err);
+    if constexpr (co_converts<MODE>()) {  // chunk c0's pass before the loop takes over
+      co_barrier<2 * co_dmas<MODE>()>();
+      co_convert<MODE>(p, sg, scl, c0, co_land<MODE>(lds, c0), co_slot<MODE>(lds, c0));
+    }
     int c = c0;
     const int cpe = cp < sg.c_hi ? cp : sg.c_hi;
-    for (; c < cpe; ++c) co_step<true>(p, tl, cln, sg, ptab, c, lds, q, st, wv, n, j, err);
-    for (; c < sg.c_hi; ++c) co_step<false>(p, tl, cln, sg, ptab, c, lds, q, st, wv, n, j, err);
+    for (; c < cpe; ++c) co_step<MODE, true>(p, tl, cln, sg, ptab, scl, c, lds, q, st, wv, n, j, err);
+    for (; c < sg.c_hi; ++c) co_step<MODE, false>(p, tl, cln, sg, ptab, scl, c, lds, q, st, wv, n, j, err);
     co_drain();  // the clamped DMAs past the segment land before the slots are reused
   }
 
@@ -2157,6 +2264,7 @@ __device__ __forceinline__ int co_tile_parts(int sz, int np) {
 // workgroup writes every unit's key (one thread per unit: a binary search over the sequences'
 // first pairs finds its sequence), ranks them in LDS and maps queue position r to the unit of rank
 // r / Hkv, kv head r % Hkv.  Calls with more units than kPfOrderMax keep the pair order unsplit.
+template <int MODE>
 __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, uint8_t* lds, int* s_tile,
                                         int lane, int wv, int n, int j, int& err) {
   const CoPairs cp = co_pairs(p, wsi, pf_min, lane);
@@ -2173,7 +2281,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
   int nvalid = nunits;
   int* pkey = (int*)(lds + kCoOrderBase);
   int* pord = pkey + kPfOrderMax;
-  const CoLane cln = co_lane(wv, lane);
+  const CoLane cln = co_lane<MODE>(wv, lane);
   if (ranked) {
     // per sequence (256 entries each, over pord's area and the page table until they are
     // written): its first pair (the exclusive scan of the pair counts: never decreasing, and a
@@ -2181,7 +2289,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
     int* sq_off = pord;
     int* sq_kv = pord + 256;
     int* sq_ql = (int*)(lds + kCoPageBase);
-    static_assert(kCoPages >= 256, "sequence table");
+    static_assert(kCoPages * 12 >= 256 * 4, "sequence table over the page-id and scale tables");
     if (wv == 0) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -2267,7 +2375,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
         d->valid[threadIdx.x] = 1;
       }
     }
-    co_tile(p, tl, cln, lds, wv, lane, n, j, err, slot);
+    co_tile<MODE>(p, tl, cln, lds, wv, lane, n, j, err, slot);
   }
 }
 
@@ -2320,7 +2428,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (nseq > 64 * kWin) tv = fz ? 0 : uni(p.cu_q_lens[nseq]);
     if (fz) tv = nseq;
     // prefill tiles need the whole metadata in the four windows
-    pf_min = (MODE == KV_BF16 && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
+    pf_min = (co_tiles<MODE>() && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
       wsi[w] = SeqInfo{0, 0, 0, 0};
@@ -2350,7 +2458,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   bool any_pf = false;
 #pragma unroll
   for (int w = 0; w < kWin; ++w) any_pf = any_pf || wsi[w].q_len >= pf_min;
-  if (MODE == KV_BF16 && pf_min > 0 && !p.pf_kernel && __ballot(any_pf) != 0) {
+  if (co_tiles<MODE>() && pf_min > 0 && !p.pf_kernel && __ballot(any_pf) != 0) {
     // per lane over the four windows, then one wave sum each (skipped when no sequence is a
     // prefill sequence)
     float st = 0.f;
@@ -2386,7 +2494,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ int s_tile;
   bool pf_first;
   int bd;
-  if (MODE == KV_BF16 && p.co) {
+  if (co_tiles<MODE>() && p.co) {
     const int half = p.grid >> 1;
     pf_first = b >= half && b < half + gpre;
     bd = pf_first ? -1 : (b < half ? b : b - gpre);
@@ -2395,10 +2503,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     bd = b - gpre;
   }
   const int gd = p.grid - gpre;  // stream-K workgroup count
-  if (MODE == KV_BF16 && pf_first) {
+  if (co_tiles<MODE>() && pf_first) {
     if (UPG && p.co)
-      co_role(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
-    else  // (HG == 8: one K and one V piece per thread per chunk)
+      co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
+    else if constexpr (MODE == KV_BF16)  // (HG == 8: one K and one V piece per thread per chunk)
       pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
   const Partition pt = make_partition_fast(W, gd > 0 ? gd : 1);
@@ -2493,9 +2601,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   }
-  if (MODE == KV_BF16 && UPG && p.co && !pf_first && pf_total > 0) {
+  if (co_tiles<MODE>() && UPG && p.co && !pf_first && pf_total > 0) {
     __syncthreads();  // every wave is done with its stream-K LDS regions
-    co_role(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
+    co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
   }
 
   {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
@@ -3975,7 +4083,8 @@ int nominal_per_cu(int hg, size_t lds) {
 void resolve_layout(Params& p, int mode, const rpa_shape_t* shape, const rpa_options_t* opt) {
   const int pt = opt->prefill_tiles;
   const bool bf = mode == KV_BF16 && p.skip_masked;
-  const bool co_ok = bf && (pt == 0 || pt == 2) && p.S % KV_CHUNK == 0 && p.Hkv % kCoWaves == 0 &&
+  const bool co_mode = mode == KV_BF16 || mode == KV_BF16_SCALED || mode == KV_FP8;  // any mask value
+  const bool co_ok = co_mode && (pt == 0 || pt == 2) && p.S % KV_CHUNK == 0 && p.Hkv % kCoWaves == 0 &&
                      p.G <= 32 * kCoWaves && (long long)shape->num_tokens >= (long long)shape->max_num_seqs + 15;
   const bool tiles_ok = bf && p.HG == 8 && p.G <= 32 * p.HG;
   const bool pk_ok = bf && p.G <= kPkRows && p.S % kPkChunk == 0;

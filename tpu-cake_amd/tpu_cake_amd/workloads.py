@@ -42,7 +42,7 @@ LOGNORMAL_SIGMA = 0.5
 POOL_FACTOR = 1.25
 FP8_MAX = 448.0
 
-CONFIG_SEEDS = {"c1": 97, "c2": 98, "c3": 99, "c4": 98, "c5": 101}
+CONFIG_SEEDS = {"c1": 97, "c2": 98, "c3": 99, "c4": 98, "c5": 101, "c3f": 99, "c5t": 101}
 
 CONFIG_DESCRIPTIONS = {
     "c1": "tiny decode: 4 seqs x 1 token, kv_len U[1,512], Hq 8 / Hkv 2, D 128, page 16, 160-page pool",
@@ -50,6 +50,9 @@ CONFIG_DESCRIPTIONS = {
     "c3": "mixed: 24 decode rows (kv_len U[512,8192]) + 4 causal prefill chunks of 512 over prior U[0,3584], Hq 32 / Hkv 8, page 64",
     "c4": "fp8-e4m3 KV decode: C2 shapes, per-(page, kv head) K and V scales = max|x|/448",
     "c5": "heavy-tail decode: 256 seqs x 1 token, kv_len 16*(1+Lomax(1.2)) clip 16-131072, Hq 64 / Hkv 8, D 128, page 64",
+    # the two below are this build's measurement workloads beside BASELINE's five
+    "c3f": "C3's mixed batch (24 decode rows + 4 prefill chunks of 512) over an fp8-e4m3 pool with per-(page, kv head) K and V scales = max|x|/448",
+    "c5t": "C5 with its first sequence at the clip, 131072 keys (the heavy tail's worst case)",
 }
 
 
@@ -238,26 +241,31 @@ def _config_meta(cfg: str, rng) -> ConfigMeta:
         qls = np.concatenate([np.ones(24, dtype=np.int64), np.full(4, 512)])
         pages = int(np.sum(-(-lens // 64)))
         return ConfigMeta("c3", lens, qls, 32, 8, 128, 64, math.ceil(POOL_FACTOR * pages), 128)
-    if cfg == "c5":
+    if cfg == "c3f":
+        m = _config_meta("c3", rng)
+        return dataclasses.replace(m, name="c3f", kv_dtype="fp8")
+    if cfg in ("c5", "c5t"):
         lens = np.clip(np.floor(16.0 * (1.0 + rng.pareto(1.2, size=256))), 16, 131072).astype(np.int64)
+        if cfg == "c5t":
+            lens[0] = 131072
         pages = int(np.sum(-(-lens // 64)))
-        return ConfigMeta("c5", lens, np.ones(256, np.int64), 64, 8, 128, 64, math.ceil(POOL_FACTOR * pages), 2048)
-    raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+        return ConfigMeta(cfg, lens, np.ones(256, np.int64), 64, 8, 128, 64, math.ceil(POOL_FACTOR * pages), 2048)
+    raise ValueError(f"unknown config {cfg!r}; expected one of {sorted(CONFIG_SEEDS)}")
 
 
 def config_meta(cfg: str, seed: int | None = None) -> ConfigMeta:
     """Shapes and lengths of configuration ``cfg`` (the same draws as make_config), no values."""
     cfg = cfg.lower()
     if cfg not in CONFIG_SEEDS:
-        raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+        raise ValueError(f"unknown config {cfg!r}; expected one of {sorted(CONFIG_SEEDS)}")
     return _config_meta(cfg, np.random.default_rng(CONFIG_SEEDS[cfg] if seed is None else seed))
 
 
 def make_config(cfg: str, seed: int | None = None, values: str = "auto") -> RpaCase:
-    """Build one of the benchmark configurations ``c1`` .. ``c5``."""
+    """Build one of the benchmark configurations ``c1`` .. ``c5`` (or ``c3f`` / ``c5t``)."""
     cfg = cfg.lower()
     if cfg not in CONFIG_SEEDS:
-        raise ValueError(f"unknown config {cfg!r}; expected one of c1..c5")
+        raise ValueError(f"unknown config {cfg!r}; expected one of {sorted(CONFIG_SEEDS)}")
     if seed is None:
         seed = CONFIG_SEEDS[cfg]
     rng = np.random.default_rng(seed)
@@ -266,7 +274,7 @@ def make_config(cfg: str, seed: int | None = None, values: str = "auto") -> RpaC
                       num_kv_heads=m.num_kv_heads, head_dim=m.head_dim, page_size=m.page_size,
                       pool_pages=m.pool_pages, pages_per_seq=m.pages_per_seq, rng=rng,
                       values=_resolve_values(values), seed=seed)
-    return quantize_fp8(case) if cfg == "c4" else case
+    return quantize_fp8(case) if cfg in ("c4", "c3f") else case
 
 
 def make_custom(*, kv_lens, q_lens, num_q_heads, num_kv_heads, head_dim=128, page_size=16,
