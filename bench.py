@@ -271,8 +271,8 @@ def host_submit(args, dev, calls: int = 400) -> int:
     """Host time per call: ``calls`` back-to-back ops.ragged_paged_attention calls on C1 (kernels of
     a few microseconds, so the host is the bound), wall time / calls, median of 5 batches; the
     same with the validation plan dropped each call (the first call of a new signature); the call
-    prepared once (ops.PreparedCall); and the call captured into a HIP graph (ops.CapturedCall),
-    per replay."""
+    prepared once (ops.PreparedCall); the call captured into a HIP graph (ops.CapturedCall), per
+    replay; and 32 calls captured into one graph (ops.CapturedCalls), per call."""
     import statistics
 
     import torch
@@ -343,8 +343,27 @@ def host_submit(args, dev, calls: int = 400) -> int:
         cc.replay()
     ev1.record()
     torch.cuda.synchronize()
+    graph1_us = round(ev0.elapsed_time(ev1) * 1e3 / calls, 2)
+    # a whole step's calls in one graph (ops.CapturedCalls: 32 calls, one per layer of a model,
+    # here over the same buffers), per call
+    layers = 32
+    many = ops.CapturedCalls([((d["q"], d["kv_pages"], d["kv_lens"], d["page_indices"], d["cu_q_lens"],
+                                d["num_seqs"]), dict(sm_scale=case.sm_scale, out=torch.empty_like(d["q"])))
+                              for _ in range(layers)])
+    for _ in range(5):
+        many.replay()
+    torch.cuda.synchronize()
+    reps = max(1, calls // layers)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(reps):
+        many.replay()
+    ev1.record()
+    res["graph_of_32_calls"] = round((time.perf_counter() - t0) / (reps * layers) * 1e6, 2)
+    torch.cuda.synchronize()
     print(json.dumps({"host_submit_us_per_call": res, "device_us_per_call_back_to_back": device_us,
-                      "device_us_per_call_graph_replays": round(ev0.elapsed_time(ev1) * 1e3 / calls, 2),
+                      "device_us_per_call_graph_replays": graph1_us,
+                      "device_us_per_call_graph_of_32_calls": round(ev0.elapsed_time(ev1) * 1e3 / (reps * layers), 2),
                       "calls": calls, "workload": "c1 (kernels of a few us: the host is the bound)"}), flush=True)
     return 0
 

@@ -201,6 +201,17 @@ int rpa_gather_kv(const rpa_shape_t* shape, const void* kv_pages, const int32_t*
 int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* host_word,
                         void* stream);
 
+/* Diagnostic, with no counterpart in the reference: the attention kernel's per-workgroup
+ * timeline of the last launch, for a library built with -DRPA_TIMELINE (the variant
+ * `python -m tpu_cake_amd.timeline` builds); the product library returns RPA_E_UNSUPPORTED.
+ * Synchronises `stream`, then copies rows 0 .. rows-1 (workgroup b = row b, rows <= 8192),
+ * 16 int64 fields each: stamps of the 100 MHz constant clock at kernel entry, work split known,
+ * first stream-K loads issued, stream-K range done, prefill-tile role entered, tile order ready,
+ * kernel exit; the role bits (1 prefill-first, 2 stream-K range, 4 tiles joined after it);
+ * stream-K units; prefill tiles and their 32-key chunk steps; clock ticks summed over the tiles
+ * in queue fetches, tile set-up, chunk-step loops and row writes; XCC_ID << 32 | HW_ID. */
+int rpa_timeline_read(int64_t* host_rows, int32_t rows, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Fused Inkling decode (v3 semantics): write each sequence's new K/V token into the paged
  * cache, then attend over the updated cache with an additive relative-position bias.

@@ -201,3 +201,12 @@ def test_search_refuses_noop_waves_per_cu_candidate():
         search.refuse_noop_candidates(c, case, grid)
     ok = search.SearchContract(config="c2", baseline="base", candidates=(("base", {}), ("w4", {"waves_per_cu": 4})), rounds=4)
     search.refuse_noop_candidates(ok, case, grid)
+
+
+def test_product_library_has_no_timeline(lib):
+    # the product build records no timeline: its read entry point says so without touching a GPU
+    import ctypes
+
+    buf = (ctypes.c_int64 * 16)()
+    assert lib.rpa_timeline_read(buf, 1, None) == -2  # RPA_E_UNSUPPORTED
+    assert b"RPA_TIMELINE" in lib.rpa_last_error()

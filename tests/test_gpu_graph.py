@@ -70,6 +70,53 @@ def test_captured_call_replays_match_eager(cuda, name):
             assert err["finite"] and err["max_abs"] <= 2e-2, err
 
 
+def test_captured_calls_layers_match_eager(cuda):
+    """Four calls in one graph, as a model's decode step captures one call per layer: each layer
+    has its own queries, K/V pool and output and all share the step's metadata tensors; the second
+    and fourth layers carry an fp8 pool and a sliding window.  Every layer of every replay is
+    bitwise equal to the same eager call."""
+    _say("captured calls, 4 layers")
+    case = make_custom(kv_lens=[700, 45, 1030, 9, 2100], q_lens=[1, 45, 30, 1, 64], num_q_heads=16,
+                       num_kv_heads=4, page_size=64, seed=21)
+    d = ops.case_to_device(case, "cuda")
+    meta = (d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"])
+    gen = torch.Generator(device="cuda").manual_seed(17)
+    layers = []
+    for li in range(4):
+        q = torch.randn(d["q"].shape, generator=gen, device="cuda").to(torch.bfloat16)
+        if li % 2:
+            kv = (torch.randn(d["kv_pages"].shape, generator=gen, device="cuda") * 4).to(torch.float8_e4m3fn)
+            kw = dict(sm_scale=case.sm_scale, k_scale=0.5, v_scale=0.25, sliding_window=512)
+        else:
+            kv = torch.randn(d["kv_pages"].shape, generator=gen, device="cuda").to(torch.bfloat16)
+            kw = dict(sm_scale=case.sm_scale)
+        layers.append(((q, kv) + meta, kw))
+    cc = ops.CapturedCalls(layers)
+    kv_lens0 = d["kv_lens"].clone()
+    q_lens = (d["cu_q_lens"][1:] - d["cu_q_lens"][:-1])[: kv_lens0.numel()].to(kv_lens0.dtype)
+    for r in range(3):
+        for (args, _) in layers:
+            args[0].copy_(torch.randn(args[0].shape, generator=gen, device="cuda").to(torch.bfloat16))
+        if r == 2:  # shorter sequences, still covering their query tokens
+            d["kv_lens"].copy_(torch.maximum(kv_lens0 - 41, q_lens))
+        torch.cuda.synchronize()
+        wants = [ops.ragged_paged_attention(*args, **kw).clone() for args, kw in layers]
+        torch.cuda.synchronize()
+        gots = cc.replay()
+        torch.cuda.synchronize()
+        for li, (got, want) in enumerate(zip(gots, wants)):
+            assert torch.equal(got, want), f"replay {r} layer {li} differs from the eager call"
+
+
+def test_captured_calls_rejects_bad_calls(cuda):
+    with pytest.raises(ValueError, match="no calls"):
+        ops.CapturedCalls([])
+    case = make_config("c1")
+    d = ops.case_to_device(case, "cuda")
+    with pytest.raises(ValueError, match="six positional"):
+        ops.CapturedCalls([((d["q"], d["kv_pages"]), {})])
+
+
 def test_captured_call_rejects_events(cuda):
     case = make_config("c1")
     d = ops.case_to_device(case, "cuda")

@@ -78,6 +78,60 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 // KV_BF16_FUSED: the fused Inkling decode step in one attention launch (Params::fused).
 enum KvMode { KV_BF16 = 0, KV_BF16_SCALED = 1, KV_FP8 = 2, KV_BF16_BIAS = 3, KV_BF16_FUSED = 4 };
 
+// Per-workgroup timeline of the attention kernel, compiled in only with -DRPA_TIMELINE (the
+// library variant tpu_cake_amd.timeline builds; the product library records nothing).  Thread 0
+// of workgroup b writes row b: stamps of the 100 MHz constant clock (s_memrealtime) at the
+// kernel's phases, the role, work counts, per-tile phase sums of the prefill tiles, and where
+// the workgroup ran.  Only the workgroup's own thread 0 reads or writes its row.
+enum TlField {
+  TL_START = 0,   // kernel entry
+  TL_SCHED,       // work split and roles known
+  TL_FIRST,       // stream-K: first unit's loads issued (0: no stream-K range)
+  TL_DEC,         // stream-K range done
+  TL_TILES0,      // prefill-tile role entered (0: none)
+  TL_RANKED,      // tile order ready (first queue fetch next)
+  TL_END,         // kernel exit
+  TL_ROLE,        // bit 0 prefill-first workgroup, bit 1 stream-K range, bit 2 tiles joined after it
+  TL_UNITS,       // stream-K units of the range
+  TL_NTILES,      // prefill tiles (or tile parts) taken
+  TL_NSTEPS,      // 32-key chunk steps of those tiles
+  TL_QUEUE,       // clock ticks in queue fetches
+  TL_SETUP,       // ticks from a tile's start to its first chunk step (tables, prologue DMAs)
+  TL_LOOP,        // ticks in the chunk-step loops
+  TL_WRITE,       // ticks from the last step to the tile's rows written
+  TL_WHERE,       // XCC_ID << 32 | HW_ID (CU, shader array, shader engine)
+  TL_FIELDS
+};
+#ifdef RPA_TIMELINE
+constexpr int kTlRows = 8192;
+__device__ long long g_timeline[kTlRows * TL_FIELDS];
+__device__ __forceinline__ long long tl_clock() { return (long long)__builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ void tl_set(int f, long long v) {
+  if (threadIdx.x == 0 && blockIdx.x < kTlRows) g_timeline[blockIdx.x * TL_FIELDS + f] = v;
+}
+__device__ __forceinline__ void tl_add(int f, long long v) {
+  if (threadIdx.x == 0 && blockIdx.x < kTlRows) g_timeline[blockIdx.x * TL_FIELDS + f] += v;
+}
+__device__ __forceinline__ void tl_begin() {
+  if (threadIdx.x == 0 && blockIdx.x < kTlRows) {
+    long long* row = g_timeline + blockIdx.x * TL_FIELDS;
+    for (int f = 1; f < TL_FIELDS; ++f) row[f] = 0;
+    const unsigned xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // XCC_ID[3:0]
+    const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_ID
+    row[TL_WHERE] = (long long)xcc << 32 | hw;
+  }
+}
+#define RPA_TL(...) __VA_ARGS__
+#else
+#define RPA_TL(...)
+#endif
+// Per-workgroup sums of the prefill tiles' phases, kept in registers (empty without RPA_TIMELINE).
+struct TlAcc {
+#ifdef RPA_TIMELINE
+  long long queue = 0, setup = 0, loop = 0, write = 0, tiles = 0, steps = 0;
+#endif
+};
+
 // Modes that add a relative-position bias to the scores.
 template <int MODE>
 constexpr bool has_bias() {
@@ -2085,7 +2139,8 @@ __device__ __forceinline__ void co_step(const Params& p, const PfTile& tl, const
 // slot >= 0: the tile is one part of a split tile, its (m, l, acc) go to that partial slot
 template <int MODE>
 __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const CoLane& cln, uint8_t* lds, int wv,
-                                        int lane, int n, int j, int& err, int slot) {
+                                        int lane, int n, int j, int& err, int slot, TlAcc& ta) {
+  RPA_TL(const long long tl_a = tl_clock(); long long tl_b = 0;)
   PfRow st[2];
   bf16x8 q[2][4];
 #pragma unroll
@@ -2145,11 +2200,14 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
       co_convert<MODE>(p, sg, scl, c0, co_land<MODE>(lds, c0), co_slot<MODE>(lds, c0));
     }
     int c = c0;
+    RPA_TL(if (tl_b == 0) tl_b = tl_clock();)
     const int cpe = cp < sg.c_hi ? cp : sg.c_hi;
     for (; c < cpe; ++c) co_step<MODE, true>(p, tl, cln, sg, ptab, scl, c, lds, q, st, wv, n, j, err);
     for (; c < sg.c_hi; ++c) co_step<MODE, false>(p, tl, cln, sg, ptab, scl, c, lds, q, st, wv, n, j, err);
     co_drain();  // the clamped DMAs past the segment land before the slots are reused
   }
+  RPA_TL(const long long tl_c = tl_clock(); ta.setup += tl_b - tl_a; ta.loop += tl_c - tl_b; ta.tiles += 1;
+         ta.steps += tl.c_hi - tl.c_lo;)
 
   if (slot >= 0) {  // a part of a split tile: its unnormalised state, (m, l) in log2 units
 #pragma unroll
@@ -2163,6 +2221,7 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
 #pragma unroll
       for (int d = 0; d < 8; ++d) *(f32x4*)(acc + 16 * d) = st[rb].acc[d];
     }
+    RPA_TL(ta.write += tl_clock() - tl_c;)
     return;
   }
 #pragma unroll
@@ -2181,6 +2240,7 @@ __device__ __forceinline__ void co_tile(const Params& p, const PfTile& tl, const
       *(u32x2*)(op + 16 * d) = w;
     }
   }
+  RPA_TL(ta.write += tl_clock() - tl_c;)
 }
 
 // The (sequence, token block) pairs of the call's prefill tiles in queue order (sequences in window
@@ -2267,6 +2327,8 @@ __device__ __forceinline__ int co_tile_parts(int sz, int np) {
 template <int MODE>
 __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, uint8_t* lds, int* s_tile,
                                         int lane, int wv, int n, int j, int& err) {
+  RPA_TL(tl_set(TL_TILES0, tl_clock());)
+  TlAcc ta;
   const CoPairs cp = co_pairs(p, wsi, pf_min, lane);
   const int npairs = cp.base[4];
   int np = 1;
@@ -2339,11 +2401,14 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
     __syncthreads();
   }
   const int total = (ranked ? nvalid : npairs) * p.Hkv;
+  RPA_TL(tl_set(TL_RANKED, tl_clock());)
   for (;;) {
+    RPA_TL(const long long tl_q = tl_clock();)
     if (threadIdx.x == 0) *s_tile = atomicAdd(p.err + kQueueWord, 1);
     __syncthreads();
     const int tq = uni(*s_tile);
     __syncthreads();
+    RPA_TL(ta.queue += tl_clock() - tl_q;)
     if (tq >= total) break;
     const int h = tq % p.Hkv;
     int pair = tq / p.Hkv, part = 0, unit_np = 1;
@@ -2375,8 +2440,10 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
         d->valid[threadIdx.x] = 1;
       }
     }
-    co_tile<MODE>(p, tl, cln, lds, wv, lane, n, j, err, slot);
+    co_tile<MODE>(p, tl, cln, lds, wv, lane, n, j, err, slot, ta);
   }
+  RPA_TL(tl_set(TL_NTILES, ta.tiles); tl_set(TL_NSTEPS, ta.steps); tl_set(TL_QUEUE, ta.queue);
+         tl_set(TL_SETUP, ta.setup); tl_set(TL_LOOP, ta.loop); tl_set(TL_WRITE, ta.write);)
 }
 
 template <int MODE, bool UPG>
@@ -2389,6 +2456,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n = lane & 15, j = lane >> 4;
   const int b = blockIdx.x;
   int err = 0;
+  RPA_TL(const long long tl_t0 = tl_clock(); tl_begin(); tl_set(TL_START, tl_t0);)
 
   // Schedule: total work W, this workgroup's range [u0, u1), the sequence holding u0 and a
   // window of per-lane sequence metadata.  num_seqs and the metadata of the first 256 sequences
@@ -2503,6 +2571,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     bd = b - gpre;
   }
   const int gd = p.grid - gpre;  // stream-K workgroup count
+  RPA_TL(tl_set(TL_SCHED, tl_clock()); int tl_role = pf_first ? 1 : 0;)
   if (co_tiles<MODE>() && pf_first) {
     if (UPG && p.co)
       co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
@@ -2569,6 +2638,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           load_q<MODE>(p, cur, n, j, wv, q, rst);
           load_lines<MODE>(p, a0, lane, 1, v);
         }
+        RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
         store_k_tile<MODE>(p, k, kt, lane);
         line_bias_values<MODE>(p, cur, bias_in, rst, rs, lane, n, j, bias);
         RowState st;
@@ -2587,6 +2657,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           load_q<MODE>(p, cur, n, j, wv, q);
           load_half<MODE, UPG>(p, a0, 1, va);
         }
+        RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
         RowState st;
 
         long long u = u0;
@@ -2601,8 +2672,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
     }
   }
+  RPA_TL(tl_set(TL_DEC, tl_clock());)
   if (co_tiles<MODE>() && UPG && p.co && !pf_first && pf_total > 0) {
     __syncthreads();  // every wave is done with its stream-K LDS regions
+    RPA_TL(tl_role |= 4;)
     co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
   }
 
@@ -2613,6 +2686,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (size_t k = first + (size_t)b * blockDim.x + threadIdx.x; k < last; k += (size_t)p.grid * blockDim.x)
       o[k] = u32x4{0u, 0u, 0u, 0u};
   }
+  RPA_TL(tl_set(TL_END, tl_clock()); tl_set(TL_ROLE, tl_role);)
   if (err) atomicOr(p.err, err);
 }
 
@@ -4011,6 +4085,20 @@ int rpa_read_error_word(const void* workspace, size_t workspace_bytes, int32_t* 
       hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
     return fail(RPA_E_HIP, "reading the error word failed");
   return RPA_OK;
+}
+
+int rpa_timeline_read(int64_t* host_rows, int32_t rows, void* stream) {
+#ifdef RPA_TIMELINE
+  if (!host_rows || rows <= 0 || rows > kTlRows) return fail(RPA_E_INVALID, "bad timeline arguments");
+  if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess ||
+      hipMemcpyFromSymbol(host_rows, HIP_SYMBOL(g_timeline), (size_t)rows * TL_FIELDS * sizeof(long long)) !=
+          hipSuccess)
+    return fail(RPA_E_HIP, "reading the timeline failed");
+  return RPA_OK;
+#else
+  (void)host_rows, (void)rows, (void)stream;
+  return fail(RPA_E_UNSUPPORTED, "this library was built without RPA_TIMELINE");
+#endif
 }
 
 // Workspaces whose last call could not launch its combine kernel (descriptors, flags and the tile

@@ -13,6 +13,7 @@ from . import fused, inkling  # noqa: F401
 from .ops import (  # noqa: F401
     DEFAULT_MASK_VALUE,
     CapturedCall,
+    CapturedCalls,
     PreparedCall,
     dynamic_validate_inputs,
     gather_kv,
@@ -23,6 +24,7 @@ from .ops import (  # noqa: F401
 
 __all__ = [
     "CapturedCall",
+    "CapturedCalls",
     "DEFAULT_MASK_VALUE",
     "PreparedCall",
     "fused",

@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "rpa_inkling_workspace_size",
     "rpa_inkling_decode",
     "rpa_attention_grid",
+    "rpa_timeline_read",
 )
 
 
@@ -166,6 +167,8 @@ def load() -> ctypes.CDLL:
         lib.rpa_attention_grid.restype = ctypes.c_int
         lib.rpa_attention_grid.argtypes = [ctypes.POINTER(RpaShape), ctypes.POINTER(RpaOptions), ctypes.c_int32,
                                            i32p, i32p]
+        lib.rpa_timeline_read.restype = ctypes.c_int
+        lib.rpa_timeline_read.argtypes = [ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, vp]
         lib.rpa_inkling_decode.restype = ctypes.c_int
         lib.rpa_inkling_decode.argtypes = [ctypes.POINTER(RpaInklingShape), ctypes.c_float] + [vp] * 8 + [sz, vp]
         version = lib.rpa_abi_version()

@@ -1,4 +1,9 @@
-"""Build ``librpa.so`` for gfx950 in-tree with hipcc (``python -m tpu_cake_amd.build``)."""
+"""Build ``librpa.so`` for gfx950 in-tree with hipcc (``python -m tpu_cake_amd.build``).
+
+Also builds ``librpa_timeline.so``: the same sources with ``-DRPA_TIMELINE``, whose attention
+kernel records a per-workgroup timeline (read by ``tpu_cake_amd.timeline``); the product path
+never loads it.
+"""
 
 from __future__ import annotations
 
@@ -15,6 +20,7 @@ INCLUDE = ROOT / "include"
 SOURCES = [CSRC / "rpa_kernels.hip"]
 HEADERS = [CSRC / "rpa_schedule.h", INCLUDE / "rpa.h"]
 OUTPUT = PKG / "librpa.so"
+TIMELINE_OUTPUT = PKG / "librpa_timeline.so"
 ARCH = "gfx950"
 
 
@@ -35,17 +41,31 @@ def command(output: pathlib.Path = OUTPUT, extra: list[str] | None = None) -> li
     ]
 
 
-def build(verbose: bool = False) -> pathlib.Path:
-    """Compile every HIP source into ``librpa.so`` (always recompiles)."""
-    tmp = OUTPUT.with_suffix(".so.tmp")
-    cmd = command(tmp)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
-    if verbose and res.stderr.strip():
-        print(res.stderr, file=sys.stderr)
-    os.replace(tmp, OUTPUT)
-    return OUTPUT
+def _start(output: pathlib.Path, extra: list[str]):
+    tmp = output.with_suffix(".so.tmp")
+    cmd = command(tmp, extra)
+    return output, tmp, cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def _finish(job, verbose: bool) -> pathlib.Path:
+    output, tmp, cmd, proc = job
+    _, err = proc.communicate()
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, output)
+    return output
+
+
+def build(verbose: bool = False, timeline: bool = True) -> pathlib.Path:
+    """Compile every HIP source into ``librpa.so`` (always recompiles), and (``timeline``) the
+    timeline variant beside it, the two compilations in parallel.  Returns the product path."""
+    jobs = [_start(OUTPUT, [])]
+    if timeline:
+        jobs.append(_start(TIMELINE_OUTPUT, ["-DRPA_TIMELINE"]))
+    out = [_finish(j, verbose) for j in jobs]
+    return out[0]
 
 
 if __name__ == "__main__":

@@ -332,34 +332,70 @@ def ragged_paged_attention(
     return out
 
 
-class CapturedCall:
-    """One ``ragged_paged_attention`` call captured into a HIP graph over fixed buffers.
+class CapturedCalls:
+    """Several ``ragged_paged_attention`` calls captured into one HIP graph over fixed buffers.
 
-    A serving loop writes each step's queries, K/V pages and metadata into the same tensors and
-    calls ``replay()``: the graph re-runs the call's kernels on whatever those tensors hold, at the
-    host cost of one graph launch instead of the wrapper's per-call work.  Capture happens on a
-    stream of this object (default priority) after one warm-up call on it, so the validated plan and
-    the stream's workspace (allocated and initialised by ``rpa_workspace_init``) exist beforehand:
-    the graph records only the call's kernel launches -- no allocation, no memset node.  The
-    workspace is this stream's, so replays must not overlap other calls on it.  Metadata changes
-    keep the shapes (``num_seqs``, ``kv_lens``, ``cu_q_lens`` and ``page_indices`` values may
-    change; their sizes, the dtypes and the knobs are fixed at capture).
+    The form a serving loop uses when its whole step is a graph: one call per layer, each over its
+    own queries, K/V pool and output, usually sharing the step's metadata tensors.  The loop writes
+    each step's values and metadata into the same tensors and calls ``replay()``; the graph re-runs
+    every call's kernels on what those tensors hold, for one graph launch.  Capture happens on a
+    stream of this object (default priority) after one warm-up run of every call on it, so the
+    validated plans and the stream's workspace (allocated and initialised by
+    ``rpa_workspace_init``) exist beforehand: the graph records only the calls' kernel launches --
+    no allocation, no memset node.  The calls run in list order on the one stream and share its
+    workspace, so replays must not overlap other calls on it.  Metadata changes keep the shapes
+    (``num_seqs``, ``kv_lens``, ``cu_q_lens`` and ``page_indices`` values may change; their sizes,
+    the dtypes and the knobs are fixed at capture).
+
+    ``calls`` is a sequence of ``(args, kwargs)`` pairs, ``args`` the operator's six positionals;
+    a call without ``out`` in its keywords gets a new output tensor.  ``outs`` holds the outputs.
     """
 
-    def __init__(self, q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *, out=None, **kwargs):
-        if kwargs.get("kernel_events") is not None:
-            raise ValueError("a captured call takes no kernel_events")
-        self.out = out if out is not None else torch.empty_like(q)
-        self._args = (q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs)
-        self._kwargs = dict(kwargs, out=self.out)
-        self.stream = torch.cuda.Stream(device=q.device)
-        self.stream.wait_stream(torch.cuda.current_stream(q.device))
+    def __init__(self, calls):
+        calls = list(calls)
+        if not calls:
+            raise ValueError("no calls to capture")
+        self._calls = []
+        for args, kwargs in calls:
+            if len(args) != 6:
+                raise ValueError("each call takes the operator's six positional arguments")
+            if kwargs.get("kernel_events") is not None:
+                raise ValueError("a captured call takes no kernel_events")
+            out = kwargs.get("out")
+            if out is None:
+                out = torch.empty_like(args[0])
+            self._calls.append((tuple(args), dict(kwargs, out=out)))
+        self.outs = [kw["out"] for _, kw in self._calls]
+        dev = self._calls[0][0][0].device
+        self.stream = torch.cuda.Stream(device=dev)
+        self.stream.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(self.stream):
-            ragged_paged_attention(*self._args, **self._kwargs)  # plan + this stream's workspace
+            for args, kwargs in self._calls:  # plans + this stream's workspace
+                ragged_paged_attention(*args, **kwargs)
         self.stream.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=self.stream):
-            ragged_paged_attention(*self._args, **self._kwargs)
+            for args, kwargs in self._calls:
+                ragged_paged_attention(*args, **kwargs)
+
+    def replay(self) -> list:
+        """Launch the captured calls (ordered after the current stream's work); returns ``outs``."""
+        self.graph.replay()
+        return self.outs
+
+
+class CapturedCall(CapturedCalls):
+    """One ``ragged_paged_attention`` call captured into a HIP graph over fixed buffers
+    (``CapturedCalls`` with one call; ``replay()`` returns ``out``).
+
+    A graph launch costs more host time on this platform than the operator's own eager call, so a
+    graph of one call is host-bound at the graph-launch rate; a graph holding a whole step's calls
+    (``CapturedCalls``) pays that launch once for all of them.
+    """
+
+    def __init__(self, q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *, out=None, **kwargs):
+        super().__init__([((q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs), dict(kwargs, out=out))])
+        self.out = self.outs[0]
 
     def replay(self) -> torch.Tensor:
         """Launch the captured call (ordered after the current stream's work) and return ``out``."""
