@@ -302,6 +302,32 @@ def test_receipt_passes_and_detects_tampering(tmp_path):
         evidence.validate_receipt(tmp_path)
 
 
+def test_receipt_mfma_fraction_and_markdown(tmp_path):
+    ident = {"kernel_source_digest": "k", "library_sha256": "l"}
+    for m in ("timing", "trace"):
+        _phase(tmp_path, m, ident)
+    # the counters phase with the MFMA counters: 2.56e6 busy cycles over 1024 SIMDs against 8e4 GUI-active
+    # cycles summed over 8 XCD instances (1e4 per XCD) is a busy fraction of 2.56e6 / (1e4 * 1024) = 0.25
+    d = tmp_path / "counters"
+    _write_profile(d, counters={"FETCH_SIZE": 5.0, "WRITE_SIZE": 1.0, "SQ_VALU_MFMA_BUSY_CYCLES": 2.56e6 - 1,
+                                "GRBM_GUI_ACTIVE": 8e4 - 1, "SQ_INSTS_VALU_MFMA_MOPS_BF16": 10.0})
+    prof = evidence.inspect_profile(d)
+    ass = evidence.assess_profile(prof, dispatches=10, counters=evidence.COUNTERS + evidence.MFMA_COUNTERS)
+    arts = [{"path": str(p.relative_to(d)), "sha256": evidence.sha256_file(p), "role": "x"}
+            for p in sorted(d.rglob("*")) if p.is_file()]
+    (d / "result.json").write_text(json.dumps({"mode": "counters", "identity": ident, "config": "c1", "steps": 10,
+                                               "input_sha256": "ab", "profile": prof, "assessment": ass,
+                                               "passed": ass["accepted"], "artifacts": arts}))
+    rec = evidence.build_receipt(tmp_path)
+    assert rec["status"] == "passed", rec["reasons"]
+    assert rec["metrics"]["counters.attention_mfma_busy_fraction"] == 0.25
+    md = evidence.receipt_markdown(tmp_path, "python tests/evidence_run.py --config c1 --root R")
+    assert md.startswith("# Evidence receipt: C1 (timing, trace, counters)")
+    assert "Status: **passed**" in md and "digest k." in md
+    assert "| counters.attention_mfma_busy_fraction | 0.25 |" in md
+    assert "Assessments: counters: accepted; trace: accepted" in md
+
+
 @pytest.mark.parametrize("mutate,reason", [("identity", "disagree on identity"), ("unchecked", "not checked"),
                                            ("failed", "timing phase did not pass")])
 def test_receipt_rejections(tmp_path, mutate, reason):

@@ -280,7 +280,14 @@ def build_receipt(root) -> dict:
         "trace.combine_avg_ns": trace_k.get("rpa_combine_kernel", {}).get("avg_ns"),
         "counters.attention_fetch_kib": cnt.get("FETCH_SIZE"),
         "counters.attention_write_kib": cnt.get("WRITE_SIZE"),
+        "counters.attention_mfma_busy_cycles": cnt.get("SQ_VALU_MFMA_BUSY_CYCLES"),
+        "counters.attention_gui_active_cycles": cnt.get("GRBM_GUI_ACTIVE"),
+        "counters.attention_mfma_mops_bf16": cnt.get("SQ_INSTS_VALU_MFMA_MOPS_BF16"),
     }
+    busy, active = metrics["counters.attention_mfma_busy_cycles"], metrics["counters.attention_gui_active_cycles"]
+    if busy is not None and active:
+        # GRBM_GUI_ACTIVE is summed over the 8 XCDs' instances, the busy cycles over 1024 SIMDs
+        metrics["counters.attention_mfma_busy_fraction"] = round(busy / (active / 8 * 1024), 4)
     artifacts = []
     for m in PHASES:
         artifacts.append({"path": f"{m}/result.json", "sha256": sha256_file(root / m / "result.json"),
@@ -322,6 +329,31 @@ def validate_receipt(root) -> dict:
     return receipt
 
 
+def receipt_markdown(root, command: str) -> str:
+    """A validated receipt as the markdown summary kept under ``profiles/``."""
+    rec = validate_receipt(root)
+    cfg = rec["config"]
+    name = cfg.get("config", "?") if isinstance(cfg, dict) else str(cfg)
+    corr = rec["correctness"]
+    lines = [f"# Evidence receipt: {name.upper()} (timing, trace, counters)", "",
+             "Command (repository root, MI355X box, `PYTHONPATH=tpu-cake_amd:.`):", "", "```", command,
+             f"python -m tpu_cake_amd.evidence validate {root}", "```", "",
+             f"Status: **{rec['status']}** (validated: every artifact re-hashed), kernel sources digest "
+             f"{rec['identity'].get('kernel_source_digest', '?')}.", "", "| metric | value |", "|---|---|"]
+    for k in sorted(rec["metrics"]):
+        v = rec["metrics"][k]
+        lines.append(f"| {k} | {v if v is not None else 'n/a'} |")
+    lines += ["", f"Correctness (oracle `{corr.get('oracle', '?')}`): max-abs {corr.get('max_abs', float('nan')):.3e}, "
+              f"rel-L2 {corr.get('rel_l2', float('nan')):.2e}, tolerance {corr.get('tolerance')}.", "",
+              "Assessments: " + "; ".join(f"{m}: {'accepted' if a.get('accepted') else 'rejected'}"
+                                          for m, a in sorted(rec["assessments"].items())), "",
+              f"{len(rec['artifacts'])} artifacts (three result.json, timing samples, rocprofv3 CSVs) with sha256 "
+              "in the receipt."]
+    if rec["reasons"]:
+        lines += ["", "Reasons: " + "; ".join(rec["reasons"])]
+    return "\n".join(lines) + "\n"
+
+
 # --------------------------------------------------------------------------- CLI
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(prog="python -m tpu_cake_amd.evidence")
@@ -335,6 +367,10 @@ def main(argv=None) -> int:
     i.add_argument("path")
     v = sub.add_parser("validate")
     v.add_argument("root")
+    rm = sub.add_parser("receipt-md", help="write a validated receipt's markdown summary")
+    rm.add_argument("root")
+    rm.add_argument("--command", required=True, help="the command that produced the receipt")
+    rm.add_argument("--write", required=True)
     pr = sub.add_parser("profile", help="run every rocprofv3 pass behind profiles/ (GPU box)")
     pr.add_argument("--raw", required=True)
     pr.add_argument("--configs", nargs="*", default=None)
@@ -353,6 +389,9 @@ def main(argv=None) -> int:
     if a.cmd == "_steps":
         res, _, _ = _steps(a.config, a.steps, a.warmup, events=False)
         pathlib.Path(a.out).write_text(json.dumps(res) + "\n")
+        return 0
+    if a.cmd == "receipt-md":
+        pathlib.Path(a.write).write_text(receipt_markdown(a.root, a.command))
         return 0
     if a.cmd == "inspect":
         print(json.dumps(inspect_profile(a.path), indent=1, sort_keys=True))
