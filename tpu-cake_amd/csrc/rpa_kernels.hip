@@ -4157,16 +4157,17 @@ int nominal_per_cu(int hg, size_t lds) {
   return per_cu < 1 ? 1 : per_cu;
 }
 
-// Where the rows of sequences with >= 16 query tokens go (bf16 KV without scales, masked keys at
-// weight 0), and the workgroup shape that follows:
-//   prefill_tiles 2 or 0, page size a multiple of 32, Hkv a multiple of 4, and num_tokens >=
-//     max_num_seqs + 15 (the batch can hold such a sequence; a batch of one token per sequence
-//     keeps the decode layout): the attention kernel's tiles in the co-resident layout (4-wave
-//     workgroups, two per CU, one prefill and one stream-K workgroup side by side);
-//   prefill_tiles 3, or 2 / 0 otherwise with eight kv heads per workgroup: the attention
-//     kernel's tiles in 8-wave workgroups, one per CU, roles split by CU;
-//   prefill_tiles 1, or 0 when neither applies: the prefill kernel, when chunks lie in one page
-//     (page size a multiple of 64);
+// Where the rows of sequences with >= 16 query tokens go, and the workgroup shape that follows:
+//   prefill_tiles 2 or 0, bf16 KV (plain or with scalar k/v scales) or fp8 KV, any mask value,
+//     page size a multiple of 32, Hkv a multiple of 4, and num_tokens >= max_num_seqs + 15 (the
+//     batch can hold such a sequence; a batch of one token per sequence keeps the decode layout):
+//     the attention kernel's tiles in the co-resident layout (4-wave workgroups, two per CU, one
+//     prefill and one stream-K workgroup side by side);
+//   prefill_tiles 3, or 2 / 0 otherwise, for plain bf16 KV whose masked keys get weight 0 and
+//     eight kv heads per workgroup: the attention kernel's tiles in 8-wave workgroups, one per
+//     CU, roles split by CU;
+//   prefill_tiles 1, or 0 when none of these applies: the prefill kernel (plain bf16 KV, masked
+//     keys at weight 0, chunks in one page: page size a multiple of 64);
 //   otherwise, and with -1: causal row blocks of the stream-K role.
 void resolve_layout(Params& p, int mode, const rpa_shape_t* shape, const rpa_options_t* opt) {
   const int pt = opt->prefill_tiles;
