@@ -1407,6 +1407,7 @@ constexpr int kPfQBase = 2 * kPfBufBytes;    // the tile's Q fragments follow th
 // prefill tiles run in workgroups of eight waves, whose dynamic LDS is eight decode-wave regions
 static_assert(kPfQBase + 8 * kPfQWave <= 8 * kWaveLds, "prefill tile LDS exceeds the workgroup's allocation");
 constexpr int kQueueWord = 16;  // int index of the tile counter in the workspace header
+constexpr int kXcds = 8;        // the co-resident layout's tile queues: one per XCD, words kQueueWord ..+7
 constexpr float kPfCost = 0.45f;  // prefill chunk-step cost in stream-K units (Latin-square search on C3)
 
 struct PfPages {
@@ -2402,9 +2403,45 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
   }
   const int total = (ranked ? nvalid : npairs) * p.Hkv;
   RPA_TL(tl_set(TL_RANKED, tl_clock());)
+  // Tile t (queue order t = rank * Hkv + head) is queued on XCD t % 8, so with Hkv a multiple of 8
+  // every token block of one (sequence, kv head) runs on one XCD and re-reads the causal prefix
+  // its neighbours just fetched from that XCD's L2.  A workgroup takes tiles from its own XCD's
+  // queue; once that is empty, wave 0 reads all eight counters at once (agent-scope loads) and
+  // takes from the queue with the most tiles left, until none has any.
+  const int x0 = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (kXcds - 1));  // XCC_ID
+  bool own_left = true;  // wave 0's view of its own queue
   for (;;) {
     RPA_TL(const long long tl_q = tl_clock();)
-    if (threadIdx.x == 0) *s_tile = atomicAdd(p.err + kQueueWord, 1);
+    if (wv == 0) {
+      int t = total;
+      if (own_left) {
+        int q = 0;
+        if (lane == 0) q = atomicAdd(p.err + kQueueWord + x0, 1);
+        q = uni(q);
+        if (q < (total - x0 + kXcds - 1) / kXcds)
+          t = q * kXcds + x0;
+        else
+          own_left = false;
+      }
+      while (t >= total) {
+        const int x = (x0 + lane) & (kXcds - 1);
+        int left = 0;
+        if (lane < kXcds)
+          left = (total - x + kXcds - 1) / kXcds -
+                 __hip_atomic_load(p.err + kQueueWord + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int key = left > 0 ? (left << 3) | (kXcds - 1 - lane) : -1;  // most left, then nearest
+        int best = -1;
+#pragma unroll
+        for (int i = 0; i < kXcds; ++i) best = max(best, rl(key, i));
+        if (best < 0) break;  // every queue is empty
+        const int bl = kXcds - 1 - (best & (kXcds - 1)), bx = (x0 + bl) & (kXcds - 1);
+        int q = 0;
+        if (lane == 0) q = atomicAdd(p.err + kQueueWord + bx, 1);
+        q = uni(q);
+        if (q < (total - bx + kXcds - 1) / kXcds) t = q * kXcds + bx;
+      }
+      if (lane == 0) *s_tile = t;
+    }
     __syncthreads();
     const int tq = uni(*s_tile);
     __syncthreads();
@@ -3456,7 +3493,7 @@ __device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
   __shared__ float red[3][64][33];    // waves 1..3's o (33: conflict-free row stride)
   __shared__ float redml[3][64][16];  // waves 1..3's (m, l) per row slot
-  if (blockIdx.x == 0 && threadIdx.x == 0) p.err[kQueueWord] = 0;  // prefill tile queue, for the next call
+  if (blockIdx.x == 0 && threadIdx.x < kXcds) p.err[kQueueWord + threadIdx.x] = 0;  // tile queues, for the next call
   if ((int)blockIdx.x >= p.grid * p.HG) {
     const int hb = blockIdx.x - p.grid * p.HG, nheavy = heavy_slots(p.grid) * p.HG * kHeavySlices;
     if (hb < nheavy)
