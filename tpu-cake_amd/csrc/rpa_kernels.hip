@@ -2483,8 +2483,12 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
          tl_set(TL_SETUP, ta.setup); tl_set(TL_LOOP, ta.loop); tl_set(TL_WRITE, ta.write);)
 }
 
-template <int MODE, bool UPG>
+// CO: the co-resident layout's instantiation (p.co set), with the co-resident prefill role; the
+// other instantiations carry the 8-wave prefill role (plain bf16 KV) or none, so the decode-only
+// launches keep the registers of a kernel without the co-resident role.
+template <int MODE, bool UPG, bool CO = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
+  constexpr bool kTiles = CO ? co_tiles<MODE>() : MODE == KV_BF16;  // a prefill-tile role exists
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x (V region, K tile)
   const int lane = threadIdx.x & 63;
   const int wv = uni(threadIdx.x >> 6);
@@ -2533,7 +2537,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (nseq > 64 * kWin) tv = fz ? 0 : uni(p.cu_q_lens[nseq]);
     if (fz) tv = nseq;
     // prefill tiles need the whole metadata in the four windows
-    pf_min = (co_tiles<MODE>() && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
+    pf_min = (kTiles && p.pf_tq > 0 && nseq <= 64 * kWin) ? p.pf_min : 0;
 #pragma unroll
     for (int w = 0; w < kWin; ++w) {
       wsi[w] = SeqInfo{0, 0, 0, 0};
@@ -2563,7 +2567,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   bool any_pf = false;
 #pragma unroll
   for (int w = 0; w < kWin; ++w) any_pf = any_pf || wsi[w].q_len >= pf_min;
-  if (co_tiles<MODE>() && pf_min > 0 && !p.pf_kernel && __ballot(any_pf) != 0) {
+  if (kTiles && pf_min > 0 && !p.pf_kernel && __ballot(any_pf) != 0) {
     // per lane over the four windows, then one wave sum each (skipped when no sequence is a
     // prefill sequence)
     float st = 0.f;
@@ -2588,7 +2592,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       gpre = (int)((float)p.grid * pw / (pw + dw) + 0.5f);
       gpre = gpre < 1 ? 1 : gpre;
       if (W > 0 && gpre > p.grid - 1) gpre = p.grid - 1;
-      if (p.co && gpre > p.grid / 2) gpre = p.grid / 2;  // at most one prefill workgroup per CU
+      if (CO && gpre > p.grid / 2) gpre = p.grid / 2;  // at most one prefill workgroup per CU
       if (gpre > pf_total) gpre = pf_total;
     }
   }
@@ -2599,7 +2603,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ int s_tile;
   bool pf_first;
   int bd;
-  if (co_tiles<MODE>() && p.co) {
+  if constexpr (CO) {
     const int half = p.grid >> 1;
     pf_first = b >= half && b < half + gpre;
     bd = pf_first ? -1 : (b < half ? b : b - gpre);
@@ -2609,8 +2613,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   const int gd = p.grid - gpre;  // stream-K workgroup count
   RPA_TL(tl_set(TL_SCHED, tl_clock()); int tl_role = pf_first ? 1 : 0;)
-  if (co_tiles<MODE>() && pf_first) {
-    if (UPG && p.co)
+  if (kTiles && pf_first) {
+    if constexpr (CO)
       co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
     else if constexpr (MODE == KV_BF16)  // (HG == 8: one K and one V piece per thread per chunk)
       pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
@@ -2710,7 +2714,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   }
   RPA_TL(tl_set(TL_DEC, tl_clock());)
-  if (co_tiles<MODE>() && UPG && p.co && !pf_first && pf_total > 0) {
+  if (CO && !pf_first && pf_total > 0) {
     __syncthreads();  // every wave is done with its stream-K LDS regions
     RPA_TL(tl_role |= 4;)
     co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
@@ -4343,13 +4347,16 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, false>), grid, block, lds, st, p);
   } else if (mode == KV_FP8) {
-    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true>), grid, block, lds, st, p);
+    if (p.co) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true, true>), grid, block, lds, st, p);
+    else if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, false>), grid, block, lds, st, p);
   } else if (mode == KV_BF16_SCALED) {
-    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true>), grid, block, lds, st, p);
+    if (p.co) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true, true>), grid, block, lds, st, p);
+    else if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, false>), grid, block, lds, st, p);
   } else {
-    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true>), grid, block, lds, st, p);
+    if (p.co) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true, true>), grid, block, lds, st, p);
+    else if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, false>), grid, block, lds, st, p);
   }
   hipError_t e = hipGetLastError();
