@@ -211,6 +211,7 @@ struct Params {
   float* pk_acc;               // [2 * pk_grid][256][kD] split-tile partials
   float* pk_ml;                // [2 * pk_grid][256][2]
   struct PkDesc* pk_desc;      // [pk_grid] split tile ending in prefill workgroup b
+  int D;  // head_dim of q, kv_pages and out rows: kD, or a narrower one (rpa_attn_kernel NW)
 };
 
 // A co-resident prefill tile split into nparts chunk ranges: its partials are in slots slot0 ..
@@ -387,9 +388,10 @@ __device__ __forceinline__ int slot_of(int kt, const Params& p) {
 }
 
 // Element index of combined head `comb` of key `kt` stored in page `pg`.
-__device__ __forceinline__ size_t kv_elem(const Params& p, int pg, int kt, int comb) {
+// D: the pool's head dim (kD everywhere but the narrow decode instantiation).
+__device__ __forceinline__ size_t kv_elem(const Params& p, int pg, int kt, int comb, int D = kD) {
   return (((size_t)pg * (size_t)p.S + (size_t)slot_of(kt, p)) * (size_t)(2 * p.Hkv) + (size_t)comb) *
-         (size_t)kD;
+         (size_t)D;
 }
 
 // Two floats to bf16 (round to nearest even), lo in the low half: one v_cvt_pk_bf16_f32.
@@ -697,7 +699,7 @@ struct UnitAddr {
 };
 
 __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, const Pages& pages, int n, int j,
-                                              int wv, int& err) {
+                                              int wv, int& err, int D = kD) {
   UnitAddr a;
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
@@ -713,7 +715,7 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
     if (in_seq && !pg_ok) err |= ERR_PAGE;
     pg = pg_ok ? pg : 0;
     a.pg[blk] = pg;
-    a.e[blk] = kv_elem(p, pg, kt, 2 * a.h) + 8 * j;
+    a.e[blk] = kv_elem(p, pg, kt, 2 * a.h, D) + 8 * j;
   }
   // relative-bias table position of the scores this lane holds: row n, keys c*32 + 4j .. +3 (the
   // host keeps every index below 2^31); chunks before the window read the zero head
@@ -726,18 +728,23 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
 }
 
 // which = 0 loads K (combined head 2h), 1 loads V (2h+1, one row of kD further).
+// A narrow pool (D < kD) is read as rows of kD elements from each row's start: the elements past
+// D belong to the next row of the key (zero in Q, so they add nothing to a score; in V they only
+// reach output dims >= D, which are not stored); pieces wholly past D read the row's first piece
+// instead, so no load leaves the key's rows.
 template <int MODE, bool UPG>
-__device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, int which, HalfRegs<MODE>& r) {
+__device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, int which, HalfRegs<MODE>& r,
+                                          int D = kD) {
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
-    const size_t e = a.e[blk] + (size_t)which * kD;
+    const size_t e = a.e[blk] + (size_t)which * D;
     if constexpr (MODE == KV_BF16_BIAS) {
       if (which == 0) r.bias[blk] = *(const f32x4*)(p.rel_bias + a.bias_at + 16 * blk);  // aligned
     }
     if constexpr (MODE == KV_FP8) {
       const uint8_t* kp = p.kv + e + a.j8;  // bytes 16j (+64) of the row: kdim<KV_FP8>
 #pragma unroll
-      for (int i = 0; i < 2; ++i) r.w[blk][i] = *(const u32x4*)(kp + 64 * i);
+      for (int i = 0; i < 2; ++i) r.w[blk][i] = *(const u32x4*)(kp + (D == kD || 2 * a.j8 + 64 * i < D ? 64 * i : 0));
       // the raw per-(page, head) scale; multiplied in where it is used (to_bf16x8), a step later,
       // so that nothing waits for this load here.  UPG: one page per unit, whose K and V scales
       // (adjacent) come with K in one 8-byte load
@@ -757,7 +764,7 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
     } else {
       const uint16_t* kp = (const uint16_t*)p.kv + e;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) r.w[blk][s] = *(const u32x4*)(kp + 32 * s);
+      for (int s = 0; s < 4; ++s) r.w[blk][s] = *(const u32x4*)(kp + (D == kD || a.j8 + 32 * s < D ? 32 * s : 0));
     }
   }
 }
@@ -768,7 +775,7 @@ __device__ __forceinline__ void load_half(const Params& p, const UnitAddr& a, in
 // with its queries (once per row block).
 template <int MODE>
 __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, int j, int wv, bf16x8 q[4],
-                                       uint32_t* rst = nullptr) {
+                                       uint32_t* rst = nullptr, int D = kD) {
   const bool live = x.nch > 0;
   int row = x.rb * ROW_BLOCK + n;
   if (!(live && row < x.q_len * p.G)) row = 0;
@@ -776,9 +783,14 @@ __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, 
   const int g = row - tok * p.G;
   const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)(x.h * p.HG + wv) * p.G : 0;
   const size_t qrow = (size_t)tok * p.Hq + base + g;
-  const uint16_t* qp = p.q + qrow * kD;
+  const uint16_t* qp = p.q + qrow * D;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) q[s] = __builtin_bit_cast(bf16x8, *(const u32x4*)(qp + kdim<MODE>(j, s)));
+  for (int s = 0; s < 4; ++s) {  // a narrow row's dims past D are zero
+    const int d = kdim<MODE>(j, s);
+    const bool in = D == kD || d < D;
+    const u32x4 w = *(const u32x4*)(qp + (in ? d : 0));
+    q[s] = __builtin_bit_cast(bf16x8, in ? w : u32x4{0u, 0u, 0u, 0u});
+  }
   if constexpr (MODE == KV_BF16_FUSED) {
     if (rst && p.rel_states) {
       const uint2 sv = *(const uint2*)(p.rel_states + qrow * kRelRows + 4 * j);
@@ -997,7 +1009,7 @@ template <int MODE, bool UPG>
 __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, const HalfRegs<MODE>& kr,
                                              const HalfRegs<MODE>& vr, bf16x8 q[4], const Cursor& nx,
                                              const UnitAddr& nx_addr, HalfRegs<MODE>& v_next, RowState& st,
-                                             uint8_t* vt, int n, int j, int wv) {
+                                             uint8_t* vt, int n, int j, int wv, int D = kD) {
   // S = K Q^T for the two 16-key blocks
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1021,8 +1033,8 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       *(u32x4*)(vt + (16 * blk + n) * kVRow + 2 * kdim<MODE>(j, s)) = to_bf16x8<MODE, UPG>(vr, p, blk, s, 1, vs);
-  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q);  // a new row block's queries (as in compute_unit_line)
-  load_half<MODE, UPG>(p, nx_addr, 1, v_next);
+  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, nullptr, D);  // a new row block's queries (as in compute_unit_line)
+  load_half<MODE, UPG>(p, nx_addr, 1, v_next, D);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias_of(kr), st, j);
 
@@ -1046,7 +1058,7 @@ __device__ __forceinline__ void begin_row_block(const Params& p, const Cursor& x
 }
 
 __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& x, RowState& st, int b,
-                                                 bool complete, int n, int j, int wv) {
+                                                 bool complete, int n, int j, int wv, int D = kD) {
   const float lt = rows4_sum(st.l);
   if (complete) {
     const int row = x.rb * ROW_BLOCK + n;
@@ -1054,13 +1066,13 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
       const int tok = row / p.G;
       const int head = (x.h * p.HG + wv) * p.G + (row - tok * p.G);
       const float inv = 1.f / lt;
-      uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * kD + 4 * j;
+      uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * D + 4 * j;
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         u32x2 w;
         w[0] = pack_bf16x2(st.acc[d][0] * inv, st.acc[d][1] * inv);
         w[1] = pack_bf16x2(st.acc[d][2] * inv, st.acc[d][3] * inv);
-        *(u32x2*)(op + 16 * d) = w;
+        if (D == kD || 16 * d + 4 * j < D) *(u32x2*)(op + 16 * d) = w;  // a narrow row stores dims < D
       }
     }
   } else {
@@ -1111,7 +1123,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
                                      long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
                                      Pages& pg_nxt, const HalfRegs<MODE>& k_cur, const HalfRegs<MODE>& v_cur,
                                      HalfRegs<MODE>& k_nxt, HalfRegs<MODE>& v_nxt, bf16x8 q[4], RowState& st,
-                                     uint8_t* vt, int& err, const Partition& pt, int wv) {
+                                     uint8_t* vt, int& err, const Partition& pt, int wv, int D = kD) {
   // Prefetch, oldest-needed first: page ids two units ahead, then the next unit's K (its page
   // ids arrived a step ago); its queries and V follow inside compute_unit as registers free up.
   // Every buffer is redefined each step.
@@ -1121,18 +1133,18 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
   else
     ahead.nch = 0;
   const Pages pg_ahead = load_pages<MODE, UPG>(p, ahead, n);
-  const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, wv, err);
+  const UnitAddr nx_addr = unit_addr(p, nxt, pg_nxt, n, j, wv, err, D);
   // keep the workgroup's waves (the kv heads of one group) in step, so the heads' slices of the
   // same keys reach the memory system together
   __syncthreads();
-  load_half<MODE, UPG>(p, nx_addr, 0, k_nxt);
+  load_half<MODE, UPG>(p, nx_addr, 0, k_nxt, D);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit<MODE, UPG>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j, wv);
+  compute_unit<MODE, UPG>(p, cur, k_cur, v_cur, q, nxt, nx_addr, v_nxt, st, vt, n, j, wv, D);
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
-    finish_row_block(p, cur, st, b, complete, n, j, wv);
+    finish_row_block(p, cur, st, b, complete, n, j, wv, D);
     if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
 
@@ -1179,11 +1191,12 @@ struct LineAddr {
 
 template <int MODE>
 __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, const Pages& pages, int lane, int n,
-                                              int j, int wv, int& err) {
-  const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err);  // page checks, head, bias position
+                                              int j, int wv, int& err, int D = kD) {
+  const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err, D);  // page checks, head, bias position
   LineAddr a;
   const bool live = x.nch > 0;
-  a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h) + 8 * (lane & 15);
+  // (a narrow pool's pieces wholly past D read the row's first piece, as in load_half)
+  a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h, D) + (D == kD || 8 * (lane & 15) < D ? 8 * (lane & 15) : 0);
   const int k = live ? x.kv_len - 1 - x.key0() : 0;
   a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
   a.bias_at = u.bias_at;
@@ -1201,9 +1214,10 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
 
 // which = 0: K rows (combined head 2h), 1: V rows (2h+1).
 template <int MODE>
-__device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, int lane, int which, LineRegs& r) {
-  const uint16_t* kv = (const uint16_t*)p.kv + a.e0 + (size_t)which * kD;
-  const size_t row = (size_t)(2 * p.Hkv) * kD;
+__device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, int lane, int which, LineRegs& r,
+                                           int D = kD) {
+  const uint16_t* kv = (const uint16_t*)p.kv + a.e0 + (size_t)which * D;
+  const size_t row = (size_t)(2 * p.Hkv) * D;
   const uint16_t* nw = nullptr;
   if constexpr (MODE == KV_BF16_FUSED) nw = (which ? p.new_v : p.new_k) + a.newoff;
 #pragma unroll
@@ -1316,7 +1330,7 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
                                                   bf16x8 q[4], uint32_t rst[2], const Cursor& nx,
                                                   const LineAddr& nx_addr,
                                                   RowState& st, uint8_t* vt, const uint8_t* kt, int lane, int n,
-                                                  int j, int wv) {
+                                                  int j, int wv, int D = kD) {
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -1334,8 +1348,8 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
   // a new row block's queries (else q already holds its rows), issued after the wait for this
   // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
   // issued before it they would make that wait also retire the next unit's K
-  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst);
-  load_lines<MODE>(p, nx_addr, lane, 1, v);
+  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst, D);
+  load_lines<MODE>(p, nx_addr, lane, 1, v, D);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
 
@@ -1354,21 +1368,21 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
                                           Pages& pg_nxt, LineRegs& k, LineRegs& v, f32x4 bias[2], bf16x8 q[4],
                                           uint32_t rst[2], RowState& st, uint8_t* vt, uint8_t* kt, uint8_t* rs,
                                           int& err,
-                                          const Partition& pt, int wv) {
+                                          const Partition& pt, int wv, int D = kD) {
   Cursor ahead = nxt;
   if (u + 2 < u1)
     advance<MODE>(p, nseq, lane, win, ahead, err);
   else
     ahead.nch = 0;
   const Pages pg_ahead = load_pages<MODE, UPG>(p, ahead, n);
-  const LineAddr nx_addr = line_addr<MODE>(p, nxt, pg_nxt, lane, n, j, wv, err);
+  const LineAddr nx_addr = line_addr<MODE>(p, nxt, pg_nxt, lane, n, j, wv, err, D);
   __syncthreads();
-  load_lines<MODE>(p, nx_addr, lane, 0, k);  // the next unit's K (this unit's K is in the tile)
+  load_lines<MODE>(p, nx_addr, lane, 0, k, D);  // the next unit's K (this unit's K is in the tile)
   LineBias bias_nx;
   load_line_bias<MODE>(p, nxt, nx_addr, lane, n, j, wv, bias_nx);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit_line<MODE>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv);
+  compute_unit_line<MODE>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D);
   // The next unit's K goes to the tile before a row block's finish stores: its wait then counts
   // the same younger operations (the next unit's V) on every path.  Issued before it, the stores
   // made that wait also retire most of the V just loaded on the steps that end a row block.
@@ -1376,7 +1390,7 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
-    finish_row_block(p, cur, st, b, complete, n, j, wv);
+    finish_row_block(p, cur, st, b, complete, n, j, wv, D);
     if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
   line_bias_values<MODE>(p, nxt, bias_nx, rst, rs, lane, n, j, bias);
@@ -2486,9 +2500,11 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
 // CO: the co-resident layout's instantiation (p.co set), with the co-resident prefill role; the
 // other instantiations carry the 8-wave prefill role (plain bf16 KV) or none, so the decode-only
 // launches keep the registers of a kernel without the co-resident role.
-template <int MODE, bool UPG, bool CO = false>
+// NW: a narrow head dim (p.D < kD; decode role only, every row through stream-K).
+template <int MODE, bool UPG, bool CO = false, bool NW = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
-  constexpr bool kTiles = CO ? co_tiles<MODE>() : MODE == KV_BF16;  // a prefill-tile role exists
+  constexpr bool kTiles = NW ? false : CO ? co_tiles<MODE>() : MODE == KV_BF16;  // a prefill-tile role exists
+  const int D = NW ? p.D : kD;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x (V region, K tile)
   const int lane = threadIdx.x & 63;
   const int wv = uni(threadIdx.x >> 6);
@@ -2673,11 +2689,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // K, bias, queries, V: the loop's order (vmcnt retires in order, and the compiler
         // counts each wait for the least favourable path into it, this prologue included)
         {
-          const LineAddr a0 = line_addr<MODE>(p, cur, pg_cur, lane, n, j, wv, err);
-          load_lines<MODE>(p, a0, lane, 0, k);
+          const LineAddr a0 = line_addr<MODE>(p, cur, pg_cur, lane, n, j, wv, err, D);
+          load_lines<MODE>(p, a0, lane, 0, k, D);
           load_line_bias<MODE>(p, cur, a0, lane, n, j, wv, bias_in);
-          load_q<MODE>(p, cur, n, j, wv, q, rst);
-          load_lines<MODE>(p, a0, lane, 1, v);
+          load_q<MODE>(p, cur, n, j, wv, q, rst, D);
+          load_lines<MODE>(p, a0, lane, 1, v, D);
         }
         RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
         store_k_tile<MODE>(p, k, kt, lane);
@@ -2686,17 +2702,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         long long u = u0;
         for (;;) {
           step_line<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, k, v, bias, q, rst, st, vt,
-                               kt, rs, err, pt, wv);
+                               kt, rs, err, pt, wv, D);
           if (++u >= u1) break;
         }
       } else {
         HalfRegs<MODE> ka, va, kb, vb;
         bf16x8 q[4];
         {  // K, queries, V: the loop's order (as above)
-          const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err);
-          load_half<MODE, UPG>(p, a0, 0, ka);
-          load_q<MODE>(p, cur, n, j, wv, q);
-          load_half<MODE, UPG>(p, a0, 1, va);
+          const UnitAddr a0 = unit_addr(p, cur, pg_cur, n, j, wv, err, D);
+          load_half<MODE, UPG>(p, a0, 0, ka, D);
+          load_q<MODE>(p, cur, n, j, wv, q, nullptr, D);
+          load_half<MODE, UPG>(p, a0, 1, va, D);
         }
         RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
         RowState st;
@@ -2704,10 +2720,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         long long u = u0;
         for (;;) {
           step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, ka, va, kb, vb, q, st, vt, err, pt,
-                          wv);
+                          wv, D);
           if (++u >= u1) break;
           step<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, kb, vb, ka, va, q, st, vt, err, pt,
-                          wv);
+                          wv, D);
           if (++u >= u1) break;
         }
       }
@@ -2722,7 +2738,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
     tv = tv < 0 ? 0 : (tv > p.T ? p.T : tv);
-    const size_t first = (size_t)tv * p.Hq * kD / 8, last = (size_t)p.T * p.Hq * kD / 8;
+    const size_t first = (size_t)tv * p.Hq * D / 8, last = (size_t)p.T * p.Hq * D / 8;
     u32x4* o = (u32x4*)p.out;
     for (size_t k = first + (size_t)b * blockDim.x + threadIdx.x; k < last; k += (size_t)p.grid * blockDim.x)
       o[k] = u32x4{0u, 0u, 0u, 0u};
@@ -3336,7 +3352,7 @@ __device__ __forceinline__ void merge_waves_store(const Params& p, const SplitDe
       u32x2 w2;
       w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
       w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
-      *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * kD + c4) = w2;
+      if (c4 < p.D) *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * p.D + c4) = w2;  // dims < D
     }
   }
   __syncthreads();  // red / redml free for a next merge
@@ -3559,7 +3575,7 @@ __global__ __launch_bounds__(256) void rpa_gather_kernel(Params p, uint8_t* dens
     if (threadIdx.x == 0) atomicOr(p.err, ERR_KVLEN);
     return;
   }
-  const int row_bytes = 2 * p.Hkv * kD * elem;
+  const int row_bytes = 2 * p.Hkv * p.D * elem;
   const int vec = row_bytes / 16;
   for (long long t = 0; t < L; ++t) {
     int kt = (int)t;
@@ -3568,7 +3584,7 @@ __global__ __launch_bounds__(256) void rpa_gather_kernel(Params p, uint8_t* dens
       if (threadIdx.x == 0) atomicOr(p.err, ERR_PAGE);
       continue;
     }
-    const u32x4* src = (const u32x4*)(p.kv + kv_elem(p, pg, kt, 0) * elem);
+    const u32x4* src = (const u32x4*)(p.kv + kv_elem(p, pg, kt, 0, p.D) * elem);
     u32x4* dst = (u32x4*)(dense + (size_t)(row0 + t) * row_bytes);
     for (int v = threadIdx.x; v < vec; v += blockDim.x) dst[v] = src[v];
   }
@@ -3700,8 +3716,14 @@ size_t workspace_bytes_for(const DeviceInfo& d) { return ws_layout(d).total; }
 
 int check_shape(const rpa_shape_t* s) {
   if (!s) return fail(RPA_E_INVALID, "shape is NULL");
-  if (s->head_dim != kD)
-    return fail(RPA_E_UNSUPPORTED, "head_dim " + std::to_string(s->head_dim) + " is not built (only 128)");
+  // head dims up to 128: 128 itself, and narrower ones read as 128-element rows (the decode role's
+  // narrow instantiation); a 16-byte piece of a row is then wholly inside or past the head dim
+  if (s->head_dim > kD)
+    return fail(RPA_E_UNSUPPORTED, "head_dim " + std::to_string(s->head_dim) + " is not built (at most 128)");
+  if (s->head_dim != kD && (s->kv_dtype == RPA_KV_FP8_E4M3 ? s->head_dim < 64 || s->head_dim % 16
+                                                             : s->head_dim < 32 || s->head_dim % 8))
+    return fail(RPA_E_UNSUPPORTED, "head_dim " + std::to_string(s->head_dim) +
+                                       " is not built (a multiple of 8 in [32, 128]; fp8: of 16 in [64, 128])");
   if (s->num_tokens < 0 || s->num_q_heads <= 0 || s->num_kv_heads <= 0 || s->total_pages <= 0 ||
       s->page_size <= 0 || s->max_num_seqs < 0 || s->pages_per_seq <= 0)
     return fail(RPA_E_INVALID, "non-positive dimension in shape");
@@ -3928,6 +3950,7 @@ Params base_params(const rpa_shape_t* s) {
   p.PPS = s->pages_per_seq;
   p.HG = heads_per_group(p.Hkv);
   p.NG = p.Hkv / p.HG;
+  p.D = s->head_dim;
   return p;
 }
 
@@ -4211,6 +4234,7 @@ int nominal_per_cu(int hg, size_t lds) {
 //     keys at weight 0, chunks in one page: page size a multiple of 64);
 //   otherwise, and with -1: causal row blocks of the stream-K role.
 void resolve_layout(Params& p, int mode, const rpa_shape_t* shape, const rpa_options_t* opt) {
+  if (p.D != kD) return;  // a narrow head dim: every row through stream-K
   const int pt = opt->prefill_tiles;
   const bool bf = mode == KV_BF16 && p.skip_masked;
   const bool co_mode = mode == KV_BF16 || mode == KV_BF16_SCALED || mode == KV_FP8;  // any mask value
@@ -4346,6 +4370,17 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   } else if (mode == KV_BF16_BIAS) {
     if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, false>), grid, block, lds, st, p);
+  } else if (p.D != kD) {  // a narrow head dim (decode role only)
+    if (mode == KV_FP8) {
+      if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true, false, true>), grid, block, lds, st, p);
+      else hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, false, false, true>), grid, block, lds, st, p);
+    } else if (mode == KV_BF16_SCALED) {
+      if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true, false, true>), grid, block, lds, st, p);
+      else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, false, false, true>), grid, block, lds, st, p);
+    } else {
+      if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true, false, true>), grid, block, lds, st, p);
+      else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, false, false, true>), grid, block, lds, st, p);
+    }
   } else if (mode == KV_FP8) {
     if (p.co) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true, true>), grid, block, lds, st, p);
     else if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true>), grid, block, lds, st, p);
