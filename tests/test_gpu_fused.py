@@ -92,6 +92,22 @@ def test_bias_windows_and_launch_forms(cuda, hq, hkv, page, lens, rel_dim, exten
     _run_and_check(inp)
 
 
+@pytest.mark.parametrize("hq,hkv,d,page,lens,rel_dim", [
+    # one attention launch at head dims below 128 (queries, new rows and output that wide; the
+    # cache rows 128, zero past d)
+    (32, 8, 64, 64, [1, 31, 32, 33, 96, 700, 2048], 16),
+    (16, 4, 96, 32, [2, 33, 64, 65, 1000], 0),
+    (16, 4, 32, 64, [5, 64, 65, 300, 1500], 16),
+    (8, 2, 120, 128, [3, 129, 257, 900], 16),
+])
+def test_one_launch_narrow_head_dims(cuda, hq, hkv, d, page, lens, rel_dim):
+    _say(f"fused one launch d={d} hq={hq} hkv={hkv} page={page} R={rel_dim}")
+    pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(d * 3 + page + rel_dim, nseq=len(lens), hq=hq, hkv=hkv, d=d, page_size=page,
+                               pool_pages=pool, lengths=lens, rel_dim=rel_dim, extent=512)
+    _run_and_check(inp)
+
+
 def test_random_one_launch_sweep(cuda):
     """Seeded random shapes of the one-launch form (page 32/64/128, GQA 1-8, Hkv 1-16, R 0 or 16,
     E a multiple of 8 from 8 to 600, lengths 1-3000 incl. page and chunk edges) against the oracle

@@ -1204,9 +1204,9 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
   a.newoff = 0;
   if constexpr (MODE == KV_BF16_FUSED) {
     // the step's new token (key kv_len-1) is not in the cache yet: its rows come from new_k/new_v
-    if (live && k < KV_CHUNK) {
+    if (live && k < KV_CHUNK) {  // (rows of p.D elements; pieces past them read the first piece)
       a.knew = k;
-      a.newoff = ((size_t)x.i * p.Hkv + u.h) * kD + 8 * (lane & 15);
+      a.newoff = ((size_t)x.i * p.Hkv + u.h) * p.D + (8 * (lane & 15) < p.D ? 8 * (lane & 15) : 0);
     }
   }
   return a;
@@ -1330,7 +1330,7 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
                                                   bf16x8 q[4], uint32_t rst[2], const Cursor& nx,
                                                   const LineAddr& nx_addr,
                                                   RowState& st, uint8_t* vt, const uint8_t* kt, int lane, int n,
-                                                  int j, int wv, int D = kD) {
+                                                  int j, int wv, int D = kD, int Dq = kD) {
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -1348,7 +1348,7 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
   // a new row block's queries (else q already holds its rows), issued after the wait for this
   // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
   // issued before it they would make that wait also retire the next unit's K
-  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst, D);
+  if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst, Dq);
   load_lines<MODE>(p, nx_addr, lane, 1, v, D);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
@@ -1382,7 +1382,9 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
   load_line_bias<MODE>(p, nxt, nx_addr, lane, n, j, wv, bias_nx);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
-  compute_unit_line<MODE>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D);
+  // the fused step's queries and output rows are p.D wide (its cache rows kD)
+  const int Dq = MODE == KV_BF16_FUSED ? p.D : D;
+  compute_unit_line<MODE>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D, Dq);
   // The next unit's K goes to the tile before a row block's finish stores: its wait then counts
   // the same younger operations (the next unit's V) on every path.  Issued before it, the stores
   // made that wait also retire most of the V just loaded on the steps that end a row block.
@@ -1390,7 +1392,7 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
-    finish_row_block(p, cur, st, b, complete, n, j, wv, D);
+    finish_row_block(p, cur, st, b, complete, n, j, wv, Dq);
     if (!complete && !st.started_here && last_of_rb && lane == 0) write_split_desc(p, cur, u, pt, b, wv);
   }
   line_bias_values<MODE>(p, nxt, bias_nx, rst, rs, lane, n, j, bias);
@@ -2692,7 +2694,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const LineAddr a0 = line_addr<MODE>(p, cur, pg_cur, lane, n, j, wv, err, D);
           load_lines<MODE>(p, a0, lane, 0, k, D);
           load_line_bias<MODE>(p, cur, a0, lane, n, j, wv, bias_in);
-          load_q<MODE>(p, cur, n, j, wv, q, rst, D);
+          load_q<MODE>(p, cur, n, j, wv, q, rst, MODE == KV_BF16_FUSED ? p.D : D);
           load_lines<MODE>(p, a0, lane, 1, v, D);
         }
         RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
@@ -3456,10 +3458,10 @@ __device__ __forceinline__ void fused_store_token(const Params& p, int s) {
   }
   uint16_t* rows = (uint16_t*)p.kv + ((size_t)page * p.S + pos % p.S) * (size_t)(2 * p.Hkv) * kD;
   const int n = 2 * p.Hkv * kD;
-  for (int i = 8 * threadIdx.x; i < n; i += 8 * blockDim.x) {
+  for (int i = 8 * threadIdx.x; i < n; i += 8 * blockDim.x) {  // new rows of p.D elements, zeros past them
     const int r = i / kD, d = i - r * kD;
-    const uint16_t* src = ((r & 1) ? p.new_v : p.new_k) + ((size_t)s * p.Hkv + (r >> 1)) * kD + d;
-    *(u32x4*)(rows + i) = *(const u32x4*)src;
+    const uint16_t* src = ((r & 1) ? p.new_v : p.new_k) + ((size_t)s * p.Hkv + (r >> 1)) * p.D + d;
+    *(u32x4*)(rows + i) = d < p.D ? *(const u32x4*)src : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -4197,6 +4199,7 @@ struct FusedInline {
   const uint16_t* rel_states;  // nullptr: no relative bias
   const uint16_t* rel_proj;
   int rel_extent;
+  int head_dim;  // of queries, new K/V rows and the output (the cache rows are kD wide)
 };
 
 int check_options(const rpa_options_t* opt) {
@@ -4336,6 +4339,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     p.rel_states = fz->rel_states;
     p.rel_proj = fz->rel_states ? fz->rel_proj : d.zero_proj;
     p.rel_extent = fz->rel_states ? fz->rel_extent : 8;
+    p.D = fz->head_dim;  // (the cache rows keep kD: the kernel's row strides stay kD)
   } else if (rel_bias) {
     if (shape->kv_dtype != RPA_KV_BF16 || kv_scales || opt->has_k_scale || opt->has_v_scale || rel_extent <= 0)
       return fail(RPA_E_INVALID, "a relative bias needs bf16 kv_pages without scales and a positive extent");
@@ -4615,11 +4619,12 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
   uint8_t* ws = (uint8_t*)workspace;
   hipStream_t st = (hipStream_t)stream;
   // One attention launch (metadata, new token and relative bias handled in the kernel, the token
-  // stored by the combine launch) for full 128-dim heads on the full-line path with aligned
-  // tensors and a 16-wide relative projection; the prep launch below otherwise.
+  // stored by the combine launch) on the full-line path with aligned tensors, head dims that are
+  // multiples of 8 in [32, 128] (queries, new rows and the output of that width, the cache rows
+  // 128) and a 16-wide relative projection; the prep launch below otherwise.
   const bool aligned = ((uintptr_t)queries | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)cache |
                         (uintptr_t)relative_states | (uintptr_t)relative_projection) % 16 == 0;
-  if (f->head_dim == kD && f->page_size % KV_CHUNK == 0 && aligned &&
+  if (f->head_dim >= 32 && f->head_dim % 8 == 0 && f->page_size % KV_CHUNK == 0 && aligned &&
       (f->relative_dim == 0 || (f->relative_dim == kRelRows && f->relative_extent % 8 == 0))) {
     const rpa_shape_t rs = fused_rpa_shape(f);
     rpa_options_t o;
@@ -4634,6 +4639,7 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
     fi.rel_states = f->relative_dim > 0 ? (const uint16_t*)relative_states : nullptr;
     fi.rel_proj = f->relative_dim > 0 ? (const uint16_t*)relative_projection : nullptr;
     fi.rel_extent = f->relative_dim > 0 ? f->relative_extent : 0;
+    fi.head_dim = f->head_dim;
     return launch_rpa(&rs, &o, queries, cache, nullptr, kv_lens, page_indices, nullptr, nullptr, out, workspace,
                       workspace_bytes, stream, nullptr, nullptr, nullptr, 0, &fi);
   }
