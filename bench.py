@@ -373,9 +373,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2w", "c3f", "c5t", "c2d64", "inkling"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "c2w", "c3f", "c5t", "c2d64", "c2d256", "inkling"],
                     help="c1..c5: the RPA operator configurations; c2w: C2 with a 512-key sliding window; "
-                         "c3f: C3's batch over an fp8 pool; c5t: C5 with one 131072-key sequence; c2d64: C2 at head_dim 64; "
+                         "c3f: C3's batch over an fp8 pool; c5t: C5 with one 131072-key sequence; c2d64 / c2d256: C2 at head_dim 64 / 256; "
                          "inkling: the fused decode step (KV-cache write + relative-bias attention)")
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--rotate-bytes", type=float, default=2.0e9,

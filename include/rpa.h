@@ -45,8 +45,8 @@ typedef struct rpa_shape {
   int32_t num_tokens;    /* T = q.shape[0] (max_num_batched_tokens) */
   int32_t num_q_heads;   /* Hq */
   int32_t num_kv_heads;  /* Hkv; kv_pages.shape[2] == 2*Hkv */
-  int32_t head_dim;      /* D: 128, or a multiple of 8 in [32, 128) (fp8: of 16 in [64, 128)),
-                            whose rows run through the decode role only */
+  int32_t head_dim;      /* D: 128; a multiple of 8 in [32, 128) (fp8: of 16 in [64, 128)); or
+                            256 -- the last two run every row through the decode role */
   int32_t total_pages;   /* P = kv_pages.shape[0] */
   int32_t page_size;     /* S = kv_pages.shape[1] */
   int32_t max_num_seqs;  /* N_max = page_indices.shape[0] */

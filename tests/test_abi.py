@@ -77,9 +77,9 @@ def _shape(**kw):
     return _lib.RpaShape(**base)
 
 
-@pytest.mark.parametrize("head_dim,kv_dtype", [(256, 0), (192, 0), (24, 0), (36, 0), (48, 1), (72, 1)])
+@pytest.mark.parametrize("head_dim,kv_dtype", [(512, 0), (192, 0), (24, 0), (36, 0), (48, 1), (72, 1)])
 def test_unsupported_head_dim_rejected_before_launch(lib, head_dim, kv_dtype):
-    # built: 128, and narrower multiples of 8 in [32, 128] (fp8: multiples of 16 in [64, 128])
+    # built: 128, 256, and narrower multiples of 8 in [32, 128] (fp8: multiples of 16 in [64, 128])
     opts = _lib.RpaOptions(sm_scale=1.0)
     rc = lib.rpa_ragged_paged_attention(ctypes.byref(_shape(head_dim=head_dim, kv_dtype=kv_dtype)),
                                         ctypes.byref(opts), *([None] * 9), 0, None)
@@ -87,7 +87,8 @@ def test_unsupported_head_dim_rejected_before_launch(lib, head_dim, kv_dtype):
     assert f"head_dim {head_dim}".encode() in lib.rpa_last_error()
 
 
-@pytest.mark.parametrize("head_dim,kv_dtype", [(32, 0), (64, 0), (96, 0), (120, 0), (64, 1), (112, 1)])
+@pytest.mark.parametrize("head_dim,kv_dtype", [(32, 0), (64, 0), (96, 0), (120, 0), (64, 1), (112, 1), (256, 0),
+                                               (256, 1)])
 def test_narrow_head_dims_pass_the_shape_check(lib, head_dim, kv_dtype):
     # the shape check accepts them: the call then stops at the missing workspace, before any launch
     opts = _lib.RpaOptions(sm_scale=1.0)

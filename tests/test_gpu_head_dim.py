@@ -1,6 +1,7 @@
-"""GPU parity for head dims below 128 (the decode role's narrow instantiation): C2-shaped batches,
-fp8 pools, prefill rows, windows and soft caps, short pages, GQA groups and split row blocks,
-against the CPU oracle at the bar of the 128-dim tests; the page-table gather bit-exact."""
+"""GPU parity for head dims other than 128 (the decode role's NW instantiation: narrower heads read
+as 128-element rows, 256-dim heads as two 128-dim halves in paired waves): C2-shaped batches, fp8
+pools, prefill rows, windows and soft caps, short pages, GQA groups and split row blocks, against
+the CPU oracle at the bar of the 128-dim tests; the page-table gather bit-exact."""
 
 import sys
 
@@ -43,19 +44,20 @@ def _c2_shaped(head_dim, kv_dtype="bf16", seed=7):
                        head_dim=head_dim, page_size=64, seed=seed, kv_dtype=kv_dtype)
 
 
-@pytest.mark.parametrize("head_dim", [64, 96, 32])
+@pytest.mark.parametrize("head_dim", [64, 96, 32, 256])
 def test_c2_shaped_decode(cuda, head_dim):
     _say(f"C2-shaped decode, head_dim {head_dim}")
     _check(_c2_shaped(head_dim))
 
 
-def test_c2_shaped_fp8_decode(cuda):
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_c2_shaped_fp8_decode(cuda, head_dim):
     # fp8 codes with per-(page, head) scales, against the same-codes oracle
-    _say("C2-shaped fp8 decode, head_dim 64")
-    _check(_c2_shaped(64, kv_dtype="fp8", seed=9))
+    _say(f"C2-shaped fp8 decode, head_dim {head_dim}")
+    _check(_c2_shaped(head_dim, kv_dtype="fp8", seed=9))
 
 
-@pytest.mark.parametrize("head_dim,page", [(64, 64), (64, 16), (32, 16), (96, 24)])
+@pytest.mark.parametrize("head_dim,page", [(64, 64), (64, 16), (32, 16), (96, 24), (256, 64), (256, 16)])
 def test_mixed_batch_prefill_rows(cuda, head_dim, page):
     # prefill rows run as causal stream-K row blocks at these head dims; page sizes that are not a
     # multiple of 32 take the operand-layout path
@@ -64,31 +66,36 @@ def test_mixed_batch_prefill_rows(cuda, head_dim, page):
                        num_kv_heads=4, head_dim=head_dim, page_size=page, seed=11 + head_dim + page))
 
 
-def test_window_soft_cap_and_mask(cuda):
-    _say("head_dim 64: sliding window 512, soft cap 30, finite mask value")
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_window_soft_cap_and_mask(cuda, head_dim):
+    _say(f"head_dim {head_dim}: sliding window 512, soft cap 30, finite mask value")
     case = make_custom(kv_lens=[3000, 800, 5000, 64], q_lens=[1, 32, 1, 1], num_q_heads=32, num_kv_heads=8,
-                       head_dim=64, page_size=64, seed=13)
+                       head_dim=head_dim, page_size=64, seed=13)
     _check(case, sliding_window=512, soft_cap=30.0)
     _check(case, mask_value=-2.5)
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 2), (12, 4), (8, 8)])
-def test_gqa_groups(cuda, hq, hkv):
-    _say(f"head_dim 64, Hq {hq} / Hkv {hkv}")
+@pytest.mark.parametrize("head_dim,hq,hkv", [(64, 8, 2), (64, 12, 4), (64, 8, 8), (256, 8, 1), (256, 9, 3),
+                                             (256, 16, 16)])
+def test_gqa_groups(cuda, head_dim, hq, hkv):
+    # 256: one kv head (a workgroup of its two halves), three (six halves), sixteen (two groups)
+    _say(f"head_dim {head_dim}, Hq {hq} / Hkv {hkv}")
     _check(make_custom(kv_lens=[1500, 33, 4000, 700], q_lens=[1, 1, 3, 1], num_q_heads=hq, num_kv_heads=hkv,
-                       head_dim=64, page_size=32, seed=17 + hq))
+                       head_dim=head_dim, page_size=32, seed=17 + hq))
 
 
-def test_long_sequence_split_over_many_workgroups(cuda):
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_long_sequence_split_over_many_workgroups(cuda, head_dim):
     # one 60000-key sequence over most of the grid (a heavy merge) beside short ones
-    _say("head_dim 64, a 60000-key sequence")
+    _say(f"head_dim {head_dim}, a 60000-key sequence")
     _check(make_custom(kv_lens=[60000, 40, 1, 3000], q_lens=[1, 1, 1, 1], num_q_heads=32, num_kv_heads=8,
-                       head_dim=64, page_size=64, seed=19))
+                       head_dim=head_dim, page_size=64, seed=19))
 
 
-def test_gather_bit_exact(cuda):
-    _say("head_dim 64 gather probe")
-    case = make_custom(kv_lens=[100, 7, 300], q_lens=[1, 1, 1], num_q_heads=8, num_kv_heads=2, head_dim=64,
+@pytest.mark.parametrize("head_dim", [64, 256])
+def test_gather_bit_exact(cuda, head_dim):
+    _say(f"head_dim {head_dim} gather probe")
+    case = make_custom(kv_lens=[100, 7, 300], q_lens=[1, 1, 1], num_q_heads=8, num_kv_heads=2, head_dim=head_dim,
                        page_size=16, seed=21)
     d = ops.case_to_device(case, "cuda")
     dense = ops.gather_kv(d["kv_pages"], d["kv_lens"], d["page_indices"], d["num_seqs"])

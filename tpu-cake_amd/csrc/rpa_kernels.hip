@@ -61,6 +61,9 @@ namespace {
 constexpr int kD = 128;          // head_dim built
 constexpr int kVRow = kD * 2 + 32;            // a 32-key V chunk as key rows of 288 bytes (conflict-free transposing reads)
 constexpr int kVtBytes_ = KV_CHUNK * kVRow;  // one wave's V region (prefill tiles lay their buffers over these)
+constexpr int kKtRow = kD * 2 + 16;            // the full-line path's K tile: key rows of 272 bytes
+constexpr int kKtBytes = KV_CHUNK * kKtRow;
+constexpr int kWaveLds = kVtBytes_ + kKtBytes;  // LDS per decode wave: V region + K tile
 constexpr int kMaxWavesPerCU = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.f;  // lazy softmax rescale threshold (log2 units)
@@ -394,6 +397,13 @@ __device__ __forceinline__ size_t kv_elem(const Params& p, int pg, int kt, int c
          (size_t)D;
 }
 
+// Head geometry of the decode role: wave wv of kv-head group h computes virtual head v = h * HG +
+// wv.  With 256-dim heads (D = 2 kD) every kv head r is two 128-dim virtual heads v = 2r + half,
+// paired in one workgroup (HG even): half `half` reads dims 128 half .. +127 of the head's K, V,
+// query and output rows and the pair adds its two halves' scores (wide_scores).
+__device__ __forceinline__ int real_head(int v, int D) { return D > kD ? v >> 1 : v; }
+__device__ __forceinline__ int half_offset(int v, int D) { return D > kD ? kD * (v & 1) : 0; }
+
 // Two floats to bf16 (round to nearest even), lo in the low half: one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
@@ -703,7 +713,8 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
   UnitAddr a;
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
-  a.h = live ? x.h * p.HG + wv : 0;
+  const int v = live ? x.h * p.HG + wv : 0;
+  a.h = real_head(v, D);
   a.j8 = 8 * j;
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
@@ -715,7 +726,7 @@ __device__ __forceinline__ UnitAddr unit_addr(const Params& p, const Cursor& x, 
     if (in_seq && !pg_ok) err |= ERR_PAGE;
     pg = pg_ok ? pg : 0;
     a.pg[blk] = pg;
-    a.e[blk] = kv_elem(p, pg, kt, 2 * a.h, D) + 8 * j;
+    a.e[blk] = kv_elem(p, pg, kt, 2 * a.h, D) + half_offset(v, D) + 8 * j;
   }
   // relative-bias table position of the scores this lane holds: row n, keys c*32 + 4j .. +3 (the
   // host keeps every index below 2^31); chunks before the window read the zero head
@@ -781,9 +792,10 @@ __device__ __forceinline__ void load_q(const Params& p, const Cursor& x, int n, 
   if (!(live && row < x.q_len * p.G)) row = 0;
   const int tok = row / p.G;
   const int g = row - tok * p.G;
-  const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)(x.h * p.HG + wv) * p.G : 0;
+  const int v = live ? x.h * p.HG + wv : 0;
+  const size_t base = live ? (size_t)x.q_start * p.Hq + (size_t)real_head(v, D) * p.G : 0;
   const size_t qrow = (size_t)tok * p.Hq + base + g;
-  const uint16_t* qp = p.q + qrow * D;
+  const uint16_t* qp = p.q + qrow * D + half_offset(v, D);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {  // a narrow row's dims past D are zero
     const int d = kdim<MODE>(j, s);
@@ -996,6 +1008,23 @@ __device__ __forceinline__ void read_vt_fragments(const uint8_t* vt, int n, int 
   }
 }
 
+// The two halves of a 256-dim head add their scores: each wave of the pair stores its 16 x 32
+// tile past the workgroup's wave regions and reads its partner's after a workgroup barrier (every
+// wave is at the same unit; the barrier waits for LDS only, the unit's prefetches stay in flight).
+// fp32 a + b is commutative, so both halves hold the same scores.  The previous unit's reads of
+// these slots finished before the step's opening barrier.
+constexpr int kWideSlot = 64 * 2 * 16;  // bytes per wave: 64 lanes x two f32x4
+__device__ __forceinline__ void wide_scores(uint8_t* vt, int wv, int lane, int hg, f32x4& s0, f32x4& s1) {
+  uint8_t* base = vt - wv * kWaveLds + hg * kWaveLds;
+  f32x4* mine = (f32x4*)(base + wv * kWideSlot) + 2 * lane;
+  mine[0] = s0;
+  mine[1] = s1;
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const f32x4* other = (const f32x4*)(base + (wv ^ 1) * kWideSlot) + 2 * lane;
+  s0 += other[0];
+  s1 += other[1];
+}
+
 template <int MODE>
 __device__ __forceinline__ const f32x4* bias_of(const HalfRegs<MODE>& r) {
   if constexpr (MODE == KV_BF16_BIAS) return r.bias;
@@ -1022,6 +1051,7 @@ __device__ __forceinline__ void compute_unit(const Params& p, const Cursor& x, c
     s0 *= ks;
     s1 *= ks;
   }
+  if (D > kD) wide_scores(vt, wv, n + 16 * j, p.HG, s0, s1);
   float vs = 1.f;
   if constexpr (MODE == KV_FP8 && UPG) vs = p.v_scale * kr.sc[1];  // the unit's V scale (one page)
 
@@ -1064,9 +1094,10 @@ __device__ __forceinline__ void finish_row_block(const Params& p, const Cursor& 
     const int row = x.rb * ROW_BLOCK + n;
     if (row < x.q_len * p.G) {
       const int tok = row / p.G;
-      const int head = (x.h * p.HG + wv) * p.G + (row - tok * p.G);
+      const int v = x.h * p.HG + wv;
+      const int head = real_head(v, D) * p.G + (row - tok * p.G);
       const float inv = 1.f / lt;
-      uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * D + 4 * j;
+      uint16_t* op = p.out + ((size_t)(x.q_start + tok) * p.Hq + head) * D + half_offset(v, D) + 4 * j;
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         u32x2 w;
@@ -1167,9 +1198,6 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
 // + LDS probe of both patterns): 104 vs 111 us per 638 MB.  One K and one V register set suffice:
 // K of the next unit lands while this unit's K is read from the tile, V of the next unit is loaded
 // once this unit's V is stored.
-constexpr int kKtRow = kD * 2 + 16;
-constexpr int kKtBytes = KV_CHUNK * kKtRow;
-constexpr int kWaveLds = kVtBytes_ + kKtBytes;
 
 template <int MODE, bool UPG>
 struct LinePath {
@@ -1196,7 +1224,8 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
   LineAddr a;
   const bool live = x.nch > 0;
   // (a narrow pool's pieces wholly past D read the row's first piece, as in load_half)
-  a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h, D) + (D == kD || 8 * (lane & 15) < D ? 8 * (lane & 15) : 0);
+  a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h, D) + half_offset(live ? x.h * p.HG + wv : 0, D) +
+         (D == kD || 8 * (lane & 15) < D ? 8 * (lane & 15) : 0);
   const int k = live ? x.kv_len - 1 - x.key0() : 0;
   a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
   a.bias_at = u.bias_at;
@@ -1339,6 +1368,7 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
     s0 = mfma(a0, q[s], s0);
     s1 = mfma(a1, q[s], s1);
   }
+  if (D > kD) wide_scores(vt, wv, lane, p.HG, s0, s1);
 
   // V as key rows (key 4i + lane/16, kVRow stride), as the K tile; read back transposed below
   wave_lds_fence();
@@ -3349,12 +3379,14 @@ __device__ __forceinline__ void merge_waves_store(const Params& p, const SplitDe
       const float inv = 1.f / L;
       const int grow = d.rb * ROW_BLOCK + row;  // row of the sequence's (token, head) rows
       const int tok = grow / p.G;
-      const int head = (d.h * p.HG + hw) * p.G + (grow - tok * p.G);
+      const int vh = d.h * p.HG + hw;  // virtual head (finish_row_block)
+      const int head = real_head(vh, p.D) * p.G + (grow - tok * p.G);
       // a partial's row n holds O^T column n: dim d at index d (see finish_row_block)
       u32x2 w2;
       w2[0] = pack_bf16x2(v[0] * inv, v[1] * inv);
       w2[1] = pack_bf16x2(v[2] * inv, v[3] * inv);
-      if (c4 < p.D) *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * p.D + c4) = w2;  // dims < D
+      if (c4 < p.D)  // dims < D
+        *(u32x2*)(p.out + ((size_t)(d.q_start + tok) * p.Hq + head) * p.D + half_offset(vh, p.D) + c4) = w2;
     }
   }
   __syncthreads();  // red / redml free for a next merge
@@ -3718,14 +3750,14 @@ size_t workspace_bytes_for(const DeviceInfo& d) { return ws_layout(d).total; }
 
 int check_shape(const rpa_shape_t* s) {
   if (!s) return fail(RPA_E_INVALID, "shape is NULL");
-  // head dims up to 128: 128 itself, and narrower ones read as 128-element rows (the decode role's
-  // narrow instantiation); a 16-byte piece of a row is then wholly inside or past the head dim
-  if (s->head_dim > kD)
-    return fail(RPA_E_UNSUPPORTED, "head_dim " + std::to_string(s->head_dim) + " is not built (at most 128)");
-  if (s->head_dim != kD && (s->kv_dtype == RPA_KV_FP8_E4M3 ? s->head_dim < 64 || s->head_dim % 16
-                                                             : s->head_dim < 32 || s->head_dim % 8))
+  // head dims: 128; narrower ones read as 128-element rows, and 256 as two 128-dim halves (the
+  // decode role's NW instantiation); a 16-byte piece of a narrow row is wholly inside or past it
+  if (s->head_dim > kD && s->head_dim != 2 * kD)
+    return fail(RPA_E_UNSUPPORTED, "head_dim " + std::to_string(s->head_dim) + " is not built (at most 128, or 256)");
+  if (s->head_dim < kD && (s->kv_dtype == RPA_KV_FP8_E4M3 ? s->head_dim < 64 || s->head_dim % 16
+                                                            : s->head_dim < 32 || s->head_dim % 8))
     return fail(RPA_E_UNSUPPORTED, "head_dim " + std::to_string(s->head_dim) +
-                                       " is not built (a multiple of 8 in [32, 128]; fp8: of 16 in [64, 128])");
+                                       " is not built (a multiple of 8 in [32, 128]; fp8: of 16 in [64, 128]; or 256)");
   if (s->num_tokens < 0 || s->num_q_heads <= 0 || s->num_kv_heads <= 0 || s->total_pages <= 0 ||
       s->page_size <= 0 || s->max_num_seqs < 0 || s->pages_per_seq <= 0)
     return fail(RPA_E_INVALID, "non-positive dimension in shape");
@@ -3951,8 +3983,13 @@ Params base_params(const rpa_shape_t* s) {
   p.Nmax = s->max_num_seqs;
   p.PPS = s->pages_per_seq;
   p.HG = heads_per_group(p.Hkv);
-  p.NG = p.Hkv / p.HG;
   p.D = s->head_dim;
+  if (p.D == 2 * kD) {  // two 128-dim halves per kv head, both in one workgroup
+    int g = p.Hkv < 4 ? p.Hkv : 4;
+    while (p.Hkv % g) --g;
+    p.HG = 2 * g;
+  }
+  p.NG = (p.D == 2 * kD ? 2 * p.Hkv : p.Hkv) / p.HG;
   return p;
 }
 
@@ -4368,7 +4405,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
     return fail(RPA_E_HIP, "hipEventRecord(begin) failed");
   const bool upg = p.S % KV_CHUNK == 0;
   const dim3 grid(p.grid), block(64 * p.HG);
-  const size_t lds = (size_t)p.HG * (kVtBytes + (mode == KV_BF16_FUSED ? kRelStage : 0));
+  const size_t lds = (size_t)p.HG * (kVtBytes + (mode == KV_BF16_FUSED ? kRelStage : 0) +
+                                     (p.D > kD ? kWideSlot : 0));
   if (mode == KV_BF16_FUSED) {
     hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_FUSED, true>), grid, block, lds, st, p);
   } else if (mode == KV_BF16_BIAS) {

@@ -33,7 +33,7 @@ from collections import defaultdict
 
 PACKAGE = pathlib.Path(__file__).resolve().parent
 ROOT = PACKAGE.parent.parent
-CONFIGS = ("c1", "c2", "c3", "c4", "c5", "c2w", "c3f", "c5t", "c2d64", "inkling")
+CONFIGS = ("c1", "c2", "c3", "c4", "c5", "c2w", "c3f", "c5t", "c2d64", "c2d256", "inkling")
 PASSES = {
     "fetch": ("FETCH_SIZE",),
     "write": ("WRITE_SIZE",),

@@ -101,7 +101,7 @@ def summarize(rows: list[dict], grid: int, waves: int, kernel_us: float) -> list
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "c2w", "c3f", "c5t", "c2d64"])
+    ap.add_argument("--config", default="c3", choices=["c1", "c2", "c3", "c4", "c5", "c2w", "c3f", "c5t", "c2d64", "c2d256"])
     ap.add_argument("--seed", type=int, default=None)
     ap.add_argument("--runs", type=int, default=8, help="calls before the one whose timeline is read")
     ap.add_argument("--write", default=None, help="also write the summary to this file")

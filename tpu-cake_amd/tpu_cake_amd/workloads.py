@@ -42,7 +42,7 @@ LOGNORMAL_SIGMA = 0.5
 POOL_FACTOR = 1.25
 FP8_MAX = 448.0
 
-CONFIG_SEEDS = {"c1": 97, "c2": 98, "c3": 99, "c4": 98, "c5": 101, "c3f": 99, "c5t": 101, "c2d64": 98}
+CONFIG_SEEDS = {"c1": 97, "c2": 98, "c3": 99, "c4": 98, "c5": 101, "c3f": 99, "c5t": 101, "c2d64": 98, "c2d256": 98}
 
 CONFIG_DESCRIPTIONS = {
     "c1": "tiny decode: 4 seqs x 1 token, kv_len U[1,512], Hq 8 / Hkv 2, D 128, page 16, 160-page pool",
@@ -54,6 +54,7 @@ CONFIG_DESCRIPTIONS = {
     "c3f": "C3's mixed batch (24 decode rows + 4 prefill chunks of 512) over an fp8-e4m3 pool with per-(page, kv head) K and V scales = max|x|/448",
     "c5t": "C5 with its first sequence at the clip, 131072 keys (the heavy tail's worst case)",
     "c2d64": "C2's batch with head_dim 64 (the narrow decode instantiation)",
+    "c2d256": "C2's batch with head_dim 256 (two 128-dim halves per kv head)",
 }
 
 
@@ -245,9 +246,9 @@ def _config_meta(cfg: str, rng) -> ConfigMeta:
     if cfg == "c3f":
         m = _config_meta("c3", rng)
         return dataclasses.replace(m, name="c3f", kv_dtype="fp8")
-    if cfg == "c2d64":
+    if cfg in ("c2d64", "c2d256"):
         m = _config_meta("c2", rng)
-        return dataclasses.replace(m, name="c2d64", head_dim=64)
+        return dataclasses.replace(m, name=cfg, head_dim=64 if cfg == "c2d64" else 256)
     if cfg in ("c5", "c5t"):
         lens = np.clip(np.floor(16.0 * (1.0 + rng.pareto(1.2, size=256))), 16, 131072).astype(np.int64)
         if cfg == "c5t":
