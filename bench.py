@@ -386,6 +386,9 @@ def main() -> int:
                     help="1: prefill kernel, 2: the attention kernel's own prefill tiles, 3: those tiles in "
                          "one 8-wave workgroup per CU, -1: stream-K rows (default: the tuned table)")
     ap.add_argument("--prefill-cost", type=float, default=None, help="schedule knob (default: the tuned table)")
+    ap.add_argument("--graph", action="store_true",
+                    help="time steps as replays of one-call HIP graphs (ops.CapturedCall, one per rotated pool) "
+                         "instead of eager calls")
     ap.add_argument("--host-submit", action="store_true",
                     help="instead of the benchmark, measure the host time to submit one call (C1 shapes, "
                          "calls back to back, no synchronisation in between) and exit")
@@ -455,8 +458,17 @@ def main() -> int:
                                    d["num_seqs"], sm_scale=case.sm_scale, kv_scales=kv_scales, out=out,
                                    kernel_events=ev, sliding_window=window, **knobs)
 
+    step = call
+    if args.graph:  # one captured call per pool copy, replayed in the pools' rotation
+        graphs = [ops.CapturedCall(d["q"], pools[c], d["kv_lens"], d["page_indices"], d["cu_q_lens"], d["num_seqs"],
+                                   sm_scale=case.sm_scale, kv_scales=kv_scales, out=out, sliding_window=window,
+                                   **knobs) for c in range(copies)]
+
+        def step(i):
+            graphs[i % copies].replay()
+
     for i in range(args.warmup):
-        call(i)
+        step(i)
     torch.cuda.synchronize()
     # the timed region: K calls and nothing else (the headline value)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -464,7 +476,7 @@ def main() -> int:
     wall0 = time.perf_counter()
     start.record()
     for i in range(args.steps):
-        call(i)
+        step(i)
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
@@ -509,6 +521,7 @@ def main() -> int:
             "sum_kv_len": int(case.kv_lens[:n].sum()),
             "kv_bytes_per_step": kv_bytes,
             "kv_pool_copies_rotated": copies,
+            **({"steps_as": "one-call HIP graph replays"} if args.graph else {}),
             **({"knobs": knobs} if knobs else {}),
         },
         "tokens_per_s": round(T / (ms_step * 1e-3), 1),
