@@ -80,7 +80,7 @@ def test_noalloc_knobs_and_window(cuda):
 
 def test_noalloc_rejects_bad_arguments_before_any_launch(cuda):
     lib = _lib.load()
-    shape = _lib.RpaShape(4, 8, 2, 64, 10, 16, 4, 4, 0)
+    shape = _lib.RpaShape(4, 8, 2, 192, 10, 16, 4, 4, 0)  # a head dim that is not built
     rc = lib.rpa_ragged_paged_attention_noalloc(ctypes.byref(shape), ctypes.byref(_lib.RpaOptions(sm_scale=1.0)),
                                                 *([None] * 8), None)
     assert rc == -2 and b"head_dim" in lib.rpa_last_error()
