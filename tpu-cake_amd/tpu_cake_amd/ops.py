@@ -388,9 +388,10 @@ class CapturedCall(CapturedCalls):
     """One ``ragged_paged_attention`` call captured into a HIP graph over fixed buffers
     (``CapturedCalls`` with one call; ``replay()`` returns ``out``).
 
-    A graph launch costs more host time on this platform than the operator's own eager call, so a
-    graph of one call is host-bound at the graph-launch rate; a graph holding a whole step's calls
-    (``CapturedCalls``) pays that launch once for all of them.
+    A graph launch costs more host time on this platform than the operator's own eager call, and
+    each replay adds a few microseconds of device time, so a graph of one call is slower than the
+    eager call it captures (small calls are host-bound at the graph-launch rate); a graph holding a
+    whole step's calls (``CapturedCalls``) pays that launch once for all of them.
     """
 
     def __init__(self, q, kv_pages, kv_lens, page_indices, cu_q_lens, num_seqs, *, out=None, **kwargs):
