@@ -387,6 +387,21 @@ def test_prefill_tiles_window_and_soft_cap(cuda):
     _check(case, gpu_kw=dict(sliding_window=100, soft_cap=30.0), oracle_kw=dict(sliding_window=100, soft_cap=30.0))
 
 
+# Prefill-heavy batches that give every CU a prefill-first workgroup: each CU's two workgroups take
+# fixed positions of their XCD's tile queue (a long tile and a short one), the queue counters hand
+# out the positions after those.  384 tiles leave some fixed positions past the end; 720 tiles put
+# the rest through the counters; fp8 KV takes the same schedule.
+@pytest.mark.parametrize("q_lens,kv_lens,kv_dtype", [
+    ([512, 512, 512, 1, 1], [2048, 600, 3000, 4000, 90], "bf16"),
+    ([512, 512, 512, 512, 512, 300, 1, 1], [512, 1500, 2600, 900, 3100, 300, 5000, 700], "bf16"),
+    ([512, 512, 512, 512, 1], [1200, 3000, 512, 2000, 800], "fp8"),
+])
+def test_prefill_heavy_fixed_first_tiles(cuda, q_lens, kv_lens, kv_dtype):
+    _say(f"prefill-heavy batch q_lens={q_lens} kv_lens={kv_lens} {kv_dtype}")
+    _check(make_custom(kv_lens=kv_lens, q_lens=q_lens, num_q_heads=32, num_kv_heads=8, page_size=64,
+                       seed=sum(kv_lens) % 1000, kv_dtype=kv_dtype))
+
+
 def test_prefill_tiles_match_stream_k(cuda):
     """The same batch with prefill tiles switched off (the per-call prefill_tiles knob) agrees with
     the tiled result to the bf16 output tolerance."""

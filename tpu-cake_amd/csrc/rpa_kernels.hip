@@ -2373,7 +2373,7 @@ __device__ __forceinline__ int co_tile_parts(int sz, int np) {
 // r / Hkv, kv head r % Hkv.  Calls with more units than kPfOrderMax keep the pair order unsplit.
 template <int MODE>
 __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, uint8_t* lds, int* s_tile,
-                                        int lane, int wv, int n, int j, int& err) {
+                                        int lane, int wv, int n, int j, int& err, int sq = -1, int sn = 0) {
   RPA_TL(tl_set(TL_TILES0, tl_clock());)
   TlAcc ta;
   const CoPairs cp = co_pairs(p, wsi, pf_min, lane);
@@ -2454,16 +2454,27 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
   // its neighbours just fetched from that XCD's L2.  A workgroup takes tiles from its own XCD's
   // queue; once that is empty, wave 0 reads all eight counters at once (agent-scope loads) and
   // takes from the queue with the most tiles left, until none has any.
+  //
+  // sq >= 0 (every CU with one prefill-first and one stream-K workgroup): the first sn positions of
+  // each XCD's queue are handed out statically -- the prefill-first workgroup of a CU takes position
+  // k (its rank among its XCD's prefill-first workgroups, longest tiles first), the CU's stream-K
+  // workgroup, joining later, position sn - 1 - k: each CU pairs a long first tile with a short
+  // late one, and neither pays a queue round trip for it.  The counters then hand out positions
+  // sn, sn + 1, ...
   const int x0 = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & (kXcds - 1));  // XCC_ID
   bool own_left = true;  // wave 0's view of its own queue
-  for (;;) {
+  for (int first = 1;; first = 0) {
     RPA_TL(const long long tl_q = tl_clock();)
     if (wv == 0) {
       int t = total;
-      if (own_left) {
+      if (first && sq >= 0) {
+        const int ts = sq * kXcds + ((int)blockIdx.x & (kXcds - 1));  // the static position's tile
+        t = ts < total ? ts : total;
+      }
+      if (t >= total && own_left) {
         int q = 0;
         if (lane == 0) q = atomicAdd(p.err + kQueueWord + x0, 1);
-        q = uni(q);
+        q = uni(q) + sn;
         if (q < (total - x0 + kXcds - 1) / kXcds)
           t = q * kXcds + x0;
         else
@@ -2473,7 +2484,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
         const int x = (x0 + lane) & (kXcds - 1);
         int left = 0;
         if (lane < kXcds)
-          left = (total - x + kXcds - 1) / kXcds -
+          left = (total - x + kXcds - 1) / kXcds - sn -
                  __hip_atomic_load(p.err + kQueueWord + x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int key = left > 0 ? (left << 3) | (kXcds - 1 - lane) : -1;  // most left, then nearest
         int best = -1;
@@ -2483,7 +2494,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
         const int bl = kXcds - 1 - (best & (kXcds - 1)), bx = (x0 + bl) & (kXcds - 1);
         int q = 0;
         if (lane == 0) q = atomicAdd(p.err + kQueueWord + bx, 1);
-        q = uni(q);
+        q = uni(q) + sn;
         if (q < (total - bx + kXcds - 1) / kXcds) t = q * kXcds + bx;
       }
       if (lane == 0) *s_tile = t;
@@ -2661,9 +2672,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   const int gd = p.grid - gpre;  // stream-K workgroup count
   RPA_TL(tl_set(TL_SCHED, tl_clock()); int tl_role = pf_first ? 1 : 0;)
+  // static first tiles of the co-resident layout when every CU holds a prefill-first workgroup
+  // (co_role): b and b + grid/2 share a CU and an XCD (b mod 8), so the pair's positions in that
+  // XCD's queue are k and sn - 1 - k, with k the CU's rank on its XCD
+  int sq = -1, sn = 0;
+  if constexpr (CO) {
+    const int half = p.grid >> 1;
+    if (gpre == half && (half & (kXcds - 1)) == 0) {
+      const int per = half / kXcds;  // CUs per XCD
+      sn = 2 * per;
+      sq = pf_first ? (b - half) / kXcds : 2 * per - 1 - b / kXcds;
+    }
+  }
   if (kTiles && pf_first) {
     if constexpr (CO)
-      co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
+      co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err, sq, sn);
     else if constexpr (MODE == KV_BF16)  // (HG == 8: one K and one V piece per thread per chunk)
       pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
@@ -2765,7 +2788,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (CO && !pf_first && pf_total > 0) {
     __syncthreads();  // every wave is done with its stream-K LDS regions
     RPA_TL(tl_role |= 4;)
-    co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err);
+    co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err, sq, sn);
   }
 
   {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
