@@ -2471,6 +2471,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
         const int ts = sq * kXcds + ((int)blockIdx.x & (kXcds - 1));  // the static position's tile
         t = ts < total ? ts : total;
       }
+      if (sn * kXcds >= total) own_left = false;  // the fixed positions cover every queue
       if (t >= total && own_left) {
         int q = 0;
         if (lane == 0) q = atomicAdd(p.err + kQueueWord + x0, 1);
@@ -2480,7 +2481,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
         else
           own_left = false;
       }
-      while (t >= total) {
+      while (t >= total && sn * kXcds < total) {
         const int x = (x0 + lane) & (kXcds - 1);
         int left = 0;
         if (lane < kXcds)
