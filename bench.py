@@ -204,7 +204,8 @@ def fused_bench(args, dev) -> int:
     from tpu_cake_amd.workloads import FUSED_DESCRIPTION, make_fused_case
 
     t0 = time.perf_counter()
-    case = make_fused_case(seed=args.seed if args.seed is not None else 102)
+    page = args.fused_page_size
+    case = make_fused_case(seed=args.seed if args.seed is not None else 102, page_size=page)
     log(f"built inkling in {time.perf_counter() - t0:.1f}s")
     a = case.arrays
     tensors = []
@@ -249,14 +250,15 @@ def fused_bench(args, dev) -> int:
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic: seeded N(0,1) queries / new K,V, N(0,0.25) cache, N(0,0.4) relative tensors",
-        "config": {"workload": f"inkling: {FUSED_DESCRIPTION}", "num_seqs": int(nseq),
+        "config": {"workload": "inkling: " + FUSED_DESCRIPTION.replace("page 64", f"page {page}"), "num_seqs": int(nseq),
                    "sum_kv_len": int(a["kv_lengths"].sum()), "kv_bytes_per_step": kv_bytes,
                    "cache_copies_rotated": copies},
         "tokens_per_s": round(nseq / (ms_step * 1e-3), 1),
         "hbm_fraction": round(value / peak, 4),
         "wall_s_timed_region": round(wall, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": peak, "unit": "GB/s",
-                     "frac": round(achieved / peak, 4), "traffic": measured_traffic("inkling"),
+                     "frac": round(achieved / peak, 4),
+                     "traffic": measured_traffic("inkling") if page == 64 else None,
                      "basis": "whole step (every launch of the call: attention with the in-kernel bias, merge "
                               "with the new-token store; a preparation launch first for shapes that need one)"},
     }
@@ -378,6 +380,9 @@ def main() -> int:
                          "c3f: C3's batch over an fp8 pool; c5t: C5 with one 131072-key sequence; c2d64 / c2d256: C2 at head_dim 64 / 256; "
                          "inkling: the fused decode step (KV-cache write + relative-bias attention)")
     ap.add_argument("--seed", type=int, default=None)
+    ap.add_argument("--fused-page-size", type=int, default=64,
+                    help="inkling: the cache's page size (64: the profiled workload; any size runs in one "
+                         "attention launch)")
     ap.add_argument("--rotate-bytes", type=float, default=2.0e9,
                     help="KV pool copies rotated so that at least this many bytes separate reuses")
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -230,10 +230,10 @@ int rpa_timeline_read(int64_t* host_rows, int32_t rows, void* stream);
  * the device still range-checks what it dereferences (error word).  cu_q_lens and
  * distribution are part of the reference's input list and are validated by that preflight;
  * the device does not read them.  head_dim <= cache_width = 128.
- * With head_dim = 128, a page size that is a multiple of 32, 16-byte aligned tensors and
- * R in {0, 16} with E a multiple of 8, the step is one attention launch (new token read from
- * keys/values, bias formed in the kernel) plus the merge launch, which also stores the token;
- * other shapes take a preparation launch first (cache write, page table, bias table).
+ * With head_dim a multiple of 8 in [32, 128], 16-byte aligned tensors, P * S < 2^31 and R in
+ * {0, 16} with E a multiple of 8 -- any page size -- the step is one attention launch (new token
+ * read from keys/values, bias formed in the kernel) plus the merge launch, which also stores the
+ * token; other shapes take a preparation launch first (cache write, page table, bias table).
  * --------------------------------------------------------------------------------------- */
 typedef struct rpa_fused_shape {
   int32_t num_seqs;          /* B */

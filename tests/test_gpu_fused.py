@@ -83,8 +83,8 @@ def test_decode_shapes(cuda, hq, hkv, d, page, lens):
     (32, 8, 64, [5, 70, 200], 32, 64),
 ])
 def test_bias_windows_and_launch_forms(cuda, hq, hkv, page, lens, rel_dim, extent):
-    """Relative-bias windows at chunk edges and both forms of the call: the one-launch path (page
-    size a multiple of 32, D = 128, R in {0, 16}, E a multiple of 8) and the prep launch."""
+    """Relative-bias windows at chunk edges and both forms of the call: the one-launch path (R in
+    {0, 16}, E a multiple of 8) and the prep launch."""
     _say(f"fused bias hq={hq} hkv={hkv} page={page} R={rel_dim} E={extent}")
     pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
     inp = fo.fused_inputs_like(rel_dim * 5 + extent + page, nseq=len(lens), hq=hq, hkv=hkv, d=128,
@@ -129,6 +129,45 @@ def test_random_one_launch_sweep(cuda):
         _run_and_check(inp)
 
 
+@pytest.mark.parametrize("hq,hkv,d,page,lens,rel_dim,extent", [
+    # one attention launch with pages smaller than a 32-key unit (each key's own page id): page 1 as
+    # in the reference's sharded fixture, page 16 at unit and page edges, pages that do not divide 32
+    (32, 8, 128, 1, [1, 2, 31, 32, 33, 300, 1000], 16, 512),
+    (32, 8, 128, 16, [1, 15, 16, 17, 31, 32, 33, 64, 700, 2048], 16, 512),
+    (16, 4, 64, 16, [5, 16, 17, 300, 1000], 0, 512),
+    (32, 8, 128, 24, [1, 23, 24, 25, 48, 49, 500], 16, 40),
+    (8, 8, 128, 8, [2, 9, 33, 100], 16, 8),
+    (16, 2, 96, 48, [3, 47, 48, 49, 97, 1500], 16, 512),
+])
+def test_one_launch_small_pages(cuda, hq, hkv, d, page, lens, rel_dim, extent):
+    _say(f"fused one launch page={page} d={d} hq={hq} hkv={hkv} R={rel_dim} E={extent}")
+    pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(page * 7 + d + rel_dim, nseq=len(lens), hq=hq, hkv=hkv, d=d, page_size=page,
+                               pool_pages=pool, lengths=lens, rel_dim=rel_dim, extent=extent)
+    _run_and_check(inp)
+
+
+def test_random_small_page_sweep(cuda):
+    """Seeded random shapes of the one-launch form with pages of 1 to 31 keys (each key of a unit
+    read from its own page), GQA 1-8, Hkv 1-16, R 0 or 16, head dims 32-128, cache bit-exact."""
+    rng = np.random.default_rng(4048)
+    for case in range(10):
+        hkv = int(rng.choice([1, 2, 4, 8, 16]))
+        g = int(rng.choice([1, 2, 4, 8]))
+        page = int(rng.choice([1, 2, 4, 8, 12, 16, 20, 31]))
+        d = int(rng.choice([32, 64, 128]))
+        nseq = int(rng.integers(1, 20))
+        lens = [int(x) for x in rng.integers(1, 1500, size=nseq)]
+        lens[0] = int(rng.choice([1, 32, 33, page, page + 1]))
+        rel = int(rng.choice([0, 16]))
+        extent = 8 * int(rng.integers(1, 76))
+        _say(f"fused small-page sweep {case}: hq={hkv * g} hkv={hkv} d={d} page={page} nseq={nseq} R={rel} E={extent}")
+        pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+        inp = fo.fused_inputs_like(300 + case, nseq=nseq, hq=hkv * g, hkv=hkv, d=d, page_size=page,
+                                   pool_pages=pool, lengths=lens, rel_dim=rel, extent=extent)
+        _run_and_check(inp)
+
+
 def test_more_than_256_sequences(cuda):
     """Metadata past the first four 64-sequence windows (loaded one window at a time)."""
     rng = np.random.default_rng(11)
@@ -154,15 +193,15 @@ def test_rejected_metadata_never_reaches_the_kernel(cuda):
     assert np.array_equal(_bits(args[3]), before)
 
 
-@pytest.mark.parametrize("bad", [-64, 5])
-def test_one_launch_drops_a_sequence_with_bad_page_offset(cuda, bad):
+@pytest.mark.parametrize("bad,page", [(-64, 64), (5, 64), (-16, 16), (5, 16)])
+def test_one_launch_drops_a_sequence_with_bad_page_offset(cuda, bad, page):
     """Metadata the preflight would reject, sent straight to the kernel (fused.invoke): a negative or
     unaligned cu_kv_lens entry drops that sequence (page bit of the error word, its cache slot left
     as it was) and leaves every other sequence's output and cache update as the oracle's."""
-    _say(f"fused one launch, cu_kv[1] = {bad}")
+    _say(f"fused one launch, page {page}, cu_kv[1] = {bad}")
     lens = [40, 100, 70, 300]
-    pool = int(sum(-(-x // 64) for x in lens) * 1.25) + 2
-    inp = fo.fused_inputs_like(5, nseq=4, hq=32, hkv=8, d=128, page_size=64, pool_pages=pool, lengths=lens,
+    pool = int(sum(-(-x // page) for x in lens) * 1.25) + 2
+    inp = fo.fused_inputs_like(5, nseq=4, hq=32, hkv=8, d=128, page_size=page, pool_pages=pool, lengths=lens,
                                rel_dim=16, extent=512)
     expected = fo.inkling_fused_rpa_reference(inp)
     bad_inp = dict(inp)
@@ -183,10 +222,10 @@ def test_one_launch_drops_a_sequence_with_bad_page_offset(cuda, bad):
     assert np.allclose(got_o[keep], exp_o[keep], atol=0.02, rtol=0.02)
     got_c = _bits(cache).reshape(inp["cache"].shape)
     # sequence 1's slot: untouched; everything else: the oracle's updated cache
-    page = int(inp["page_indices"][int(inp["cu_kv_lens"][1]) // 64 + (lens[1] - 1) // 64])
-    slot = (lens[1] - 1) % 64
+    pg = int(inp["page_indices"][int(inp["cu_kv_lens"][1]) // page + (lens[1] - 1) // page])
+    slot = (lens[1] - 1) % page
     want = expected[1].copy()
-    want[page, slot] = before[page, slot]
+    want[pg, slot] = before[pg, slot]
     assert np.array_equal(got_c, want)
 
 

@@ -645,6 +645,15 @@ __device__ __forceinline__ Pages load_pages(const Params& p, const Cursor& x, in
   const bool live = x.nch > 0;
   const int last = x.kv_len > 0 ? x.kv_len - 1 : 0;
   const size_t row = live ? page_row<MODE>(p, x) : 0;
+  if constexpr (MODE == KV_BF16_FUSED) {
+    // the full-line path with pages smaller than a unit: lane L's key key0 + L % 32 -- its page id
+    // and its slot in the page (line_addr)
+    int kt = x.key0() + (n + 16 * ((threadIdx.x >> 4) & 1));
+    kt = live ? (kt < last ? kt : last) : 0;
+    r.pg[0] = p.page_indices[row + page_of(kt, p)];
+    r.pg[1] = slot_of(kt, p);
+    return r;
+  }
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk) {
     int kt = x.key0() + 16 * blk + n;
@@ -1202,7 +1211,7 @@ __device__ __forceinline__ void step(const Params& p, int nseq, int lane, int n,
 template <int MODE, bool UPG>
 struct LinePath {
   static constexpr bool on =
-      UPG && (MODE == KV_BF16 || MODE == KV_BF16_SCALED || MODE == KV_BF16_BIAS || MODE == KV_BF16_FUSED);
+      MODE == KV_BF16_FUSED || (UPG && (MODE == KV_BF16 || MODE == KV_BF16_SCALED || MODE == KV_BF16_BIAS));
 };
 
 struct LineRegs {
@@ -1215,14 +1224,38 @@ struct LineAddr {
   int bias_at;  // as UnitAddr
   int knew;       // fused step: the unit's key (0..31) read from new_k / new_v instead, -1 = none
   size_t newoff;  // fused step: element index of this lane's dims of that key's row in new_k / new_v
+  int row;        // fused step, pages smaller than a unit: pool row (page * S + slot) of key lane % 32
 };
 
-template <int MODE>
+template <int MODE, bool UPG = true>
 __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, const Pages& pages, int lane, int n,
                                               int j, int wv, int& err, int D = kD) {
-  const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err, D);  // page checks, head, bias position
   LineAddr a;
   const bool live = x.nch > 0;
+  if constexpr (!UPG) {
+    // (the fused step only: D = kD, head v = h * HG + wv) pages smaller than a unit: the keys of
+    // one load instruction may lie in different pages; lane L checks the page of key L % 32 and
+    // keeps its pool row, which load_lines hands to the lanes that read that key
+    static_assert(MODE == KV_BF16_FUSED, "per-key pages on the full-line path: the fused step only");
+    const int v = live ? x.h * p.HG + wv : 0;
+    const bool in_seq = live && x.key0() + (lane & 31) < x.kv_len;
+    const bool pg_ok = pages.pg[0] >= 0 && pages.pg[0] < p.P;
+    if (in_seq && !pg_ok) err |= ERR_PAGE;
+    a.row = (pg_ok ? pages.pg[0] : 0) * p.S + pages.pg[1];
+    a.e0 = (size_t)(2 * v) * kD + 8 * (lane & 15);
+    const int k = live ? x.kv_len - 1 - x.key0() : 0;
+    a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
+    a.bias_at = 0;
+    a.knew = -1;
+    a.newoff = 0;
+    if (live && k < KV_CHUNK) {
+      a.knew = k;
+      a.newoff = ((size_t)x.i * p.Hkv + v) * p.D + (8 * (lane & 15) < p.D ? 8 * (lane & 15) : 0);
+    }
+    return a;
+  }
+  const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err, D);  // page checks, head, bias position
+  a.row = 0;
   // (a narrow pool's pieces wholly past D read the row's first piece, as in load_half)
   a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h, D) + half_offset(live ? x.h * p.HG + wv : 0, D) +
          (D == kD || 8 * (lane & 15) < D ? 8 * (lane & 15) : 0);
@@ -1242,7 +1275,7 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
 }
 
 // which = 0: K rows (combined head 2h), 1: V rows (2h+1).
-template <int MODE>
+template <int MODE, bool UPG = true>
 __device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, int lane, int which, LineRegs& r,
                                            int D = kD) {
   const uint16_t* kv = (const uint16_t*)p.kv + a.e0 + (size_t)which * D;
@@ -1253,7 +1286,11 @@ __device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, i
   for (int i = 0; i < 8; ++i) {
     int key = 4 * i + (lane >> 4);
     key = key < a.kmax ? key : a.kmax;
-    const uint16_t* src = kv + (size_t)key * row;
+    const uint16_t* src;
+    if constexpr (UPG)
+      src = kv + (size_t)key * row;
+    else  // the key's pool row, from lane key (line_addr)
+      src = kv + (size_t)__builtin_amdgcn_ds_bpermute(4 * key, a.row) * row;
     if constexpr (MODE == KV_BF16_FUSED) src = key == a.knew ? nw : src;  // the step's new token
     r.w[i] = ld_stream((const u32x4*)src);
   }
@@ -1354,7 +1391,7 @@ __device__ __forceinline__ void store_k_tile(const Params& p, const LineRegs& k,
 
 // compute_unit with K read from the K tile, V stored as key rows from the line layout and the
 // next unit's V loaded into v (after that store).
-template <int MODE>
+template <int MODE, bool UPG = true>
 __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor& x, LineRegs& v, const f32x4* bias,
                                                   bf16x8 q[4], uint32_t rst[2], const Cursor& nx,
                                                   const LineAddr& nx_addr,
@@ -1379,7 +1416,7 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
   // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
   // issued before it they would make that wait also retire the next unit's K
   if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst, Dq);
-  load_lines<MODE>(p, nx_addr, lane, 1, v, D);
+  load_lines<MODE, UPG>(p, nx_addr, lane, 1, v, D);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
 
@@ -1405,16 +1442,16 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
   else
     ahead.nch = 0;
   const Pages pg_ahead = load_pages<MODE, UPG>(p, ahead, n);
-  const LineAddr nx_addr = line_addr<MODE>(p, nxt, pg_nxt, lane, n, j, wv, err, D);
+  const LineAddr nx_addr = line_addr<MODE, UPG>(p, nxt, pg_nxt, lane, n, j, wv, err, D);
   __syncthreads();
-  load_lines<MODE>(p, nx_addr, lane, 0, k, D);  // the next unit's K (this unit's K is in the tile)
+  load_lines<MODE, UPG>(p, nx_addr, lane, 0, k, D);  // the next unit's K (this unit's K is in the tile)
   LineBias bias_nx;
   load_line_bias<MODE>(p, nxt, nx_addr, lane, n, j, wv, bias_nx);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
   // the fused step's queries and output rows are p.D wide (its cache rows kD)
   const int Dq = MODE == KV_BF16_FUSED ? p.D : D;
-  compute_unit_line<MODE>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D, Dq);
+  compute_unit_line<MODE, UPG>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D, Dq);
   // The next unit's K goes to the tile before a row block's finish stores: its wait then counts
   // the same younger operations (the next unit's V) on every path.  Issued before it, the stores
   // made that wait also retire most of the V just loaded on the steps that end a row block.
@@ -2373,8 +2410,20 @@ __device__ __forceinline__ int co_tile_parts(int sz, int np) {
 // r / Hkv, kv head r % Hkv.  Calls with more units than kPfOrderMax keep the pair order unsplit.
 template <int MODE>
 __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], int pf_min, uint8_t* lds, int* s_tile,
-                                        int lane, int wv, int n, int j, int& err, int sq = -1, int sn = 0) {
+                                        int lane, int wv, int n, int j, int& err, int gpre, bool pf_first) {
   RPA_TL(tl_set(TL_TILES0, tl_clock());)
+  // fixed first positions when every CU holds a prefill-first workgroup (below): b and b + grid/2
+  // share a CU and an XCD (b mod 8), so the pair's positions in that XCD's queue are k and
+  // sn - 1 - k, with k the CU's rank on its XCD
+  int sq = -1, sn = 0;
+  {
+    const int half = p.grid >> 1, b = blockIdx.x;
+    if (gpre == half && (half & (kXcds - 1)) == 0) {
+      const int per = half / kXcds;  // CUs per XCD
+      sn = 2 * per;
+      sq = pf_first ? (b - half) / kXcds : 2 * per - 1 - b / kXcds;
+    }
+  }
   TlAcc ta;
   const CoPairs cp = co_pairs(p, wsi, pf_min, lane);
   const int npairs = cp.base[4];
@@ -2673,21 +2722,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
   const int gd = p.grid - gpre;  // stream-K workgroup count
   RPA_TL(tl_set(TL_SCHED, tl_clock()); int tl_role = pf_first ? 1 : 0;)
-  // static first tiles of the co-resident layout when every CU holds a prefill-first workgroup
-  // (co_role): b and b + grid/2 share a CU and an XCD (b mod 8), so the pair's positions in that
-  // XCD's queue are k and sn - 1 - k, with k the CU's rank on its XCD
-  int sq = -1, sn = 0;
-  if constexpr (CO) {
-    const int half = p.grid >> 1;
-    if (gpre == half && (half & (kXcds - 1)) == 0) {
-      const int per = half / kXcds;  // CUs per XCD
-      sn = 2 * per;
-      sq = pf_first ? (b - half) / kXcds : 2 * per - 1 - b / kXcds;
-    }
-  }
   if (kTiles && pf_first) {
     if constexpr (CO)
-      co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err, sq, sn);
+      co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err, gpre, pf_first);
     else if constexpr (MODE == KV_BF16)  // (HG == 8: one K and one V piece per thread per chunk)
       pf_role<1, UPG>(p, wsi, pf_min, pf_total, smem, &s_tile, lane, wv, n, j, err);
   }
@@ -2745,11 +2782,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // K, bias, queries, V: the loop's order (vmcnt retires in order, and the compiler
         // counts each wait for the least favourable path into it, this prologue included)
         {
-          const LineAddr a0 = line_addr<MODE>(p, cur, pg_cur, lane, n, j, wv, err, D);
-          load_lines<MODE>(p, a0, lane, 0, k, D);
+          const LineAddr a0 = line_addr<MODE, UPG>(p, cur, pg_cur, lane, n, j, wv, err, D);
+          load_lines<MODE, UPG>(p, a0, lane, 0, k, D);
           load_line_bias<MODE>(p, cur, a0, lane, n, j, wv, bias_in);
           load_q<MODE>(p, cur, n, j, wv, q, rst, MODE == KV_BF16_FUSED ? p.D : D);
-          load_lines<MODE>(p, a0, lane, 1, v, D);
+          load_lines<MODE, UPG>(p, a0, lane, 1, v, D);
         }
         RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
         store_k_tile<MODE>(p, k, kt, lane);
@@ -2789,7 +2826,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (CO && !pf_first && pf_total > 0) {
     __syncthreads();  // every wave is done with its stream-K LDS regions
     RPA_TL(tl_role |= 4;)
-    co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err, sq, sn);
+    co_role<MODE>(p, wsi, pf_min, smem, &s_tile, lane, wv, n, j, err, gpre, pf_first);
   }
 
   {  // rows at or past cu_q_lens[num_seqs] belong to no sequence: zero them
@@ -3686,12 +3723,22 @@ constexpr int kVtBytes = kWaveLds;  // LDS per wave: V region + K tile
 template <int MODE>
 int occupancy_grid(int cus, int hg) {
   int per_cu = 0;
-  // the fused step runs only on the full-line path, with its relative-bias staging
+  // the fused step runs only on the full-line path (whole-page units or per-key pages), with its
+  // relative-bias staging: the smaller occupancy of its two instantiations
   constexpr bool kFused = MODE == KV_BF16_FUSED;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE, kFused>, 64 * hg,
-                                                   hg * (kVtBytes + (kFused ? kRelStage : 0))) != hipSuccess ||
+  const size_t lds = hg * (kVtBytes + (kFused ? kRelStage : 0));
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, rpa_attn_kernel<MODE, kFused>, 64 * hg, lds) !=
+          hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
+  if constexpr (kFused) {
+    int pl = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&pl, rpa_attn_kernel<MODE, false>, 64 * hg, lds) !=
+            hipSuccess ||
+        pl <= 0)
+      pl = 1;
+    per_cu = pl < per_cu ? pl : per_cu;
+  }
   int max_groups = kMaxWavesPerCU / hg;
   if (max_groups < 1) max_groups = 1;
   if (per_cu > max_groups) per_cu = max_groups;
@@ -4389,7 +4436,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
 
   int mode = KV_BF16;
   if (fz) {  // the fused decode step in the attention launch (bias, if any, formed in the kernel)
-    if (p.S % KV_CHUNK) return fail(RPA_E_INVALID, "fused step in one launch needs a page size multiple of 32");
+    if ((long long)p.P * p.S > INT32_MAX)  // the per-key path's pool rows are 32-bit
+      return fail(RPA_E_INVALID, "fused step in one launch needs total_pages * page_size < 2^31");
     mode = KV_BF16_FUSED;
     p.fused = 1;
     p.fused_nseq = fz->nseq;
@@ -4432,7 +4480,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   const size_t lds = (size_t)p.HG * (kVtBytes + (mode == KV_BF16_FUSED ? kRelStage : 0) +
                                      (p.D > kD ? kWideSlot : 0));
   if (mode == KV_BF16_FUSED) {
-    hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_FUSED, true>), grid, block, lds, st, p);
+    if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_FUSED, true>), grid, block, lds, st, p);
+    else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_FUSED, false>), grid, block, lds, st, p);
   } else if (mode == KV_BF16_BIAS) {
     if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, true>), grid, block, lds, st, p);
     else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_BIAS, false>), grid, block, lds, st, p);
@@ -4681,12 +4730,13 @@ int rpa_inkling_fused_decode(const rpa_fused_shape_t* f, float sm_scale, const v
   uint8_t* ws = (uint8_t*)workspace;
   hipStream_t st = (hipStream_t)stream;
   // One attention launch (metadata, new token and relative bias handled in the kernel, the token
-  // stored by the combine launch) on the full-line path with aligned tensors, head dims that are
+  // stored by the combine launch) on the full-line path -- whole-page units when the page size is
+  // a multiple of 32, per-key pages otherwise -- with aligned tensors, head dims that are
   // multiples of 8 in [32, 128] (queries, new rows and the output of that width, the cache rows
-  // 128) and a 16-wide relative projection; the prep launch below otherwise.
+  // 128) and no or a 16-wide relative projection; the prep launch below otherwise.
   const bool aligned = ((uintptr_t)queries | (uintptr_t)keys | (uintptr_t)values | (uintptr_t)cache |
                         (uintptr_t)relative_states | (uintptr_t)relative_projection) % 16 == 0;
-  if (f->head_dim >= 32 && f->head_dim % 8 == 0 && f->page_size % KV_CHUNK == 0 && aligned &&
+  if (f->head_dim >= 32 && f->head_dim % 8 == 0 && (long long)f->total_pages * f->page_size <= INT32_MAX && aligned &&
       (f->relative_dim == 0 || (f->relative_dim == kRelRows && f->relative_extent % 8 == 0))) {
     const rpa_shape_t rs = fused_rpa_shape(f);
     rpa_options_t o;
