@@ -59,3 +59,49 @@ def test_random_batches(cuda, seed):
         small = np.abs(ref) < 4
         assert np.max(np.abs(got - ref)[small], initial=0.0) <= 2e-2, desc
         assert np.all(out[tv:] == 0.0), desc
+
+
+def _prefill_heavy_case(rng):
+    # mixed batches with enough prefill tiles that every CU holds a prefill-first workgroup (the
+    # co-resident layout's fixed first tiles), over the layout's KV modes and page sizes
+    hkv = int(rng.choice([4, 8, 12, 16]))
+    g = int(rng.choice([1, 2, 4, 8])) if hkv <= 8 else int(rng.choice([1, 2, 4]))
+    page = int(rng.choice([32, 64, 128]))
+    kvl, ql = [], []
+    for _ in range(int(rng.integers(2, 7))):  # prefill chunks over a prior
+        q = int(rng.integers(200, 700))
+        kvl.append(q + int(rng.integers(0, 2500)))
+        ql.append(q)
+    for _ in range(int(rng.integers(0, 6))):  # decode rows
+        kvl.append(int(rng.integers(1, 5000)))
+        ql.append(1)
+    order = rng.permutation(len(kvl))
+    kvl, ql = [kvl[i] for i in order], [ql[i] for i in order]
+    mode = str(rng.choice(["bf16", "bf16", "fp8", "scaled"]))
+    kw = {}
+    if mode == "scaled":
+        kw.update(k_scale=float(rng.uniform(0.5, 1.5)), v_scale=float(rng.uniform(0.5, 1.5)))
+    if rng.random() < 0.25:
+        kw["mask_value"] = float(rng.uniform(-8.0, -2.0))
+    case = make_custom(kv_lens=kvl, q_lens=ql, num_q_heads=hkv * g, num_kv_heads=hkv, page_size=page,
+                       seed=int(rng.integers(1 << 30)), kv_dtype="fp8" if mode == "fp8" else "bf16")
+    return case, kw, f"hkv {hkv} g {g} page {page} kv {kvl} q {ql} mode {mode} kw {kw}"
+
+
+def test_random_prefill_heavy_batches(cuda):
+    rng = np.random.default_rng(2027)
+    for it in range(10):
+        case, kw, desc = _prefill_heavy_case(rng)
+        print(f"[case] prefill-heavy sweep {it}: {desc}", flush=True)
+        out = ops.run_case(case, **kw)
+        torch.cuda.synchronize()
+        out = out.float().cpu().numpy()
+        ref = orc.bf16_round(orc.ref_ragged_paged_attention(
+            case.q, case.kv_pages, case.kv_lens, case.page_indices, case.cu_q_lens, case.num_seqs,
+            sm_scale=case.sm_scale, kv_scales=case.kv_scales, kv_dtype=case.kv_dtype, probs_bf16=True, **kw))
+        tv = ref.shape[0]
+        got = out[:tv]
+        assert np.all(np.isfinite(got)), desc
+        assert np.allclose(got, ref, atol=0.02, rtol=0.02), desc
+        small = np.abs(ref) < 4
+        assert np.max(np.abs(got - ref)[small], initial=0.0) <= 2e-2, desc
