@@ -222,3 +222,22 @@ def test_product_library_has_no_timeline(lib):
     buf = (ctypes.c_int64 * 16)()
     assert lib.rpa_timeline_read(buf, 1, None) == -2  # RPA_E_UNSUPPORTED
     assert b"RPA_TIMELINE" in lib.rpa_last_error()
+
+
+def test_host_checks_still_see_nan(lib):
+    # the device code is built assuming no NaN operands; the host-side option checks are not, and
+    # reject a NaN prefill_cost before anything touches a GPU
+    import ctypes
+    import math
+
+    from tpu_cake_amd import _lib
+
+    shape = _lib.RpaShape(64, 32, 8, 128, 100, 64, 64, 128, _lib.RPA_KV_BF16)
+    for cost, ok in ((math.nan, False), (0.45, True), (-math.inf, False)):
+        opts = _lib.RpaOptions(sm_scale=0.088, waves_per_cu=0, prefill_tiles=0, prefill_cost=cost)
+        grid, waves = ctypes.c_int32(0), ctypes.c_int32(0)
+        rc = lib.rpa_attention_grid(ctypes.byref(shape), ctypes.byref(opts), 256, ctypes.byref(grid),
+                                    ctypes.byref(waves))
+        assert (rc == 0) == ok, (cost, rc, lib.rpa_last_error())
+        if not ok:
+            assert b"prefill_cost" in lib.rpa_last_error()

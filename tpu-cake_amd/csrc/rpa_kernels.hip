@@ -2032,6 +2032,21 @@ __device__ __forceinline__ void co_dma(const void* src, uint32_t lds_addr) {
       : "memory");
 }
 
+// The same DMA with the address split into a wave-uniform base (SGPRs) and a per-lane 32-bit byte
+// offset: the form for chunks whose every key exists, whose per-lane offsets are fixed for a tile.
+__device__ __forceinline__ void co_dma_s(const void* base, uint32_t off, uint32_t lds_addr) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(off), "s"(base), "s"(lds_addr)
+      : "memory");
+}
+
 // Per-lane parts of the DMA addresses, the same for every chunk.  bf16: lane l of wave wv carries,
 // for t = 0, 1, key 4i + l/16 of block i = wv + 4t, and 16-byte LDS position l % 16 of that key's K
 // row (column group pos ^ (key % 16)) and V row (dims of 32-byte block (pos/2) ^ (key % 8), half
@@ -2040,15 +2055,19 @@ struct CoLane {
   int key[2];   // key within the chunk
   int colk[2];  // element offset of the K piece within the key's row of kv head h
   int colv[2];  // element offset of the V piece
+  uint32_t off[4];  // byte offsets from the chunk's first key row of kv head h: K pieces t = 0, 1, then V
 };
 
 template <int MODE>
-__device__ __forceinline__ CoLane co_lane(int wv, int lane) {
+__device__ __forceinline__ CoLane co_lane(const Params& p, int wv, int lane) {
   CoLane c;
+  const uint32_t stride = 2 * p.Hkv * kD;  // elements per key row of the pool
   if constexpr (MODE == KV_FP8) {
     c.key[0] = c.key[1] = 8 * wv + (lane >> 3);
     c.colk[0] = c.colk[1] = 16 * (lane & 7);
     c.colv[0] = c.colv[1] = kD + 16 * (lane & 7);
+    c.off[0] = c.off[1] = (uint32_t)c.key[0] * stride + c.colk[0];  // (1-byte elements)
+    c.off[2] = c.off[3] = (uint32_t)c.key[0] * stride + c.colv[0];
     return c;
   }
   const int pos = lane & 15;
@@ -2058,6 +2077,8 @@ __device__ __forceinline__ CoLane co_lane(int wv, int lane) {
     c.key[t] = k;
     c.colk[t] = 8 * (pos ^ (k & 15));
     c.colv[t] = kD + 16 * ((pos >> 1) ^ (k & 7)) + 8 * (pos & 1);
+    c.off[t] = 2 * ((uint32_t)k * stride + c.colk[t]);
+    c.off[2 + t] = 2 * ((uint32_t)k * stride + c.colv[t]);
   }
   return c;
 }
@@ -2082,6 +2103,21 @@ __device__ __forceinline__ void co_issue(const Params& p, const PfTile& tl, cons
     pg = 0;
   }
   const int kmax = tl.kv_len - 1 - c * KV_CHUNK, stride = 2 * p.Hkv * kD;
+  if (kmax >= KV_CHUNK - 1) {  // every key of the chunk exists: a uniform base and the lane's fixed offsets
+    const uint8_t* base = p.kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h) * (MODE == KV_FP8 ? 1 : 2);
+    if constexpr (MODE == KV_FP8) {
+      co_dma_s(base, cl.off[0], dst + 1024u * wv);
+      co_dma_s(base, cl.off[2], dst + 4096u + 1024u * wv);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t i = (uint32_t)(wv + kCoWaves * t);
+        co_dma_s(base, cl.off[t], dst + 1024u * i);
+        co_dma_s(base, cl.off[2 + t], dst + 8192u + 1024u * i);
+      }
+    }
+    return;
+  }
   if constexpr (MODE == KV_FP8) {
     const uint8_t* base = p.kv + kv_elem(p, pg, c * KV_CHUNK, 2 * tl.h);
     const uint8_t* row = base + (unsigned)((cl.key[0] < kmax ? cl.key[0] : kmax) * stride);
@@ -2439,7 +2475,7 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
   int nvalid = nunits;
   int* pkey = (int*)(lds + kCoOrderBase);
   int* pord = pkey + kPfOrderMax;
-  const CoLane cln = co_lane<MODE>(wv, lane);
+  const CoLane cln = co_lane<MODE>(p, wv, lane);
   if (ranked) {
     // per sequence (256 entries each, over pord's area and the page table until they are
     // written): its first pair (the exclusive scan of the pair counts: never decreasing, and a

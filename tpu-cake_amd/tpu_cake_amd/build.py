@@ -36,6 +36,9 @@ def command(output: pathlib.Path = OUTPUT, extra: list[str] | None = None) -> li
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         # packed fp32 VALU ops are kept out of generated code on this platform
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # device code only: no NaN operands, so fmaxf needs no quieting v_max_f32 x, x before each
+        # use (infinities keep their meaning: masked scores are -inf); host-side checks keep NaN
+        "-Xarch_device", "-fno-honor-nans",
         f"-I{INCLUDE}", f"-I{CSRC}", *(extra or []),
         *[str(s) for s in SOURCES], "-o", str(output),
     ]
