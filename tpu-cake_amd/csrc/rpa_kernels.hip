@@ -344,6 +344,23 @@ __device__ __forceinline__ float rows4_max(float v) {
   return fmaxf(__builtin_bit_cast(float, (unsigned)c[0]), __builtin_bit_cast(float, (unsigned)c[1]));
 }
 
+// rows4_max of two values at once, in three swaps: permlane16_swap(a, b) gives rows (a0, b0, a2,
+// b2) and (a1, b1, a3, b3), whose maximum w holds a's and b's pairs; permlane32_swap(w, w) and a
+// maximum leave (A, B, A, B); permlane16_swap of that gives A in every lane of one result and B in
+// every lane of the other.
+__device__ __forceinline__ void rows4_max2(float& a, float& b) {
+  const auto s1 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b),
+                                                   false, false);
+  const float w = fmaxf(__builtin_bit_cast(float, (unsigned)s1[0]), __builtin_bit_cast(float, (unsigned)s1[1]));
+  const unsigned wu = __builtin_bit_cast(unsigned, w);
+  const auto s2 = __builtin_amdgcn_permlane32_swap(wu, wu, false, false);
+  const float x = fmaxf(__builtin_bit_cast(float, (unsigned)s2[0]), __builtin_bit_cast(float, (unsigned)s2[1]));
+  const unsigned xu = __builtin_bit_cast(unsigned, x);
+  const auto s3 = __builtin_amdgcn_permlane16_swap(xu, xu, false, false);
+  a = __builtin_bit_cast(float, (unsigned)s3[0]);
+  b = __builtin_bit_cast(float, (unsigned)s3[1]);
+}
+
 __device__ __forceinline__ float rows4_sum(float v) {
   const unsigned u = __builtin_bit_cast(unsigned, v);
   const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
@@ -1596,13 +1613,18 @@ struct PfRow {
   bool ok;   // the row exists (token in the tile, pos >= 0)
 };
 
-// One chunk for one 16-row block that every row sees in full (no masking, scale_log2 > 0).
-__device__ __forceinline__ bf16x8 pf_softmax_plain(const Params& p, const f32x4 sc[2], PfRow& st) {
+// The lane's maximum of one 16-row block's raw scores of a chunk (keys 16kb + 4j + rr of row n).
+__device__ __forceinline__ float pf_lane_max(const f32x4 sc[2]) {
+  return fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
+               fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
+}
+
+// One chunk for one 16-row block that every row sees in full (no masking, scale_log2 > 0), given
+// the row's maximum raw score of the chunk mraw (rows4_max of pf_lane_max).
+__device__ __forceinline__ bf16x8 pf_softmax_plain_m(const Params& p, const f32x4 sc[2], PfRow& st, float mraw) {
   // no masking: the raw scores' maximum, scaled once (scale_log2 > 0, so it commutes with the
   // rounding of each scaled score), and each probability as exp2(fma(s, scale, -m))
-  float mr = fmaxf(fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3])),
-                   fmaxf(fmaxf(sc[1][0], sc[1][1]), fmaxf(sc[1][2], sc[1][3])));
-  const float mc = rows4_max(mr) * p.scale_log2;
+  const float mc = mraw * p.scale_log2;
   const bool grow = mc > st.m + kRescaleLog2;
   if (__ballot(grow)) {
     const float mn = grow ? mc : st.m;
@@ -1625,6 +1647,10 @@ __device__ __forceinline__ bf16x8 pf_softmax_plain(const Params& p, const f32x4 
   pw[2] = pack_bf16x2(pr[1][0], pr[1][1]);
   pw[3] = pack_bf16x2(pr[1][2], pr[1][3]);
   return __builtin_bit_cast(bf16x8, pw);
+}
+
+__device__ __forceinline__ bf16x8 pf_softmax_plain(const Params& p, const f32x4 sc[2], PfRow& st) {
+  return pf_softmax_plain_m(p, sc, st, rows4_max(pf_lane_max(sc)));
 }
 
 // One chunk for one 16-row block: scores sc[kb] (keys 16kb + 4j + rr of row n), softmax update,
@@ -1712,8 +1738,10 @@ __device__ __forceinline__ void pf_compute(const Params& p, const PfTile& tl, in
   const uint8_t* vt = buf + kPfKBytes;
   bf16x8 pb0, pb1;
   if constexpr (PLAIN) {
-    pb0 = pf_softmax_plain(p, sc[0], st[0]);
-    pb1 = pf_softmax_plain(p, sc[1], st[1]);
+    float m0 = pf_lane_max(sc[0]), m1 = pf_lane_max(sc[1]);
+    rows4_max2(m0, m1);  // both row blocks' row maxima in three swaps
+    pb0 = pf_softmax_plain_m(p, sc[0], st[0], m0);
+    pb1 = pf_softmax_plain_m(p, sc[1], st[1], m1);
   } else {
     pb0 = pf_softmax(p, tl, c, sc[0], st[0], j);
     pb1 = pf_softmax(p, tl, c, sc[1], st[1], j);
@@ -2220,8 +2248,10 @@ __device__ __forceinline__ void co_pv(const Params& p, const PfTile& tl, int c, 
   read_vt_fragments_x(buf, n, j, va);
   bf16x8 pb0, pb1;
   if constexpr (PLAIN) {
-    pb0 = pf_softmax_plain(p, sc[0], st[0]);
-    pb1 = pf_softmax_plain(p, sc[1], st[1]);
+    float m0 = pf_lane_max(sc[0]), m1 = pf_lane_max(sc[1]);
+    rows4_max2(m0, m1);  // both row blocks' row maxima in three swaps
+    pb0 = pf_softmax_plain_m(p, sc[0], st[0], m0);
+    pb1 = pf_softmax_plain_m(p, sc[1], st[1], m1);
   } else {
     pb0 = pf_softmax(p, tl, c, sc[0], st[0], j);
     pb1 = pf_softmax(p, tl, c, sc[1], st[1], j);
