@@ -158,17 +158,49 @@ def test_combine_grid_matches_kernel_constants():
 
 
 def test_mixed_plan_splits_prefill_and_decode():
+    # C3 takes the co-resident layout: 4-wave workgroups, two per CU, tiles of 128 rows = 128 / G tokens
     text = contracts.render_workload("mi355x-rpa-c3")
     m = config_meta("c3")
-    tiles = sum(math.ceil(int(q) / 64) * 8 for q in m.q_lens if q >= 16)
-    got = re.search(r"prefill tiles = (\d+) tiles of 64 tokens x 1 kv head \((\d+) chunk steps\) on (\d+) workgroups",
-                    text)
+    hkv, group = m.num_kv_heads, m.num_q_heads // m.num_kv_heads
+    tq = 128 // group
+    assert "co-resident>: grid 512 x block 256" in text
+    tiles = sum(math.ceil(int(q) / tq) * hkv for q in m.q_lens if q >= 16)
+    got = re.search(rf"prefill tiles = (\d+) tiles of {tq} tokens x 1 kv head \((\d+) chunk steps\); "
+                    r"workgroups (\d+) \.\. (\d+) start on them", text)
     assert got and int(got.group(1)) == tiles
-    # chunk steps of the causal tiles: tile t of a 512-token chunk sees prior + 64 (t + 1) keys
-    steps = sum(8 * sum((int(L) - int(q) + 64 * (t + 1)) / 32 for t in range(math.ceil(int(q) / 64)))
+    # chunk steps of the causal tiles: tile t of a chunk sees prior + tq (t + 1) keys
+    steps = sum(hkv * sum((int(L) - int(q) + tq * (t + 1)) / 32 for t in range(math.ceil(int(q) / tq)))
                 for L, q in zip(m.kv_lens, m.q_lens) if q >= 16)
     assert int(got.group(2)) == round(steps)
-    assert 0 < int(got.group(3)) < 256
+    # at most one prefill-first workgroup per CU, numbered from grid / 2
+    assert int(got.group(3)) == 256 and 256 <= int(got.group(4)) <= 511
+    # merges (512 workgroups x 4 heads) + 17 heavy slots x 4 heads x 4 slices + 4 per CU for split tiles
+    assert contracts.combine_grid(512, 4, co=True) == 2048 + 272 + 1024
+    assert f"grid {2048 + 272 + 1024} x block 256" in text
+
+
+def test_co_resident_gate_follows_resolve_layout():
+    # resolve_layout's conditions, restated from the kernel source and checked against the model
+    assert re.search(r"p\.S % KV_CHUNK == 0 && p\.Hkv % kCoWaves == 0 &&\s*p\.G <= 32 \* kCoWaves && "
+                     r"\(long long\)shape->num_tokens >= \(long long\)shape->max_num_seqs \+ 15", KERNEL_SRC)
+    assert re.search(r"constexpr int kCoWaves = 4;", KERNEL_SRC)
+    assert contracts.co_resident(128, 8, 4, 64, 2048, 64, "bf16")
+    assert contracts.co_resident(128, 8, 4, 32, 2048, 64, "fp8")
+    assert not contracts.co_resident(128, 8, 4, 16, 2048, 64, "bf16")    # page not a multiple of 32
+    assert not contracts.co_resident(128, 2, 4, 64, 2048, 64, "bf16")    # Hkv not a multiple of 4
+    assert not contracts.co_resident(128, 8, 4, 64, 64 + 14, 64, "bf16")  # no room for a 16-token sequence
+    assert not contracts.co_resident(64, 8, 4, 64, 2048, 64, "bf16")     # narrow heads run through stream-K
+    for cfg in ("c2", "c4", "c5"):  # decode batches keep the 8-wave layout
+        assert "co-resident" not in contracts.render_workload(f"mi355x-rpa-{cfg}")
+
+
+def test_fused_plan_is_one_attention_launch():
+    text = contracts.render_workload("mi355x-inkling-fused-rpa")
+    assert "one call = the two launches below" in text
+    assert "launch 0 = rpa_attn_kernel<KV_BF16_FUSED, page ids per key>: grid 1024 x block 128" in text
+    # 1024 workgroups x 2 heads + 34 heavy slots x 2 heads x 4 slices + one per sequence (4)
+    assert "launch 1 = rpa_combine_kernel: grid 2324 x block 256" in text
+    assert "rpa_fused_prep_kernel" not in text and "launch 2" not in text
 
 
 def test_cli_writes_artifacts(tmp_path, capsys):

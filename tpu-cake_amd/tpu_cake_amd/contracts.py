@@ -232,9 +232,12 @@ HEAVY_CONTRIB = 32
 HEAVY_SLICES = 4
 
 
-def combine_grid(grid: int, hg: int) -> int:
-    """Workgroups of one combine launch: (descriptor, kv head) merges, then the heavy-merge helpers."""
-    return grid * hg + ((grid - 1) // (HEAVY_CONTRIB - 1) + 1) * hg * HEAVY_SLICES
+def combine_grid(grid: int, hg: int, co: bool = False, fused_seqs: int = 0) -> int:
+    """Workgroups of one combine launch: (descriptor, kv head) merges, then the heavy-merge helpers,
+    then (fused step) one per sequence storing its new token, or (co-resident layout) four per
+    split-tile slot, one slot per CU."""
+    return (grid * hg + ((grid - 1) // (HEAVY_CONTRIB - 1) + 1) * hg * HEAVY_SLICES + fused_seqs
+            + (4 * MI355X_CUS if co else 0))
 PF_MIN = 16                                 # query tokens that make a sequence a prefill one
 PF_COST = 0.45                              # prefill chunk-step cost in stream-K units
 
@@ -286,12 +289,26 @@ def _seq_units(kv_len: int, q_len: int, group: int) -> int:
     return sum(_rb_units(kv_len, q_len, group, rb) for rb in range(nrb))
 
 
-def _work_split(kv_lens, q_lens, hq: int, hkv: int, kv_dtype: str, prefill_tiles: bool) -> dict:
-    """Stream-K units, prefill tiles and the workgroup split the attention kernel computes."""
-    group, hg = hq // hkv, _heads_per_group(hkv)
+CO_WAVES = 4  # the co-resident layout's workgroups (csrc/rpa_kernels.hip, kCoWaves)
+
+
+def co_resident(head_dim: int, hkv: int, group: int, page_size: int, num_tokens: int, max_num_seqs: int,
+                kv_dtype: str) -> bool:
+    """Whether a call takes the co-resident layout (resolve_layout with the default knobs): 128-dim
+    heads, bf16 or fp8 KV, page size a multiple of 32, Hkv a multiple of 4, and a batch that can hold
+    a sequence of 16 query tokens."""
+    return (head_dim == 128 and kv_dtype in ("bf16", "fp8") and page_size % KV_CHUNK == 0
+            and hkv % CO_WAVES == 0 and group <= 32 * CO_WAVES and num_tokens >= max_num_seqs + 15)
+
+
+def _work_split(kv_lens, q_lens, hq: int, hkv: int, kv_dtype: str, prefill_tiles: bool, co: bool = False) -> dict:
+    """Stream-K units, prefill tiles and the workgroup split the attention kernel computes; co: the
+    co-resident layout (4-wave workgroups, two per CU, at most one prefill-first workgroup per CU)."""
+    group = hq // hkv
+    hg = CO_WAVES if co else _heads_per_group(hkv)
     ng = hkv // hg
     grid = MI355X_CUS * max(1, WAVES_PER_CU // hg)
-    tiles_on = prefill_tiles and kv_dtype == "bf16" and hg == 8 and len(kv_lens) <= 256
+    tiles_on = prefill_tiles and len(kv_lens) <= 256 and (co or (kv_dtype == "bf16" and hg == 8))
     pf_tq = 32 * hg // group if tiles_on else 0
     W, tiles, steps = 0, 0, 0.0
     for L, ql in zip(kv_lens, q_lens):
@@ -308,6 +325,8 @@ def _work_split(kv_lens, q_lens, hq: int, hkv: int, kv_dtype: str, prefill_tiles
         gpre = max(1, int(grid * pw / (pw + W) + 0.5))
         if W > 0:
             gpre = min(gpre, grid - 1)
+        if co:
+            gpre = min(gpre, grid // 2)
         gpre = min(gpre, tiles)
     gd = grid - gpre
     return dict(group=group, heads_per_workgroup=hg, kv_head_groups=ng, grid=grid, stream_k_units=W,
@@ -347,7 +366,9 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
                                     preflight="tpu_cake_amd.ops.static_validate_inputs",
                                     source_manifest=_source_manifest()),
     )
-    split = _work_split(m.kv_lens, m.q_lens, m.num_q_heads, m.num_kv_heads, m.kv_dtype, prefill_tiles=True)
+    co = co_resident(m.head_dim, m.num_kv_heads, m.num_q_heads // m.num_kv_heads, m.page_size, m.num_tokens,
+                     m.num_seqs, m.kv_dtype)
+    split = _work_split(m.kv_lens, m.q_lens, m.num_q_heads, m.num_kv_heads, m.kv_dtype, prefill_tiles=True, co=co)
     work = m.work()
     kv_bytes = work.kv_read_bytes + work.scale_bytes
     qo_bytes = work.q_bytes + work.o_bytes
@@ -360,13 +381,16 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
     line = upg and m.kv_dtype != "fp8"
     floor_hbm = fl["hbm_s"] * 1e6
     floor_mfma = fl["mfma_s"] * 1e6
+    half = split["grid"] // 2
+    fixed = co and split["prefill_workgroups"] == half and half % 8 == 0
     lines = [
         f"description = {CONFIG_DESCRIPTIONS[cfg]}",
         "entry = rpa_ragged_paged_attention (include/rpa.h); one call = the two launches below, stream-ordered",
         f"sequences = {m.num_seqs}; query tokens = {m.num_tokens}; sum kv_len = {int(sum(m.kv_lens))}",
         f"heads = Hq {m.num_q_heads} / Hkv {m.num_kv_heads} (G {split['group']}); head_dim {m.head_dim}; "
         f"page_size {m.page_size}; pool pages {m.pool_pages}; pages per sequence {m.pages_per_seq}",
-        f"launch 0 = rpa_attn_kernel<{mode}, page ids per {'chunk' if upg else 'key'}>: "
+        f"launch 0 = rpa_attn_kernel<{mode}, page ids per {'chunk' if upg else 'key'}"
+        f"{', co-resident' if co else ''}>: "
         f"grid {split['grid']} x block {64 * hg} ({hg} kv heads per workgroup, one wave each; "
         f"{WAVES_PER_CU} waves per CU), LDS {hg * WAVE_LDS_BYTES} B",
         f"  decode loads = {'whole 128-byte K/V lines, K through an LDS tile' if line else '16-byte operand loads'}",
@@ -374,11 +398,23 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
         f"{ROW_BLOCK}-row block) over {split['stream_k_workgroups']} workgroups "
         f"({split['units_per_workgroup'][0]}..{split['units_per_workgroup'][1]} units each); "
         f"{unit_bytes} KV bytes per unit per workgroup",
-        f"  prefill tiles = {split['prefill_tiles']} tiles of {split['prefill_tile_tokens']} tokens x 1 kv head "
-        f"({split['prefill_chunk_steps']} chunk steps) on {split['prefill_workgroups']} workgroups",
-        f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg)} x block 256 (one workgroup per "
+    ]
+    if co:
+        lines.append(
+            f"  prefill tiles = {split['prefill_tiles']} tiles of {split['prefill_tile_tokens']} tokens x 1 kv head "
+            f"({split['prefill_chunk_steps']} chunk steps); workgroups {half} .. {half + split['prefill_workgroups'] - 1} "
+            f"start on them, each beside the stream-K workgroup b - {half} on its CU, which joins when its range "
+            f"is done; tiles queued per XCD (tile t on XCD t mod 8)"
+            + (f", the first {2 * half // 8} positions of each XCD's queue fixed: the CU's prefill-first "
+               f"workgroup position k, its stream-K workgroup {2 * half // 8 - 1} - k" if fixed else ""))
+    else:
+        lines.append(
+            f"  prefill tiles = {split['prefill_tiles']} tiles of {split['prefill_tile_tokens']} tokens x 1 kv head "
+            f"({split['prefill_chunk_steps']} chunk steps) on {split['prefill_workgroups']} workgroups")
+    lines += [
+        f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg, co=co)} x block 256 (one workgroup per "
         f"(split descriptor, kv head), then {HEAVY_SLICES} per (heavy slot, kv head) for splits of "
-        f">= {HEAVY_CONTRIB} workgroups)",
+        f">= {HEAVY_CONTRIB} workgroups" + (", then 4 per split-tile slot" if co else "") + ")",
         f"algorithmic = KV {kv_bytes} B + Q/O {qo_bytes} B + metadata {work.metadata_bytes} B; "
         f"QK/PV {work.flops} FLOP (prefill rows {flops})",
         f"roofline floor = HBM {floor_hbm:.2f} us; MFMA {floor_mfma:.2f} us; bound = {fl['bound']}",
@@ -456,16 +492,17 @@ def _inkling_fused_workload() -> tuple[str, WorkloadContract, dict]:
         "relative-position bias relative_states . relative_projection for distances < E, scale 1/D "
         "(workloads/inkling_rpa.py:471-589)",
         "entry = rpa_inkling_fused_decode (include/rpa.h), after the host preflight "
-        "(rpa_lowering.py:71-128); one call = the four launches below, stream-ordered",
-        f"tokens = sequences = {N}; heads = Hq {Hq} / Hkv {Hkv}; head_dim {D} (rows padded to 128); page_size {S}; "
-        f"pages {P}; relative states R {R}, extent E {E}",
-        "launch 0 = rpa_fused_prep_kernel: block s writes sequence s's new K/V rows (16-byte stores); bias blocks "
-        "(4 q heads x 256 keys); grid-stride blocks expand the flat page list to a [N, pages per sequence] table",
-        f"launch 1 = rpa_attn_kernel<KV_BF16_BIAS>: grid {split['grid']} x block {64 * split['heads_per_workgroup']}",
-        f"launch 2 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'])} x block 256",
-        "launch 3 = rpa_fused_unpad_kernel: output rows 128 -> D",
+        "(rpa_lowering.py:71-128); one call = the two launches below, stream-ordered",
+        f"tokens = sequences = {N}; heads = Hq {Hq} / Hkv {Hkv}; head_dim {D} (cache rows padded to 128); "
+        f"page_size {S}; pages {P}; relative states R {R}, extent E {E}",
+        f"launch 0 = rpa_attn_kernel<KV_BF16_FUSED, page ids per key>: grid {split['grid']} x block "
+        f"{64 * split['heads_per_workgroup']}; sequence i's pages from page_indices[cu_kv_lens[i] / S], its new "
+        "token's K/V read from keys/values, queries and output rows D wide, the relative bias formed in the "
+        "kernel (one 16x16x16 MFMA per 16 keys)",
+        f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'], fused_seqs=N)}"
+        " x block 256; the last N workgroups store each sequence's new K/V rows in its cache slot",
     ]
-    kernels = ("rpa_fused_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_unpad_kernel")
+    kernels = ("rpa_attn_kernel", "rpa_combine_kernel")
     return _plan_text("mi355x-inkling-fused-rpa", lines), contract, dict(kernels=kernels)
 
 
