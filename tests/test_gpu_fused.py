@@ -81,6 +81,7 @@ def test_decode_shapes(cuda, hq, hkv, d, page, lens):
     # the prep launch: a window that is not a multiple of 8, a 32-wide projection
     (32, 8, 64, [5, 70, 200], 16, 20),
     (32, 8, 64, [5, 70, 200], 32, 64),
+    (32, 8, 64, [5, 70, 200], 64, 64),                # R = 64 (the reference's fused core takes 16 only)
 ])
 def test_bias_windows_and_launch_forms(cuda, hq, hkv, page, lens, rel_dim, extent):
     """Relative-bias windows at chunk edges and both forms of the call: the one-launch path (R in
