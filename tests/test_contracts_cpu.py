@@ -154,7 +154,12 @@ def test_combine_grid_matches_kernel_constants():
     assert int(const["kHeavySlices"]) == contracts.HEAVY_SLICES
     # 256 workgroups of 8 kv heads: 2048 merges + 9 slots x 8 heads x 4 slices
     assert contracts.combine_grid(256, 8) == 2048 + 288
-    assert f"grid {2048 + 288} x block 256" in contracts.render_workload("mi355x-rpa-c2")
+    # C2 (G 4, decode): two-wave combine workgroups; C5 (G 8) and C3 (co-resident) four-wave ones
+    assert f"grid {2048 + 288} x block 128" in contracts.render_workload("mi355x-rpa-c2")
+    assert "rpa_combine_kernel: grid 2336 x block 256" in contracts.render_workload("mi355x-rpa-c5")
+    assert re.search(r"int combine_waves\(const Params& p\) \{ return p\.G <= 4 && !p\.co && !p\.pf_kernel \? 2 : 4; \}",
+                     KERNEL_SRC)
+    assert [contracts.combine_waves(g, co) for g, co in ((1, False), (4, False), (8, False), (4, True))] == [2, 2, 4, 4]
 
 
 def test_mixed_plan_splits_prefill_and_decode():
@@ -199,7 +204,7 @@ def test_fused_plan_is_one_attention_launch():
     assert "one call = the two launches below" in text
     assert "launch 0 = rpa_attn_kernel<KV_BF16_FUSED, page ids per key>: grid 1024 x block 128" in text
     # 1024 workgroups x 2 heads + 34 heavy slots x 2 heads x 4 slices + one per sequence (4)
-    assert "launch 1 = rpa_combine_kernel: grid 2324 x block 256" in text
+    assert "launch 1 = rpa_combine_kernel: grid 2324 x block 128" in text
     assert "rpa_fused_prep_kernel" not in text and "launch 2" not in text
 
 

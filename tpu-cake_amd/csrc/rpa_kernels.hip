@@ -21,8 +21,8 @@
 //                         directly; a row block split across workgroups leaves one partial
 //                         (m, l, acc) per workgroup, and the workgroup owning its last unit leaves
 //                         a descriptor of it.
-//   rpa_combine_kernel  one 4-wave workgroup per (descriptor, head): the partials' (m, l, acc)
-//                       folded in one pass with coalesced loads (waves take every 4th
+//   rpa_combine_kernel  one 2- or 4-wave workgroup per (descriptor, head): the partials' (m, l, acc)
+//                       folded in one pass with coalesced loads (waves take every 2nd or 4th
 //                       contributor, running states merged through LDS); writes the rows,
 //                       clears the descriptor; blocks split over 32+ workgroups go to helper
 //                       workgroups, four per head, each over 32 dims; resets the prefill tile
@@ -3412,19 +3412,19 @@ __device__ __forceinline__ size_t combine_slot(const Params& p, const SplitDesc&
   return (size_t)partial_slot(d.b0 + k, k == 0) * p.HG + hw;
 }
 
-// One-pass merge of a split row block's partials.  A lane holds NP row slots: row RS*i + lane/(64/RS)
-// of the block, dims dim0 + 4*(lane % (64/RS)) .. +3 (RS = 2: two whole 512-byte rows per load
-// instruction; RS = 8: a 32-dim slice of eight rows).  Wave wv takes contributors wv, wv+4, ...,
-// U at a time with all their (m, l, acc) loads issued before any is used (sched_barrier), and
-// folds each into a running (m, l, o) with the online log-sum-exp update -- in contributor order,
-// so the result is deterministic.
+// One-pass merge of a split row block's partials by a workgroup of CW waves.  A lane holds NP row
+// slots: row RS*i + lane/(64/RS) of the block, dims dim0 + 4*(lane % (64/RS)) .. +3 (RS = 2: two
+// whole 512-byte rows per load instruction; RS = 8: a 32-dim slice of eight rows).  Wave wv takes
+// contributors wv, wv+CW, ..., U at a time with all their (m, l, acc) loads issued before any is
+// used (sched_barrier), and folds each into a running (m, l, o) with the online log-sum-exp update
+// -- in contributor order, so the result is deterministic.
 template <int NP>
 struct MergeAcc {
   f32x4 o[NP];
   float m[NP], l[NP];
 };
 
-template <int NP, int U, int RS>
+template <int CW, int NP, int U, int RS>
 __device__ __forceinline__ void merge_rows(const Params& p, const SplitDesc& d, int hw, int ncontrib, int wv, int lane,
                                            int row0, int dim0, MergeAcc<NP>& a) {
   constexpr int kLanesPerRow = 64 / RS;
@@ -3436,12 +3436,12 @@ __device__ __forceinline__ void merge_rows(const Params& p, const SplitDesc& d, 
     a.l[i] = 0.f;
   }
 #pragma unroll 1
-  for (int k = wv; k < ncontrib; k += 4 * U) {
+  for (int k = wv; k < ncontrib; k += CW * U) {
     f32x4 x[U][NP];
     float mc[U][NP], lc[U][NP];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int kk = k + 4 * u < ncontrib ? k + 4 * u : k;  // past the end: a valid slot, skipped below
+      const int kk = k + CW * u < ncontrib ? k + CW * u : k;  // past the end: a valid slot, skipped below
       const size_t sc = combine_slot(p, d, hw, kk);
       const float* ml = p.part_ml + sc * ROW_BLOCK * 2;
       const float* acc = p.part_acc + sc * ROW_BLOCK * kD + c4;
@@ -3456,7 +3456,7 @@ __device__ __forceinline__ void merge_rows(const Params& p, const SplitDesc& d, 
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (k + 4 * u < ncontrib)
+      if (k + CW * u < ncontrib)
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
           const float mn = fmaxf(a.m[i], mc[u][i]), mu = mn == -INFINITY ? 0.f : mn;
@@ -3468,12 +3468,13 @@ __device__ __forceinline__ void merge_rows(const Params& p, const SplitDesc& d, 
   }
 }
 
-// The four waves' running states merged through LDS (waves 1..3 into wave 0, in that order),
+// The CW waves' running states merged through LDS (waves 1..CW-1 into wave 0, in that order),
 // divided by the denominator and written as bf16: rows below nrows of descriptor d, head hw.
-template <int NP, int RS>
+// red / redml rows hold a lane's 4 NP (<= 16) o values and 2 NP (m, l) values, at odd strides.
+template <int CW, int NP, int RS>
 __device__ __forceinline__ void merge_waves_store(const Params& p, const SplitDesc& d, int hw, int nrows, int wv,
                                                   int lane, int row0, int dim0, const MergeAcc<NP>& a,
-                                                  float (*red)[64][33], float (*redml)[64][16]) {
+                                                  float (*red)[64][17], float (*redml)[64][9]) {
   constexpr int kLanesPerRow = 64 / RS;
   if (wv > 0) {
 #pragma unroll
@@ -3492,12 +3493,12 @@ __device__ __forceinline__ void merge_waves_store(const Params& p, const SplitDe
       const int row = RS * i + r0;
       if (row >= nrows) continue;
       float M = a.m[i];
-      for (int w = 0; w < 3; ++w) M = fmaxf(M, redml[w][lane][2 * i]);
+      for (int w = 0; w < CW - 1; ++w) M = fmaxf(M, redml[w][lane][2 * i]);
       const float mu = M == -INFINITY ? 0.f : M;
       float sw = __builtin_amdgcn_exp2f(a.m[i] - mu);
       f32x4 v = a.o[i] * sw;
       float L = a.l[i] * sw;
-      for (int w = 0; w < 3; ++w) {
+      for (int w = 0; w < CW - 1; ++w) {
         sw = __builtin_amdgcn_exp2f(redml[w][lane][2 * i] - mu);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += red[w][lane][4 * i + e] * sw;
@@ -3528,7 +3529,8 @@ __device__ __forceinline__ int rows_of(const Params& p, const SplitDesc& d) {
 // head and dim slice from the rest.  Its flag (set by the attention kernel) says whether the slot
 // holds a heavy descriptor this call; the flag and the slot's copy of the descriptor come in one
 // round trip.  The workgroup merges those 32 dims of the block's rows and clears its flag.
-__device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*red)[64][33], float (*redml)[64][16]) {
+template <int CW>
+__device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*red)[64][17], float (*redml)[64][9]) {
   const int slot = hb / (p.HG * kHeavySlices), rem = hb - slot * (p.HG * kHeavySlices);
   const int hw = rem / kHeavySlices, slice = rem - hw * kHeavySlices;
   int32_t* flag = p.heavy + ((size_t)slot * 8 + hw) * kHeavySlices + slice;
@@ -3542,12 +3544,13 @@ __device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*r
   const int ncontrib = (int)(b - d.b0 + 1), nrows = rows_of(p, d);
   if (nrows <= 8) {
     MergeAcc<1> a;
-    merge_rows<1, 8, 8>(p, d, hw, ncontrib, wv, lane, 0, 32 * slice, a);
-    merge_waves_store<1, 8>(p, d, hw, nrows, wv, lane, 0, 32 * slice, a, red, redml);
+    // two waves keep 32 contributors in flight as four do, each taking twice as many
+    merge_rows<CW, 1, CW == 2 ? 16 : 8, 8>(p, d, hw, ncontrib, wv, lane, 0, 32 * slice, a);
+    merge_waves_store<CW, 1, 8>(p, d, hw, nrows, wv, lane, 0, 32 * slice, a, red, redml);
   } else {
     MergeAcc<2> a;
-    merge_rows<2, 4, 8>(p, d, hw, ncontrib, wv, lane, 0, 32 * slice, a);
-    merge_waves_store<2, 8>(p, d, hw, nrows, wv, lane, 0, 32 * slice, a, red, redml);
+    merge_rows<CW, 2, 4, 8>(p, d, hw, ncontrib, wv, lane, 0, 32 * slice, a);
+    merge_waves_store<CW, 2, 8>(p, d, hw, nrows, wv, lane, 0, 32 * slice, a, red, redml);
   }
   if (t == 0) *flag = 0;
 }
@@ -3557,7 +3560,8 @@ __device__ __forceinline__ void combine_heavy(const Params& p, int hb, float (*r
 // blocks, so the decode merge reads them as slots of 16 rows (slot * 16 + g); its rows map to
 // (token, q head) as the tile's rows do: row 16 g + i -> token tok0 + (16 g + i) / G, head
 // h G + (16 g + i) % G.
-__device__ __forceinline__ void combine_prefill(const Params& p, int idx, float (*red)[64][33], float (*redml)[64][16]) {
+template <int CW>
+__device__ __forceinline__ void combine_prefill(const Params& p, int idx, float (*red)[64][17], float (*redml)[64][9]) {
   const int b = p.pk_grid - 1 - idx / 16, g = idx % 16;
   int valid = p.pk_desc[b].valid[g];
   PkDesc pd = p.pk_desc[b];
@@ -3579,14 +3583,14 @@ __device__ __forceinline__ void combine_prefill(const Params& p, int idx, float 
   const int ncontrib = (int)(b - d.b0 + 1), nrows = rows_of(p, d);
   if (nrows > 0 && nrows <= 4) {
     MergeAcc<2> a;
-    merge_rows<2, 4, 2>(pm, d, g, ncontrib, wv, lane, 0, 0, a);
-    merge_waves_store<2, 2>(ps, d, 0, nrows, wv, lane, 0, 0, a, red, redml);
+    merge_rows<CW, 2, 4, 2>(pm, d, g, ncontrib, wv, lane, 0, 0, a);
+    merge_waves_store<CW, 2, 2>(ps, d, 0, nrows, wv, lane, 0, 0, a, red, redml);
   } else if (nrows > 0) {
 #pragma unroll 1
     for (int row0 = 0; row0 < nrows; row0 += 8) {
       MergeAcc<4> a;
-      merge_rows<4, 1, 2>(pm, d, g, ncontrib, wv, lane, row0, 0, a);
-      merge_waves_store<4, 2>(ps, d, 0, nrows, wv, lane, row0, 0, a, red, redml);
+      merge_rows<CW, 4, 1, 2>(pm, d, g, ncontrib, wv, lane, row0, 0, a);
+      merge_waves_store<CW, 4, 2>(ps, d, 0, nrows, wv, lane, row0, 0, a, red, redml);
     }
   }
   if (t == 0) p.pk_desc[b].valid[g] = 0;
@@ -3671,20 +3675,27 @@ __device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
   if (t == 0) dp->valid[g] = 0;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
-  __shared__ float red[3][64][33];    // waves 1..3's o (33: conflict-free row stride)
-  __shared__ float redml[3][64][16];  // waves 1..3's (m, l) per row slot
+//
+// CW = 2 (decode merges of at most 4 rows, no co-resident or prefill-kernel splits; the host
+// chooses): two-wave workgroups, eight per CU, so a call's (descriptor, head) workgroups run in
+// one round where four-wave ones took two.
+template <int CW>
+__global__ __launch_bounds__(64 * CW) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
+  static_assert(CW == 2 || CW == 4, "combine workgroups of 2 or 4 waves");
+  __shared__ float red[CW - 1][64][17];   // waves 1..CW-1's o (odd stride: conflict-free)
+  __shared__ float redml[CW - 1][64][9];  // waves 1..CW-1's (m, l) per row slot
   if (blockIdx.x == 0 && threadIdx.x < kXcds) p.err[kQueueWord + threadIdx.x] = 0;  // tile queues, for the next call
   if ((int)blockIdx.x >= p.grid * p.HG) {
     const int hb = blockIdx.x - p.grid * p.HG, nheavy = heavy_slots(p.grid) * p.HG * kHeavySlices;
     if (hb < nheavy)
-      combine_heavy(p, hb, red, redml);
+      combine_heavy<CW>(p, hb, red, redml);
     else if (p.fused)
       fused_store_token(p, hb - nheavy);
-    else if (p.co)
-      combine_co_split(p, hb - nheavy);
-    else
-      combine_prefill(p, hb - nheavy, red, redml);
+    else if (p.co) {
+      if constexpr (CW == 4) combine_co_split(p, hb - nheavy);  // (256 threads: 32 rows x 8 lanes)
+    } else {
+      combine_prefill<CW>(p, hb - nheavy, red, redml);
+    }
     return;
   }
   // descriptor (last first: long splits end in late workgroups), wave (head) of its group
@@ -3701,15 +3712,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void r
     const int nrows = rows_of(p, d);
     if (nrows <= 4) {
       MergeAcc<2> a;
-      merge_rows<2, 4, 2>(p, d, hw, ncontrib, wv, lane, 0, 0, a);
-      merge_waves_store<2, 2>(p, d, hw, nrows, wv, lane, 0, 0, a, red, redml);
+      merge_rows<CW, 2, 4, 2>(p, d, hw, ncontrib, wv, lane, 0, 0, a);
+      merge_waves_store<CW, 2, 2>(p, d, hw, nrows, wv, lane, 0, 0, a, red, redml);
     } else {
       // rows 0..7, then (16-row blocks) rows 8..15
 #pragma unroll 1
       for (int row0 = 0; row0 < nrows; row0 += 8) {
         MergeAcc<4> a;
-        merge_rows<4, 1, 2>(p, d, hw, ncontrib, wv, lane, row0, 0, a);
-        merge_waves_store<4, 2>(p, d, hw, nrows, wv, lane, row0, 0, a, red, redml);
+        merge_rows<CW, 4, 1, 2>(p, d, hw, ncontrib, wv, lane, row0, 0, a);
+        merge_waves_store<CW, 4, 2>(p, d, hw, nrows, wv, lane, row0, 0, a, red, redml);
       }
     }
   }
@@ -3816,6 +3827,11 @@ int occupancy_grid(int cus, int hg) {
 // reference's block-size parameters) at most cus * waves_per_cu waves in all: floor(cus *
 // waves_per_cu / hg) workgroups, at least one.  With 8 waves per workgroup, waves_per_cu = 4 is
 // one workgroup per two CUs.
+// Waves per combine workgroup: 2 when a decode row block's merge covers at most 4 rows (G <= 4)
+// and no co-resident or prefill-kernel split tile needs the 256-thread merges; 4 otherwise
+// (rows of 8 and more, and many contributors, merge faster over four waves).
+int combine_waves(const Params& p) { return p.G <= 4 && !p.co && !p.pf_kernel ? 2 : 4; }
+
 int grid_rule(int occ, int cus, int hg, int waves_per_cu) {
   int grid = occ;
   if (waves_per_cu >= 1 && waves_per_cu < kMaxWavesPerCU) {
@@ -4589,11 +4605,14 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess && err_rc == RPA_OK)
     err_rc = fail(RPA_E_HIP, "hipEventRecord(end) failed");
   // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot, then 16 per
-  // prefill workgroup
-  hipLaunchKernelGGL(rpa_combine_kernel,
-                     dim3(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0) +
-                          (p.fused ? p.fused_nseq : 0) + (p.co ? 4 * p.co_split_max : 0)),
-                     dim3(256), 0, st, p);
+  // prefill workgroup; two-wave workgroups when every split is a decode row block of at most 4
+  // rows (G <= 4, no co-resident or prefill-kernel split tiles), four-wave ones otherwise
+  const dim3 cgrid(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0) +
+                   (p.fused ? p.fused_nseq : 0) + (p.co ? 4 * p.co_split_max : 0));
+  if (combine_waves(p) == 2)
+    hipLaunchKernelGGL(rpa_combine_kernel<2>, cgrid, dim3(128), 0, st, p);
+  else
+    hipLaunchKernelGGL(rpa_combine_kernel<4>, cgrid, dim3(256), 0, st, p);
   e = hipGetLastError();
   if (e != hipSuccess) {
     mark_workspace_dirty(workspace);

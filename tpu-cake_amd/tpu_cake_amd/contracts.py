@@ -232,6 +232,12 @@ HEAVY_CONTRIB = 32
 HEAVY_SLICES = 4
 
 
+def combine_waves(group: int, co: bool = False) -> int:
+    """Waves per combine workgroup (combine_waves in csrc/rpa_kernels.hip): 2 when a decode row
+    block's merge covers at most 4 rows (G <= 4) and no co-resident split tile is merged, else 4."""
+    return 2 if group <= 4 and not co else 4
+
+
 def combine_grid(grid: int, hg: int, co: bool = False, fused_seqs: int = 0) -> int:
     """Workgroups of one combine launch: (descriptor, kv head) merges, then the heavy-merge helpers,
     then (fused step) one per sequence storing its new token, or (co-resident layout) four per
@@ -412,7 +418,8 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
             f"  prefill tiles = {split['prefill_tiles']} tiles of {split['prefill_tile_tokens']} tokens x 1 kv head "
             f"({split['prefill_chunk_steps']} chunk steps) on {split['prefill_workgroups']} workgroups")
     lines += [
-        f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg, co=co)} x block 256 (one workgroup per "
+        f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg, co=co)} x block "
+        f"{64 * combine_waves(split['group'], co)} (one workgroup per "
         f"(split descriptor, kv head), then {HEAVY_SLICES} per (heavy slot, kv head) for splits of "
         f">= {HEAVY_CONTRIB} workgroups" + (", then 4 per split-tile slot" if co else "") + ")",
         f"algorithmic = KV {kv_bytes} B + Q/O {qo_bytes} B + metadata {work.metadata_bytes} B; "
@@ -452,7 +459,8 @@ def _inkling_v1_workload() -> tuple[str, WorkloadContract, dict]:
         "[P, S, 2H, 128] layout, writes the bias table by key position, cu_q = 0..B, num_seqs, padded queries",
         f"launch 1 = rpa_attn_kernel<KV_BF16_BIAS>: grid {split['grid']} x block {64 * split['heads_per_workgroup']}; "
         f"at most {split['stream_k_units']} stream-K units (sequences up to {L} keys)",
-        f"launch 2 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'])} x block 256",
+        f"launch 2 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'])} x block "
+        f"{64 * combine_waves(split['group'])}",
         "launch 3 = rpa_fused_unpad_kernel: output rows 128 -> D",
     ]
     kernels = ("rpa_inkling_v1_prep_kernel", "rpa_attn_kernel", "rpa_combine_kernel", "rpa_fused_unpad_kernel")
@@ -500,7 +508,8 @@ def _inkling_fused_workload() -> tuple[str, WorkloadContract, dict]:
         "token's K/V read from keys/values, queries and output rows D wide, the relative bias formed in the "
         "kernel (one 16x16x16 MFMA per 16 keys)",
         f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], split['heads_per_workgroup'], fused_seqs=N)}"
-        " x block 256; the last N workgroups store each sequence's new K/V rows in its cache slot",
+        f" x block {64 * combine_waves(split['group'])}; the last N workgroups store each sequence's new K/V rows "
+        "in its cache slot",
     ]
     kernels = ("rpa_attn_kernel", "rpa_combine_kernel")
     return _plan_text("mi355x-inkling-fused-rpa", lines), contract, dict(kernels=kernels)
