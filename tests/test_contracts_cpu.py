@@ -154,12 +154,12 @@ def test_combine_grid_matches_kernel_constants():
     assert int(const["kHeavySlices"]) == contracts.HEAVY_SLICES
     # 256 workgroups of 8 kv heads: 2048 merges + 9 slots x 8 heads x 4 slices
     assert contracts.combine_grid(256, 8) == 2048 + 288
-    # C2 (G 4, decode): two-wave combine workgroups; C5 (G 8) and C3 (co-resident) four-wave ones
+    # C2 and C3 (G 4): two-wave combine workgroups; C5 (G 8) four-wave ones
     assert f"grid {2048 + 288} x block 128" in contracts.render_workload("mi355x-rpa-c2")
     assert "rpa_combine_kernel: grid 2336 x block 256" in contracts.render_workload("mi355x-rpa-c5")
-    assert re.search(r"int combine_waves\(const Params& p\) \{ return p\.G <= 4 && !p\.co && !p\.pf_kernel \? 2 : 4; \}",
+    assert re.search(r"int combine_waves\(const Params& p\) \{ return p\.G <= 4 && !p\.pf_kernel \? 2 : 4; \}",
                      KERNEL_SRC)
-    assert [contracts.combine_waves(g, co) for g, co in ((1, False), (4, False), (8, False), (4, True))] == [2, 2, 4, 4]
+    assert [contracts.combine_waves(g) for g in (1, 2, 4, 8, 16)] == [2, 2, 2, 4, 4]
 
 
 def test_mixed_plan_splits_prefill_and_decode():
@@ -181,7 +181,7 @@ def test_mixed_plan_splits_prefill_and_decode():
     assert int(got.group(3)) == 256 and 256 <= int(got.group(4)) <= 511
     # merges (512 workgroups x 4 heads) + 17 heavy slots x 4 heads x 4 slices + 4 per CU for split tiles
     assert contracts.combine_grid(512, 4, co=True) == 2048 + 272 + 1024
-    assert f"grid {2048 + 272 + 1024} x block 256" in text
+    assert f"grid {2048 + 272 + 1024} x block 128" in text
 
 
 def test_co_resident_gate_follows_resolve_layout():

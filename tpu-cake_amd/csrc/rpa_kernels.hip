@@ -3629,8 +3629,9 @@ __device__ __forceinline__ void fused_store_token(const Params& p, int s) {
 }
 
 // Co-resident split tile merge: workgroup idx merges rows 32 g .. 32 g + 31 (g = idx % 4) of split
-// tile idx / 4 from its nparts partial slots: thread t takes row 32 g + t / 8, dims 16 (t % 8) ..
-// +15, folds the parts in order with the online log-sum-exp update and writes bf16.
+// tile idx / 4 from its nparts partial slots: thread t takes rows 32 g + t / 8 (+ blockDim / 8 ...),
+// dims 16 (t % 8) .. +15, folds the parts in order with the online log-sum-exp update and writes
+// bf16.
 __device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
   const int st = idx >> 2, g = idx & 3;
   if (st >= p.co_split_max) return;
@@ -3639,9 +3640,11 @@ __device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
   CoDesc d = *dp;
   asm volatile("" : "+v"(valid), "+v"(d.q_row0), "+v"(d.ntok), "+v"(d.h), "+v"(d.nparts), "+v"(d.slot0));
   if (!__builtin_amdgcn_readfirstlane(valid)) return;
-  const int t = threadIdx.x, row = 32 * g + (t >> 3), c16 = 16 * (t & 7);
+  const int t = threadIdx.x, c16 = 16 * (t & 7);
   const int nparts = __builtin_amdgcn_readfirstlane(d.nparts);
-  if (row < d.ntok * p.G) {
+#pragma unroll 1
+  for (int row = 32 * g + (t >> 3); row < 32 * g + 32; row += (int)(blockDim.x >> 3)) {
+    if (row >= d.ntok * p.G) break;
     f32x4 o[4];
     float m = -INFINITY, l = 0.f;
 #pragma unroll
@@ -3676,9 +3679,9 @@ __device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
 }
 
 //
-// CW = 2 (decode merges of at most 4 rows, no co-resident or prefill-kernel splits; the host
-// chooses): two-wave workgroups, eight per CU, so a call's (descriptor, head) workgroups run in
-// one round where four-wave ones took two.
+// CW = 2 (G <= 4: a decode row block's merge covers at most 4 rows; no prefill-kernel split
+// tiles; the host chooses): two-wave workgroups, eight per CU, so a call's workgroups run in half
+// the rounds of four-wave ones.
 template <int CW>
 __global__ __launch_bounds__(64 * CW) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
   static_assert(CW == 2 || CW == 4, "combine workgroups of 2 or 4 waves");
@@ -3691,11 +3694,10 @@ __global__ __launch_bounds__(64 * CW) __attribute__((amdgpu_waves_per_eu(4))) vo
       combine_heavy<CW>(p, hb, red, redml);
     else if (p.fused)
       fused_store_token(p, hb - nheavy);
-    else if (p.co) {
-      if constexpr (CW == 4) combine_co_split(p, hb - nheavy);  // (256 threads: 32 rows x 8 lanes)
-    } else {
+    else if (p.co)
+      combine_co_split(p, hb - nheavy);
+    else
       combine_prefill<CW>(p, hb - nheavy, red, redml);
-    }
     return;
   }
   // descriptor (last first: long splits end in late workgroups), wave (head) of its group
@@ -3828,9 +3830,9 @@ int occupancy_grid(int cus, int hg) {
 // waves_per_cu / hg) workgroups, at least one.  With 8 waves per workgroup, waves_per_cu = 4 is
 // one workgroup per two CUs.
 // Waves per combine workgroup: 2 when a decode row block's merge covers at most 4 rows (G <= 4)
-// and no co-resident or prefill-kernel split tile needs the 256-thread merges; 4 otherwise
-// (rows of 8 and more, and many contributors, merge faster over four waves).
-int combine_waves(const Params& p) { return p.G <= 4 && !p.co && !p.pf_kernel ? 2 : 4; }
+// and no prefill-kernel split tile needs the 256-thread merges; 4 otherwise (rows of 8 and more
+// merge faster over four waves).
+int combine_waves(const Params& p) { return p.G <= 4 && !p.pf_kernel ? 2 : 4; }
 
 int grid_rule(int occ, int cus, int hg, int waves_per_cu) {
   int grid = occ;
@@ -4605,8 +4607,8 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess && err_rc == RPA_OK)
     err_rc = fail(RPA_E_HIP, "hipEventRecord(end) failed");
   // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot, then 16 per
-  // prefill workgroup; two-wave workgroups when every split is a decode row block of at most 4
-  // rows (G <= 4, no co-resident or prefill-kernel split tiles), four-wave ones otherwise
+  // prefill workgroup; two-wave workgroups when a decode row block has at most 4 rows (G <= 4,
+  // no prefill-kernel split tiles), four-wave ones otherwise
   const dim3 cgrid(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0) +
                    (p.fused ? p.fused_nseq : 0) + (p.co ? 4 * p.co_split_max : 0));
   if (combine_waves(p) == 2)

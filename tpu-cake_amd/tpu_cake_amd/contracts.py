@@ -232,10 +232,10 @@ HEAVY_CONTRIB = 32
 HEAVY_SLICES = 4
 
 
-def combine_waves(group: int, co: bool = False) -> int:
-    """Waves per combine workgroup (combine_waves in csrc/rpa_kernels.hip): 2 when a decode row
-    block's merge covers at most 4 rows (G <= 4) and no co-resident split tile is merged, else 4."""
-    return 2 if group <= 4 and not co else 4
+def combine_waves(group: int) -> int:
+    """Waves per combine workgroup (combine_waves in csrc/rpa_kernels.hip, default knobs): 2 when a
+    decode row block's merge covers at most 4 rows (G <= 4), else 4."""
+    return 2 if group <= 4 else 4
 
 
 def combine_grid(grid: int, hg: int, co: bool = False, fused_seqs: int = 0) -> int:
@@ -419,7 +419,7 @@ def _operator_workload(cfg: str) -> tuple[str, WorkloadContract, dict]:
             f"({split['prefill_chunk_steps']} chunk steps) on {split['prefill_workgroups']} workgroups")
     lines += [
         f"launch 1 = rpa_combine_kernel: grid {combine_grid(split['grid'], hg, co=co)} x block "
-        f"{64 * combine_waves(split['group'], co)} (one workgroup per "
+        f"{64 * combine_waves(split['group'])} (one workgroup per "
         f"(split descriptor, kv head), then {HEAVY_SLICES} per (heavy slot, kv head) for splits of "
         f">= {HEAVY_CONTRIB} workgroups" + (", then 4 per split-tile slot" if co else "") + ")",
         f"algorithmic = KV {kv_bytes} B + Q/O {qo_bytes} B + metadata {work.metadata_bytes} B; "
