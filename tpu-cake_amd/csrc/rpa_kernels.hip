@@ -3525,7 +3525,7 @@ __device__ __forceinline__ int rows_of(const Params& p, const SplitDesc& d) {
   return nrows < ROW_BLOCK ? nrows : ROW_BLOCK;
 }
 
-// Helper workgroup hb (after the grid*HG merge workgroups): heavy slot hb / (HG * kHeavySlices),
+// Helper workgroup hb (the first workgroups of the launch): heavy slot hb / (HG * kHeavySlices),
 // head and dim slice from the rest.  Its flag (set by the attention kernel) says whether the slot
 // holds a heavy descriptor this call; the flag and the slot's copy of the descriptor come in one
 // round trip.  The workgroup merges those 32 dims of the block's rows and clears its flag.
@@ -3598,9 +3598,9 @@ __device__ __forceinline__ void combine_prefill(const Params& p, int idx, float 
 
 // Workgroup b merges the row block described by desc[b] for head hw: contributors b0..b, b0's
 // share in slot 2*b0+1 and every later one's in slot 2*bb (merge_rows, merge_waves_store), unless
-// the block is heavy (its slot's helper workgroups merge it).  After the (descriptor, head)
-// workgroups come the heavy-merge helpers, then (with the prefill kernel) 16 per prefill
-// workgroup for its split tiles.
+// the block is heavy (its slot's helper workgroups merge it).  The heavy-merge helpers come
+// first in the launch, then the (descriptor, head) workgroups, then (with the prefill kernel) 16
+// per prefill workgroup for its split tiles.
 // Fused decode step: block s stores sequence s's new token (key kv_len-1, K of kv head h at combined
 // row 2h, V at 2h+1) into the cache, at slot (kv_len-1) % S of page page_indices[cu_kv[s] / S +
 // (kv_len-1) / S] (src/tpu_cake/workloads/inkling_rpa.py:518-534).  The attention kernel read
@@ -3688,20 +3688,26 @@ __global__ __launch_bounds__(64 * CW) __attribute__((amdgpu_waves_per_eu(4))) vo
   __shared__ float red[CW - 1][64][17];   // waves 1..CW-1's o (odd stride: conflict-free)
   __shared__ float redml[CW - 1][64][9];  // waves 1..CW-1's (m, l) per row slot
   if (blockIdx.x == 0 && threadIdx.x < kXcds) p.err[kQueueWord + threadIdx.x] = 0;  // tile queues, for the next call
-  if ((int)blockIdx.x >= p.grid * p.HG) {
-    const int hb = blockIdx.x - p.grid * p.HG, nheavy = heavy_slots(p.grid) * p.HG * kHeavySlices;
-    if (hb < nheavy)
-      combine_heavy<CW>(p, hb, red, redml);
-    else if (p.fused)
-      fused_store_token(p, hb - nheavy);
+  // the heavy-merge helpers first (a heavy merge is the longest, so it starts with the launch),
+  // then the (descriptor, head) merges, then the rest
+  const int nheavy = heavy_slots(p.grid) * p.HG * kHeavySlices;
+  if ((int)blockIdx.x < nheavy) {
+    combine_heavy<CW>(p, blockIdx.x, red, redml);
+    return;
+  }
+  const int mb = (int)blockIdx.x - nheavy;
+  if (mb >= p.grid * p.HG) {
+    const int hb = mb - p.grid * p.HG;
+    if (p.fused)
+      fused_store_token(p, hb);
     else if (p.co)
-      combine_co_split(p, hb - nheavy);
+      combine_co_split(p, hb);
     else
-      combine_prefill<CW>(p, hb - nheavy, red, redml);
+      combine_prefill<CW>(p, hb, red, redml);
     return;
   }
   // descriptor (last first: long splits end in late workgroups), wave (head) of its group
-  const int bi = blockIdx.x / p.HG, hw = blockIdx.x - bi * p.HG, b = p.grid - 1 - bi;
+  const int bi = mb / p.HG, hw = mb - bi * p.HG, b = p.grid - 1 - bi;
   // the flag and the fields in one round trip (the empty asm keeps the compiler from moving the
   // field loads behind the flag test)
   int valid = p.desc[b].valid[hw];
@@ -4606,7 +4612,7 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
   }
   if (ev_end && hipEventRecord((hipEvent_t)ev_end, st) != hipSuccess && err_rc == RPA_OK)
     err_rc = fail(RPA_E_HIP, "hipEventRecord(end) failed");
-  // one workgroup per (descriptor, head), then the heavy-merge helpers of every slot, then 16 per
+  // the heavy-merge helpers of every slot, then one workgroup per (descriptor, head), then 16 per
   // prefill workgroup; two-wave workgroups when a decode row block has at most 4 rows (G <= 4,
   // no prefill-kernel split tiles), four-wave ones otherwise
   const dim3 cgrid(p.grid * p.HG + heavy_slots(p.grid) * p.HG * kHeavySlices + (p.pf_kernel ? 16 * p.pk_grid : 0) +
