@@ -3678,10 +3678,9 @@ __device__ __forceinline__ void combine_co_split(const Params& p, int idx) {
   if (t == 0) dp->valid[g] = 0;
 }
 
-//
-// CW = 2 (G <= 4: a decode row block's merge covers at most 4 rows; no prefill-kernel split
-// tiles; the host chooses): two-wave workgroups, eight per CU, so a call's workgroups run in half
-// the rounds of four-wave ones.
+// The merge launch, in workgroups of CW waves.  CW = 2 (G <= 4: a decode row block's merge covers
+// at most 4 rows; no prefill-kernel split tiles; the host chooses): two-wave workgroups, eight per
+// CU, so a call's workgroups run in half the rounds of four-wave ones.
 template <int CW>
 __global__ __launch_bounds__(64 * CW) __attribute__((amdgpu_waves_per_eu(4))) void rpa_combine_kernel(Params p) {
   static_assert(CW == 2 || CW == 4, "combine workgroups of 2 or 4 waves");
