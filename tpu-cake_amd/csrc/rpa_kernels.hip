@@ -1023,11 +1023,12 @@ __device__ __forceinline__ bf16x8 unit_softmax(const Params& p, const Cursor& x,
 // 16h + 4j + e, the order the QK^T output holds).  ds_read_b64_tr_b16 transposes within each
 // 16-lane group: lane n of group j reads dims 16d + 4(n%4) .. +3 of key 16h + 4j + n/4, and lane n
 // receives dim 16d + n of keys 16h + 4j .. +3.
+template <int ND = 8>  // the first ND 16-dim blocks (narrow heads fill fewer than 8)
 __device__ __forceinline__ void read_vt_fragments(const uint8_t* vt, int n, int j, bf16x8 va[8]) {
   typedef __attribute__((address_space(3))) short4_t* lds_s4;
   const uint8_t* vb = vt + (4 * j + (n >> 2)) * kVRow + 8 * (n & 3);
 #pragma unroll
-  for (int d = 0; d < 8; ++d) {
+  for (int d = 0; d < ND; ++d) {
     const short4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(vb + 32 * d));
     const short4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(vb + 16 * kVRow + 32 * d));
     va[d] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -1235,6 +1236,20 @@ struct LineRegs {
   u32x4 w[8];  // load i: key 4i + lane/16, dims 8*(lane%16) .. +7 of the K (or V) row
 };
 
+// DN = 32 or 64 (instantiations for those head dims; 0 = rows of kD elements): rows of DN
+// elements, load i (i < DN/16) covering keys (512/DN) i .. +512/DN-1, lane L holding key
+// (512/DN) i + L/(DN/8), dims 8*(L % (DN/8)) .. +7 -- DN/16 loads per unit half instead of 8,
+// each reading whole rows -- and QK^T / PV over the DN/32 k-steps and DN/16 dim blocks those rows
+// fill (the K tile's and V region's columns past DN are neither written nor read).
+template <int DN>
+struct Lines {
+  static constexpr int loads = DN ? DN / 16 : 8;      // per unit half
+  static constexpr int keys = 32 / loads;             // keys per load
+  static constexpr int lanes = 64 / keys;             // lanes per key
+  static constexpr int ksteps = DN ? DN / 32 : 4;     // QK^T k-steps of 32 dims
+  static constexpr int dblocks = DN ? DN / 16 : 8;    // PV dim blocks of 16
+};
+
 struct LineAddr {
   size_t e0;    // element index of this lane's dims of the unit's first key, K row
   int kmax;     // the unit's last key with data (keys past it read it instead)
@@ -1244,7 +1259,7 @@ struct LineAddr {
   int row;        // fused step, pages smaller than a unit: pool row (page * S + slot) of key lane % 32
 };
 
-template <int MODE, bool UPG = true>
+template <int MODE, bool UPG = true, int DN = 0>
 __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, const Pages& pages, int lane, int n,
                                               int j, int wv, int& err, int D = kD) {
   LineAddr a;
@@ -1274,8 +1289,9 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
   const UnitAddr u = unit_addr(p, x, pages, n, j, wv, err, D);  // page checks, head, bias position
   a.row = 0;
   // (a narrow pool's pieces wholly past D read the row's first piece, as in load_half)
+  const int piece = 8 * (lane & (Lines<DN>::lanes - 1));
   a.e0 = kv_elem(p, u.pg[0], live ? x.key0() : 0, 2 * u.h, D) + half_offset(live ? x.h * p.HG + wv : 0, D) +
-         (D == kD || 8 * (lane & 15) < D ? 8 * (lane & 15) : 0);
+         (D == kD || piece < D ? piece : 0);
   const int k = live ? x.kv_len - 1 - x.key0() : 0;
   a.kmax = k < KV_CHUNK - 1 ? k : KV_CHUNK - 1;
   a.bias_at = u.bias_at;
@@ -1292,11 +1308,22 @@ __device__ __forceinline__ LineAddr line_addr(const Params& p, const Cursor& x, 
 }
 
 // which = 0: K rows (combined head 2h), 1: V rows (2h+1).
-template <int MODE, bool UPG = true>
+template <int MODE, bool UPG = true, int DN = 0>
 __device__ __forceinline__ void load_lines(const Params& p, const LineAddr& a, int lane, int which, LineRegs& r,
                                            int D = kD) {
   const uint16_t* kv = (const uint16_t*)p.kv + a.e0 + (size_t)which * D;
   const size_t row = (size_t)(2 * p.Hkv) * D;
+  if constexpr (DN != 0) {
+    static_assert(UPG && MODE != KV_BF16_FUSED, "narrow rows: whole-page units, cache rows of D");
+    using L = Lines<DN>;
+#pragma unroll
+    for (int i = 0; i < L::loads; ++i) {
+      int key = L::keys * i + lane / L::lanes;
+      key = key < a.kmax ? key : a.kmax;
+      r.w[i] = ld_stream((const u32x4*)(kv + (size_t)key * row));
+    }
+    return;
+  }
   const uint16_t* nw = nullptr;
   if constexpr (MODE == KV_BF16_FUSED) nw = (which ? p.new_v : p.new_k) + a.newoff;
 #pragma unroll
@@ -1398,25 +1425,27 @@ __device__ __forceinline__ u32x4 line_word(const LineRegs& r, int i, const Param
 }
 
 // K of a unit into the wave's K tile.
-template <int MODE>
+template <int MODE, int DN = 0>
 __device__ __forceinline__ void store_k_tile(const Params& p, const LineRegs& k, uint8_t* kt, int lane) {
   wave_lds_fence();  // the tile's previous unit has been read
+  using L = Lines<DN>;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    *(u32x4*)(kt + (4 * i + (lane >> 4)) * kKtRow + (lane & 15) * 16) = line_word<MODE>(k, i, p, 0);
+  for (int i = 0; i < L::loads; ++i)
+    *(u32x4*)(kt + (L::keys * i + lane / L::lanes) * kKtRow + (lane % L::lanes) * 16) = line_word<MODE>(k, i, p, 0);
 }
 
 // compute_unit with K read from the K tile, V stored as key rows from the line layout and the
 // next unit's V loaded into v (after that store).
-template <int MODE, bool UPG = true>
+template <int MODE, bool UPG = true, int DN = 0>
 __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor& x, LineRegs& v, const f32x4* bias,
                                                   bf16x8 q[4], uint32_t rst[2], const Cursor& nx,
                                                   const LineAddr& nx_addr,
                                                   RowState& st, uint8_t* vt, const uint8_t* kt, int lane, int n,
                                                   int j, int wv, int D = kD, int Dq = kD) {
+  using L = Lines<DN>;
   f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < L::ksteps; ++s) {
     const bf16x8 a0 = *(const bf16x8*)(kt + n * kKtRow + (32 * s + 8 * j) * 2);
     const bf16x8 a1 = *(const bf16x8*)(kt + (16 + n) * kKtRow + (32 * s + 8 * j) * 2);
     s0 = mfma(a0, q[s], s0);
@@ -1427,26 +1456,26 @@ __device__ __forceinline__ void compute_unit_line(const Params& p, const Cursor&
   // V as key rows (key 4i + lane/16, kVRow stride), as the K tile; read back transposed below
   wave_lds_fence();
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    *(u32x4*)(vt + (4 * i + (lane >> 4)) * kVRow + (lane & 15) * 16) = line_word<MODE>(v, i, p, 1);
+  for (int i = 0; i < L::loads; ++i)
+    *(u32x4*)(vt + (L::keys * i + lane / L::lanes) * kVRow + (lane % L::lanes) * 16) = line_word<MODE>(v, i, p, 1);
   // a new row block's queries (else q already holds its rows), issued after the wait for this
   // unit's V: vmcnt retires in order and the compiler counts the path without these loads, so
   // issued before it they would make that wait also retire the next unit's K
   if (nx.c == 0) load_q<MODE>(p, nx, n, j, wv, q, rst, Dq);
-  load_lines<MODE, UPG>(p, nx_addr, lane, 1, v, D);
+  load_lines<MODE, UPG, DN>(p, nx_addr, lane, 1, v, D);
 
   const bf16x8 pb = unit_softmax<MODE>(p, x, s0, s1, bias, st, j);
 
   wave_lds_fence();
   bf16x8 va[8];
-  read_vt_fragments(vt, n, j, va);
+  read_vt_fragments<L::dblocks>(vt, n, j, va);
 #pragma unroll
-  for (int d = 0; d < 8; ++d) st.acc[d] = mfma(va[d], pb, st.acc[d]);
+  for (int d = 0; d < L::dblocks; ++d) st.acc[d] = mfma(va[d], pb, st.acc[d]);
   __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
   __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
 }
 
-template <int MODE, bool UPG>
+template <int MODE, bool UPG, int DN = 0>
 __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, int n, int j, int b, long long u,
                                           long long u0, long long u1, Window& win, Cursor& cur, Cursor& nxt,
                                           Pages& pg_nxt, LineRegs& k, LineRegs& v, f32x4 bias[2], bf16x8 q[4],
@@ -1459,20 +1488,20 @@ __device__ __forceinline__ void step_line(const Params& p, int nseq, int lane, i
   else
     ahead.nch = 0;
   const Pages pg_ahead = load_pages<MODE, UPG>(p, ahead, n);
-  const LineAddr nx_addr = line_addr<MODE, UPG>(p, nxt, pg_nxt, lane, n, j, wv, err, D);
+  const LineAddr nx_addr = line_addr<MODE, UPG, DN>(p, nxt, pg_nxt, lane, n, j, wv, err, D);
   __syncthreads();
-  load_lines<MODE, UPG>(p, nx_addr, lane, 0, k, D);  // the next unit's K (this unit's K is in the tile)
+  load_lines<MODE, UPG, DN>(p, nx_addr, lane, 0, k, D);  // the next unit's K (this unit's K is in the tile)
   LineBias bias_nx;
   load_line_bias<MODE>(p, nxt, nx_addr, lane, n, j, wv, bias_nx);
 
   if (u == u0 || cur.c == 0) begin_row_block(p, cur, st, n);
   // the fused step's queries and output rows are p.D wide (its cache rows kD)
   const int Dq = MODE == KV_BF16_FUSED ? p.D : D;
-  compute_unit_line<MODE, UPG>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D, Dq);
+  compute_unit_line<MODE, UPG, DN>(p, cur, v, bias, q, rst, nxt, nx_addr, st, vt, kt, lane, n, j, wv, D, Dq);
   // The next unit's K goes to the tile before a row block's finish stores: its wait then counts
   // the same younger operations (the next unit's V) on every path.  Issued before it, the stores
   // made that wait also retire most of the V just loaded on the steps that end a row block.
-  store_k_tile<MODE>(p, k, kt, lane);
+  store_k_tile<MODE, DN>(p, k, kt, lane);
   const bool last_of_rb = cur.c == cur.nch - 1;
   if (last_of_rb || u == u1 - 1) {
     const bool complete = st.started_here && last_of_rb;
@@ -2659,11 +2688,14 @@ __device__ __forceinline__ void co_role(const Params& p, const SeqInfo wsi[4], i
 // CO: the co-resident layout's instantiation (p.co set), with the co-resident prefill role; the
 // other instantiations carry the 8-wave prefill role (plain bf16 KV) or none, so the decode-only
 // launches keep the registers of a kernel without the co-resident role.
-// NW: a narrow head dim (p.D < kD; decode role only, every row through stream-K).
-template <int MODE, bool UPG, bool CO = false, bool NW = false>
+// NW: a narrow head dim (p.D < kD; decode role only, every row through stream-K).  DN: a narrow
+// head dim of 32 or 64 fixed at compile time, whose full-line loads read whole DN-element rows
+// (Lines<DN>).
+template <int MODE, bool UPG, bool CO = false, bool NW = false, int DN = 0>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void rpa_attn_kernel(Params p) {
+  static_assert(DN == 0 || (NW && UPG && (DN == 32 || DN == 64)), "DN: a narrow instantiation of 32 or 64");
   constexpr bool kTiles = NW ? false : CO ? co_tiles<MODE>() : MODE == KV_BF16;  // a prefill-tile role exists
-  const int D = NW ? p.D : kD;
+  const int D = DN ? DN : NW ? p.D : kD;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // HG x (V region, K tile)
   const int lane = threadIdx.x & 63;
   const int wv = uni(threadIdx.x >> 6);
@@ -2848,19 +2880,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // K, bias, queries, V: the loop's order (vmcnt retires in order, and the compiler
         // counts each wait for the least favourable path into it, this prologue included)
         {
-          const LineAddr a0 = line_addr<MODE, UPG>(p, cur, pg_cur, lane, n, j, wv, err, D);
-          load_lines<MODE, UPG>(p, a0, lane, 0, k, D);
+          const LineAddr a0 = line_addr<MODE, UPG, DN>(p, cur, pg_cur, lane, n, j, wv, err, D);
+          load_lines<MODE, UPG, DN>(p, a0, lane, 0, k, D);
           load_line_bias<MODE>(p, cur, a0, lane, n, j, wv, bias_in);
           load_q<MODE>(p, cur, n, j, wv, q, rst, MODE == KV_BF16_FUSED ? p.D : D);
-          load_lines<MODE, UPG>(p, a0, lane, 1, v, D);
+          load_lines<MODE, UPG, DN>(p, a0, lane, 1, v, D);
         }
         RPA_TL(tl_set(TL_FIRST, tl_clock()); tl_set(TL_UNITS, u1 - u0); tl_role |= 2;)
-        store_k_tile<MODE>(p, k, kt, lane);
+        store_k_tile<MODE, DN>(p, k, kt, lane);
         line_bias_values<MODE>(p, cur, bias_in, rst, rs, lane, n, j, bias);
         RowState st;
         long long u = u0;
         for (;;) {
-          step_line<MODE, UPG>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, k, v, bias, q, rst, st, vt,
+          step_line<MODE, UPG, DN>(p, nseq, lane, n, j, bd, u, u0, u1, win, cur, nxt, pg_nxt, k, v, bias, q, rst, st, vt,
                                kt, rs, err, pt, wv, D);
           if (++u >= u1) break;
         }
@@ -4579,10 +4611,15 @@ static int launch_rpa(const rpa_shape_t* shape, const rpa_options_t* opt, const 
       if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, true, false, true>), grid, block, lds, st, p);
       else hipLaunchKernelGGL((rpa_attn_kernel<KV_FP8, false, false, true>), grid, block, lds, st, p);
     } else if (mode == KV_BF16_SCALED) {
-      if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true, false, true>), grid, block, lds, st, p);
+      // (32- and 64-element rows on the full-line path: their own instantiations, Lines<DN>)
+      if (upg && p.D == 64) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true, false, true, 64>), grid, block, lds, st, p);
+      else if (upg && p.D == 32) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true, false, true, 32>), grid, block, lds, st, p);
+      else if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, true, false, true>), grid, block, lds, st, p);
       else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16_SCALED, false, false, true>), grid, block, lds, st, p);
     } else {
-      if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true, false, true>), grid, block, lds, st, p);
+      if (upg && p.D == 64) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true, false, true, 64>), grid, block, lds, st, p);
+      else if (upg && p.D == 32) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true, false, true, 32>), grid, block, lds, st, p);
+      else if (upg) hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, true, false, true>), grid, block, lds, st, p);
       else hipLaunchKernelGGL((rpa_attn_kernel<KV_BF16, false, false, true>), grid, block, lds, st, p);
     }
   } else if (mode == KV_FP8) {
