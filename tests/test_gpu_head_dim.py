@@ -57,13 +57,22 @@ def test_c2_shaped_fp8_decode(cuda, head_dim):
     _check(_c2_shaped(head_dim, kv_dtype="fp8", seed=9))
 
 
-@pytest.mark.parametrize("head_dim,page", [(64, 64), (64, 16), (32, 16), (96, 24), (256, 64), (256, 16)])
+@pytest.mark.parametrize("head_dim,page", [(64, 64), (64, 16), (32, 16), (32, 64), (96, 24), (256, 64), (256, 16)])
 def test_mixed_batch_prefill_rows(cuda, head_dim, page):
     # prefill rows run as causal stream-K row blocks at these head dims; page sizes that are not a
     # multiple of 32 take the operand-layout path
     _say(f"mixed batch, head_dim {head_dim}, page {page}")
     _check(make_custom(kv_lens=[700, 45, 1030, 9, 2100], q_lens=[1, 45, 130, 1, 300], num_q_heads=16,
                        num_kv_heads=4, head_dim=head_dim, page_size=page, seed=11 + head_dim + page))
+
+
+@pytest.mark.parametrize("head_dim", [32, 64])
+def test_scaled_pool_narrow_rows(cuda, head_dim):
+    # scalar K/V scales (the scaled-bf16 mode) on whole-page units: the 32/64-element row loads
+    _say(f"head_dim {head_dim}: k_scale 0.8, v_scale 1.3, page 64, prefill rows")
+    case = make_custom(kv_lens=[2100, 70, 900, 4096], q_lens=[1, 40, 1, 1], num_q_heads=16, num_kv_heads=4,
+                       head_dim=head_dim, page_size=64, seed=23 + head_dim)
+    _check(case, k_scale=0.8, v_scale=1.3)
 
 
 @pytest.mark.parametrize("head_dim", [64, 256])
